@@ -1,0 +1,197 @@
+/*
+ * mlxr.h — C ABI of libmlxr, the MI355X (gfx950) token loop.
+ *
+ * The reference (BackendStack21/mlx-runner) has no FFI layer: its engine boundary is the Swift
+ * `Transformer` class (Sources/MLXEngine/Transformer.swift:642-1303), used by `InferenceEngine`
+ * (Engine.swift:318-345, 549-813). Each model entry point below replaces one member of that
+ * class (cited per function); a Swift shim binding these symbols is shown in INTEGRATION.md.
+ *
+ * Conventions: every function returns 0 (MLXR_OK) or a negative MLXR_E_* code; the message of the
+ * last failure on the calling thread is mlxr_last_error(). Not thread-safe per model (the
+ * reference serialises every call on one queue, Engine.swift:241). Token arrays belong to the
+ * caller and are copied before the call returns. Pointers returned by the model stay valid until
+ * the next call on it.
+ *
+ * The kernel-level entry points (mlxr_k_*) take DEVICE pointers (mlxr_dev_alloc) and run on the
+ * library's stream; they mirror the reference's kernels by host name and exist for parity tests
+ * and micro-benchmarks.
+ */
+#ifndef MLXR_H
+#define MLXR_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* EngineError cases (GPU.swift:4-33) as status codes. */
+enum {
+    MLXR_OK = 0,
+    MLXR_E_NO_DEVICE = -1,       /* noMetalDevice */
+    MLXR_E_INVALID_FILE = -2,    /* invalidFile */
+    MLXR_E_MISSING_TENSOR = -3,  /* missingTensor */
+    MLXR_E_UNSUPPORTED = -4,     /* unsupported */
+    MLXR_E_CONTEXT_FULL = -5,    /* contextFull */
+    MLXR_E_OUT_OF_MEMORY = -6,   /* outOfMemory */
+    MLXR_E_CANCELLED = -7,       /* cancelled */
+    MLXR_E_INVALID_OUTPUT = -8,  /* invalidOutput */
+    MLXR_E_GPU = -9,             /* gpuFailure */
+    MLXR_E_INVALID_ARG = -10     /* caller error (bad pointer / size) */
+};
+
+typedef struct mlxr_model mlxr_model;
+
+/* SparseAttention (SparseAttention.swift:29-54): budget of the sparse decode attention. */
+typedef struct {
+    int32_t top_k;        /* long-range keys kept per step (whole blocks of 4) */
+    int32_t window;       /* most recent keys always attended */
+    int32_t sink;         /* first keys always attended */
+    int32_t min_context;  /* sparse from this context length (position + 1); <= 0: 2*(sink+top_k+window) */
+    int32_t per_head;     /* 1: one selection per KV head (default); 0: one shared selection */
+} mlxr_sparse_cfg;
+
+/* SampleParams (GPU.swift:56-66), byte-compatible field order. V and pos are filled by the model. */
+typedef struct {
+    int32_t V, pos, window, top_k;
+    float penalty, temperature, top_p, min_p;
+} mlxr_sample_params;
+
+/* A committed decode step (Transformer.DecodeStep, Transformer.swift:1267-1272). */
+typedef struct {
+    int64_t id;        /* internal slot */
+    int32_t offset;    /* position of the token the step processed; its token lands at offset + 1 */
+} mlxr_step;
+
+/* ---------------------------------------------------------------- model lifecycle */
+/* Transformer.init(directory:contextLength:sparse:sieve:) (Transformer.swift:854-1109).
+ * sparse == NULL loads without the sparse index (dense decode). */
+int mlxr_model_open(const char* dir, int context_len, const mlxr_sparse_cfg* sparse, mlxr_model** out);
+void mlxr_model_close(mlxr_model* m);
+
+/* Info getters (Transformer.swift:792-800, 875; Engine.swift:852-873 memoryNeed). */
+int mlxr_vocab_size(const mlxr_model* m);
+int mlxr_max_seq(const mlxr_model* m);
+int mlxr_hidden_size(const mlxr_model* m);
+int mlxr_num_layers(const mlxr_model* m);
+int64_t mlxr_weight_bytes(const mlxr_model* m);
+int64_t mlxr_device_bytes(const mlxr_model* m);
+const char* mlxr_quant_description(const mlxr_model* m);   /* e.g. "q4g64" (Linear.description) */
+int mlxr_sparse_available(const mlxr_model* m);            /* Transformer.sparseAvailable (:765) */
+int mlxr_written_high(const mlxr_model* m);                /* Transformer.writtenHigh (:665) */
+
+/* ---------------------------------------------------------------- the step API */
+/* forward(_:offset:allLogits:dense:) (Transformer.swift:1117-1136): runs tokens at
+ * offset..offset+n-1 in chunks of 512; *logits_out = last row's logits (V floats) or, with
+ * all_logits (n <= 8), [n][V]. Owned by the model, valid until the next call. */
+int mlxr_forward(mlxr_model* m, const int32_t* tokens, int n, int offset, int all_logits, int dense,
+                 const float** logits_out);
+/* prefill(_:offset:sample:) (Transformer.swift:1224-1249): token selected on the GPU from the last
+ * row, stored at position offset + n. */
+int mlxr_prefill(mlxr_model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp,
+                 int32_t* token_out);
+/* beginDecodeStep(offset:sample:) (Transformer.swift:1255-1264): commits the step for the token at
+ * position offset (written by the previous step's sampler or by prefill) without waiting. Steps
+ * must be begun and finished in position order, at most two in flight. */
+int mlxr_begin_decode(mlxr_model* m, int offset, const mlxr_sample_params* sp, mlxr_step* out);
+/* finish(_:) (Transformer.swift:1298-1303): waits and returns the token at offset + 1. */
+int mlxr_finish(mlxr_model* m, const mlxr_step* step, int32_t* token_out);
+/* reusablePrefix(_:previousLength:) (Transformer.swift:1193-1209). */
+int mlxr_reusable_prefix(mlxr_model* m, int common, int previous_length);
+/* resetWriteTracking() (Transformer.swift:1213). */
+void mlxr_reset_write_tracking(mlxr_model* m);
+/* seedSampler(_:) (Transformer.swift:1216-1219): seed 0 -> 0x9E3779B97F4A7C15. */
+int mlxr_seed_sampler(mlxr_model* m, uint64_t seed);
+/* `sparse` property (Transformer.swift:813): NULL turns sparse decode off. Takes effect only for
+ * a model opened with sparse attention. */
+int mlxr_set_sparse(mlxr_model* m, const mlxr_sparse_cfg* cfg);
+/* lastGPUTime (Transformer.swift:788): seconds of the last completed step. */
+double mlxr_last_gpu_time(const mlxr_model* m);
+/* Host copies of one layer's KV cache, positions [0, rows): k/v as fp32 [nKV][rows][D]. */
+int mlxr_read_kv(mlxr_model* m, int layer, int rows, float* k_out, float* v_out);
+/* Decode steps with the whole step captured as a hipGraph (1, default) or launched kernel by kernel (0). */
+int mlxr_set_graphs(mlxr_model* m, int enabled);
+
+/* ---------------------------------------------------------------- synthetic models */
+/* Writes an MLX-format model directory (config.json + model.safetensors) whose fp32 weights are
+ * drawn N(0, std) from a seeded generator and affine-quantized (bits, group_size) with bf16
+ * scale/bias; norm weights are 1. `config_json` is a Hugging Face config.json text plus
+ * "quantization": {"bits", "group_size"}. Deterministic in (config, seed). */
+int mlxr_synth_write(const char* config_json, uint64_t seed, float std, const char* dir);
+/* Quantizes one row of fp32 weights exactly as mlxr_synth_write does (MLX affine: per group
+ * scale = (max-min)/(2^bits-1), bias = min, both rounded to bf16; codes packed little-endian). */
+int mlxr_quantize_row(const float* w, int K, int bits, int group_size, uint8_t* codes, uint16_t* scales_bf16,
+                      uint16_t* biases_bf16);
+
+/* ---------------------------------------------------------------- device helpers */
+int mlxr_device_count(void);
+const char* mlxr_device_name(void);
+int mlxr_dev_alloc(void** ptr, size_t bytes);
+int mlxr_dev_free(void* ptr);
+int mlxr_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int mlxr_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int mlxr_memset(void* dst, int value, size_t bytes);
+int mlxr_synchronize(void);
+const char* mlxr_last_error(void);
+/* Timing of kernel-level calls: events recorded on the library stream (milliseconds). */
+int mlxr_timer_start(void);
+int mlxr_timer_stop(float* ms);
+
+/* ---------------------------------------------------------------- kernels (device pointers) */
+/* One quantized matrix: codes [O][K*bits/8], scales/biases [O][K/gs] (bf16: st 0, f16: st 1),
+ * optional per-row bias [O] of the scales' dtype. */
+typedef struct {
+    const void* w; const void* scales; const void* biases; const void* bias;
+    int32_t O;
+} mlxr_qmat;
+
+/* Fused decode matvec over up to three matrices [A|B|C] sharing K and quantization
+ * (`qmv`, Kernels.swift:204-318). norm_w (fp32 [K], optional): x is first RMS-normalised and
+ * scaled (the residual stream's norm, add_rms_norm Kernels.swift:1141-1175, fused).
+ * epi: 0 store, 1 accumulate (y += Wx), 2 gated: parts A, B -> y[o] = silu(A x)[o] * (B x)[o]
+ * (`qmv` MODE / silu_mul Kernels.swift:2004-2013). */
+int mlxr_k_qmv(const mlxr_qmat* parts, int nparts, int K, int bits, int gs, int st, const float* x,
+               const float* norm_w, float eps, float* y, int epi);
+/* Small batch, T in 1..8 (`qmm` / `qmvx4`, Kernels.swift:60-113, 518-622). */
+int mlxr_k_qmm(const mlxr_qmat* parts, int nparts, int K, int bits, int gs, int st, int T, const float* x,
+               int x_stride, float* y, int y_stride);
+/* Prefill GEMM on bf16 MFMA (`qgemm`, Kernels.swift:785-851), any T >= 1. */
+int mlxr_k_qgemm(const mlxr_qmat* mat, int K, int bits, int gs, int st, int T, const float* x, int x_stride,
+                 float* y, int y_stride);
+/* Quantized embedding rows (`qembed`, Kernels.swift:1002-1023): ids device int32 [T]. */
+int mlxr_k_qembed(const mlxr_qmat* mat, int K, int bits, int gs, int st, const int32_t* ids, int T, float* out);
+/* RMSNorm rows (`rms_norm`, Kernels.swift:1037-1070), fp32 weights; add_rms_norm with r != NULL. */
+int mlxr_k_rms_norm(float* x_or_h, const float* r, float* y, const float* w, int dim, int rows, float eps);
+/* `qkv_post` (Kernels.swift:1081-1138): per-head q/k RMSNorm (qn/kn fp32 [D] or NULL), RoPE
+ * (half-split or traditional), K/V appended to the bf16 cache [nKV][max_seq][D] at positions
+ * offset..offset+T-1. */
+int mlxr_k_qkv_post(float* qkv, int row_stride, const float* inv_freq, void* kcache, void* vcache, int max_seq,
+                    const float* qn, const float* kn, int D, int nH, int nKV, int rot_dim, int traditional,
+                    int offset, int T, float eps);
+/* Decode attention (`attention_split` + `attention_combine`, Kernels.swift:1317-1374) for T query
+ * rows at positions offset+t over the bf16 cache [nKV][max_seq][D]; lists (device int32, per KV
+ * head list_stride apart, or NULL) restrict the keys to `count` listed positions
+ * (`attention_sparse`, Kernels.swift:1716-1756). */
+int mlxr_k_attention(const float* q, int q_stride, const void* kcache, const void* vcache, int max_seq, int D,
+                     int nH, int nKV, int offset, int T, float scale, float* out, int out_stride,
+                     const int32_t* lists, int count, int list_stride, int nsplit);
+/* Causal prefill attention (`flash_prefill`, Kernels.swift:1839-2000). */
+int mlxr_k_flash_prefill(const float* q, int q_stride, const void* kcache, const void* vcache, int max_seq, int D,
+                         int nH, int nKV, int offset, int T, float scale, float* out, int out_stride);
+/* `sparse_index` (Kernels.swift:1545-1555): blocks completed by positions offset..offset+T-1. */
+int mlxr_k_sparse_index(const void* kcache, int max_seq, int nKV, int D, int offset, int T, void* idx);
+/* `sparse_score` (Kernels.swift:1565-1612): rows = nKV (per head) or 1 (shared). */
+int mlxr_k_sparse_score(const float* q, const void* idx, int nH, int nKV, int D, int b0, int nb, int rows,
+                        float* scores);
+/* `sparse_select` (Kernels.swift:1628-1710): rows lists of sink_end + p*4 + (L - win_start). */
+int mlxr_k_sparse_select(const float* scores, int rows, int b0, int nb, int p, int sink_end, int win_start, int L,
+                         int32_t* lists, int list_stride);
+/* `sample_blocks` + `sample_token` (Kernels.swift:2362-2619): logits device fp32 [V] (penalised in
+ * place), hist device int32 (reads [pos-window+1, pos], writes [pos+1]), status int32 [pos+1],
+ * rng device u64[2]. */
+int mlxr_k_sample(float* logits, int V, int32_t* hist, int32_t* status, uint64_t* rng, int pos,
+                  const mlxr_sample_params* sp);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

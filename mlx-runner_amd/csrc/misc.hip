@@ -1,0 +1,347 @@
+// Embedding lookup, RMSNorm, fused q/k-norm + RoPE + KV append, SiLU gate, and token selection.
+#include "kernels.h"
+
+namespace mlxr {
+
+// ---- embedding (Kernels.swift:1002-1023, `qembed`): one thread per 8 values of a row ----
+template <int BITS, int ST>
+__global__ void qembed_kernel(QMat m, int K, int gs, const int* hist, const int* dpos, int T, float* out) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+    if (c >= K / 8 || t >= T) return;
+    const int row = hist[*dpos + t];
+    const int64_t rowBytes = (int64_t)K * BITS / 8;
+    const uint8_t* p = m.w + row * rowBytes + (int64_t)c * BITS;
+    uint64_t v = 0;
+#pragma unroll
+    for (int i = 0; i < BITS; i++) v |= (uint64_t)p[i] << (8 * i);
+    const int g = (c * 8) / gs, gpr = K / gs;
+    const float s = ld_scale<ST>(m.s + (int64_t)row * gpr + g), b = ld_scale<ST>(m.b + (int64_t)row * gpr + g);
+    float* o = out + (int64_t)t * K + c * 8;
+    constexpr uint64_t M = (1ull << BITS) - 1ull;
+#pragma unroll
+    for (int j = 0; j < 8; j++) o[j] = (float)((v >> (j * BITS)) & M) * s + b;
+}
+
+hipError_t launch_qembed(const QMat& m, int K, int bits, int gs, int st, const int* hist, const int* dpos, int T,
+                         float* out, hipStream_t s) {
+    const int n = K / 8, bs = n < 256 ? n : 256;
+    dim3 grid((n + bs - 1) / bs, T);
+#define EMB(B) case B: if (st == 0) hipLaunchKernelGGL((qembed_kernel<B, 0>), grid, dim3(bs), 0, s, m, K, gs, hist, dpos, T, out); \
+                       else hipLaunchKernelGGL((qembed_kernel<B, 1>), grid, dim3(bs), 0, s, m, K, gs, hist, dpos, T, out); break;
+    switch (bits) { EMB(2) EMB(3) EMB(4) EMB(5) EMB(6) EMB(8) default: return hipErrorInvalidValue; }
+#undef EMB
+    return hipGetLastError();
+}
+
+// ---- RMSNorm (Kernels.swift:1037-1070, 1141-1175) ----
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += red[i];
+    return t;
+}
+
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, float* y, const float* w, int dim, int row_stride,
+                                                       float eps, int add, float* h, const float* r) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    float ss = 0.0f;
+    if (add) {
+        float* hr = h + (int64_t)row * row_stride;
+        const float* rr = r + (int64_t)row * row_stride;
+        for (int i = threadIdx.x * 4; i < dim; i += 1024) {
+            float4 v = *reinterpret_cast<float4*>(hr + i);
+            const float4 u = *reinterpret_cast<const float4*>(rr + i);
+            v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+            *reinterpret_cast<float4*>(hr + i) = v;
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        x = h;
+    } else {
+        const float* xr = x + (int64_t)row * row_stride;
+        for (int i = threadIdx.x * 4; i < dim; i += 1024) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + i);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    }
+    ss = block_sum_256(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    const float* xr = x + (int64_t)row * row_stride;
+    float* yr = y + (int64_t)row * row_stride;
+    for (int i = threadIdx.x * 4; i < dim; i += 1024) {
+        const float4 v = *reinterpret_cast<const float4*>(xr + i);
+        const float4 ww = *reinterpret_cast<const float4*>(w + i);
+        float4 o; o.x = v.x * inv * ww.x; o.y = v.y * inv * ww.y; o.z = v.z * inv * ww.z; o.w = v.w * inv * ww.w;
+        *reinterpret_cast<float4*>(yr + i) = o;
+    }
+}
+
+hipError_t launch_rms_norm(const float* x, float* y, const float* w, int dim, int rows, int row_stride, float eps,
+                           hipStream_t s) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, s, x, y, w, dim, row_stride, eps, 0, (float*)nullptr,
+                       (const float*)nullptr);
+    return hipGetLastError();
+}
+hipError_t launch_add_rms_norm(float* h, const float* r, float* y, const float* w, int dim, int rows, float eps,
+                               hipStream_t s) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, s, (const float*)h, y, w, dim, dim, eps, 1, h, r);
+    return hipGetLastError();
+}
+
+// ---- fused q/k norm + RoPE + KV append (Kernels.swift:1081-1138, `qkv_post`) ----
+// One workgroup of D threads per (head, token); heads [0, nH) are queries, then nKV keys, nKV values.
+__global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
+    __shared__ float buf[256];
+    __shared__ float red[4];
+    const int h = blockIdx.x, t = blockIdx.y, i = threadIdx.x, D = a.D;
+    float* base = a.qkv + (int64_t)t * a.row_stride + (int64_t)h * D;
+    const int pos = *a.dpos + a.pos_add + t;
+    float v = base[i];
+    if (h >= a.nH + a.nKV) {   // value head: straight to the cache
+        const int kvh = h - a.nH - a.nKV;
+        a.vc[kv_row(a.pt, a.nKV, kvh, pos) * D + i] = f32_to_bf16(v);
+        return;
+    }
+    const bool isQ = h < a.nH;
+    if (a.qn) {
+        float ss = wave_sum(v * v);
+        if ((i & 63) == 0) red[i >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int s = 0; s < D / 64; s++) tot += red[s];
+        v = v * (1.0f / sqrtf(tot / (float)D + a.eps)) * (isQ ? a.qn[i] : a.kn[i]);
+    }
+    buf[i] = v;
+    __syncthreads();
+    float out = v;
+    if (i < a.rot_dim) {
+        const int half = a.rot_dim / 2;
+        int fi, partner; bool first;
+        if (a.traditional) { fi = i / 2; partner = i ^ 1; first = (i & 1) == 0; }
+        else { fi = i % half; first = i < half; partner = first ? i + half : i - half; }
+        const float ang = (float)pos * a.inv_freq[fi];
+        const float c = cosf(ang), sn = sinf(ang);
+        out = first ? v * c - buf[partner] * sn : v * c + buf[partner] * sn;
+    }
+    if (isQ) base[i] = out;
+    else a.kc[kv_row(a.pt, a.nKV, h - a.nH, pos) * D + i] = f32_to_bf16(out);
+}
+
+hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(qkv_post_kernel, dim3(a.nH + 2 * a.nKV, a.T), dim3(a.D), 0, s, a);
+    return hipGetLastError();
+}
+
+// ---- SiLU gate (Kernels.swift:2004-2013): out[t][i] = silu(gu[t][i]) * gu[t][I + i] ----
+__global__ void silu_mul_kernel(const float* gu, float* out, int I) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+    if (i >= I) return;
+    const float g = gu[(int64_t)t * 2 * I + i], u = gu[(int64_t)t * 2 * I + I + i];
+    out[(int64_t)t * I + i] = (g / (1.0f + expf(-g))) * u;
+}
+hipError_t launch_silu_mul(const float* gu, float* out, int I, int T, hipStream_t s) {
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((I + 255) / 256, T), dim3(256), 0, s, gu, out, I);
+    return hipGetLastError();
+}
+
+// ---- token selection (Kernels.swift:2362-2619) ----
+// Block maxima: one wave per block of 256 logits (4 contiguous per lane); lowest index of the max.
+constexpr int SMP_BLK = 256;
+__device__ __forceinline__ void smp_block(const float* logits, int V, int b, int lane, float& m, int& idx) {
+    const int i0 = b * SMP_BLK + lane * 4;
+    float best = -INFINITY; int bi = 0x7fffffff;
+    for (int j = 0; j < 4; j++) {
+        const int i = i0 + j;
+        if (i < V) { const float v = logits[i]; if (v > best) { best = v; bi = i; } }
+    }
+    m = wave_max(best);
+    int cand = best == m ? bi : 0x7fffffff;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) cand = min(cand, __shfl_xor(cand, o, 64));
+    idx = cand;
+}
+
+__global__ __launch_bounds__(256) void sample_blocks_kernel(const float* logits, int V, float* bmax, int* barg) {
+    const int nb = (V + SMP_BLK - 1) / SMP_BLK;
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nb) return;
+    float m; int idx;
+    smp_block(logits, V, b, threadIdx.x & 63, m, idx);
+    if ((threadIdx.x & 63) == 0) { bmax[b] = m; barg[b] = idx; }
+}
+
+// One workgroup: repetition penalty over the last `window` distinct tokens, then the greedy argmax
+// (temperature <= 0.001) or the sampled draw (top-k / min-p / top-p, xorshift64).
+constexpr int SMP_CAP = 1024;
+__device__ __forceinline__ uint32_t smp_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ void smp_emit(const SampleArgs& a, int pos, int tok, int st) {
+    a.hist[pos + 1] = tok; a.status[pos + 1] = st;
+    if (a.host_tok) { a.host_tok[(pos + 1) & a.ring_mask] = tok; a.host_status[(pos + 1) & a.ring_mask] = st; }
+    if (a.dpos_next) *a.dpos_next = pos + 1;
+}
+
+__global__ __launch_bounds__(1024) void sample_token_kernel(SampleArgs a) {
+    __shared__ float shf[16];
+    __shared__ int shi[16];
+    __shared__ uint32_t hist_cnt[256];
+    __shared__ uint32_t pick[2];
+    __shared__ uint64_t cand[SMP_CAP];
+    __shared__ float prob[SMP_CAP];
+    __shared__ int ncand;
+    __shared__ uint32_t sgt[16], seq_[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int V = a.V, pos = *a.dpos;
+    float* logits = a.logits;
+    const int nb = (V + SMP_BLK - 1) / SMP_BLK;
+    if (a.penalty != 1.0f) {
+        const int n = min(a.window, pos + 1);
+        for (int j = tid; j < n; j += blockDim.x) {
+            const int t = a.hist[pos - j];
+            bool dup = false;
+            for (int j2 = 0; j2 < j; j2++) dup = dup || (a.hist[pos - j2] == t);
+            if (!dup && t >= 0 && t < V) { const float v = logits[t]; logits[t] = v > 0.0f ? v / a.penalty : v * a.penalty; }
+        }
+        __threadfence_block();
+        __syncthreads();
+        for (int j = wave; j < n; j += nw) {
+            const int t = a.hist[pos - j];
+            bool dup = false;
+            for (int j2 = 0; j2 < j; j2++) dup = dup || (a.hist[pos - j2] == t);
+            if (dup || t < 0 || t >= V) continue;
+            float m; int idx;
+            smp_block(logits, V, t / SMP_BLK, lane, m, idx);
+            if (lane == 0) { a.bmax[t / SMP_BLK] = m; a.barg[t / SMP_BLK] = idx; }
+        }
+        __threadfence_block();
+        __syncthreads();
+    }
+    // maximum and its lowest index over the block maxima (ascending blocks, strictly greater wins)
+    float best = -INFINITY; int bi = 0x7fffffff;
+    for (int b = tid; b < nb; b += blockDim.x) { const float v = a.bmax[b]; if (v > best) { best = v; bi = a.barg[b]; } }
+    const float wm = wave_max(best);
+    int wi = best == wm ? bi : 0x7fffffff;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) wi = min(wi, __shfl_xor(wi, o, 64));
+    if (lane == 0) { shf[wave] = wm; shi[wave] = wi; }
+    __syncthreads();
+    float M = -INFINITY; int argmax = 0x7fffffff;
+    for (int w = 0; w < nw; w++) {
+        if (shf[w] > M) { M = shf[w]; argmax = shi[w]; }
+        else if (shf[w] == M && shi[w] < argmax) argmax = shi[w];
+    }
+    if (!isfinite(M)) {
+        if (tid == 0) smp_emit(a, pos, 0, 1);
+        return;
+    }
+    if (a.temperature <= 0.001f) {
+        if (tid == 0) smp_emit(a, pos, argmax, 0);
+        return;
+    }
+    // Sampled: exact top-k (k <= SMP_CAP, lowest index first among equal values) by an 8-bit radix
+    // select of the k-th largest key over all V logits, then a stable gather and a bitonic sort.
+    const int k = min(a.top_k > 0 ? min(a.top_k, V) : min(512, V), SMP_CAP);
+    uint32_t prefix = 0, mask = 0, want = (uint32_t)k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int i = tid; i < 256; i += blockDim.x) hist_cnt[i] = 0;
+        __syncthreads();
+        for (int n = tid; n < V; n += blockDim.x) {
+            const uint32_t key = smp_key(logits[n]);
+            if ((key & mask) == prefix) atomicAdd(&hist_cnt[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t acc = 0;
+            for (int bin = 255; bin >= 0; bin--) {
+                if (acc + hist_cnt[bin] >= want) { pick[0] = (uint32_t)bin; pick[1] = want - acc; break; }
+                acc += hist_cnt[bin];
+            }
+        }
+        __syncthreads();
+        prefix |= pick[0] << shift; mask |= 255u << shift; want = pick[1];
+        __syncthreads();
+    }
+    // gather: keys > prefix all kept; of keys == prefix the first `want` by index.
+    const int chunk = (V + blockDim.x - 1) / blockDim.x;
+    const int n0 = min(V, tid * chunk), n1 = min(V, n0 + chunk);
+    uint32_t gt = 0, eq = 0;
+    for (int n = n0; n < n1; n++) { const uint32_t key = smp_key(logits[n]); gt += key > prefix; eq += key == prefix; }
+    // exclusive scans over threads (wave scan then across waves)
+    uint32_t gx = gt, ex = eq;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t g2 = __shfl_up(gx, o, 64), e2 = __shfl_up(ex, o, 64);
+        if (lane >= o) { gx += g2; ex += e2; }
+    }
+    if (lane == 63) { sgt[wave] = gx; seq_[wave] = ex; }
+    __syncthreads();
+    uint32_t gbase = 0, ebase = 0;
+    for (int w = 0; w < wave; w++) { gbase += sgt[w]; ebase += seq_[w]; }
+    uint32_t gtot = 0; for (int w = 0; w < nw; w++) gtot += sgt[w];
+    uint32_t gb = gbase + gx - gt, eb = ebase + ex - eq;
+    for (int n = n0; n < n1; n++) {
+        const float v = logits[n];
+        const uint32_t key = smp_key(v);
+        int slot = -1;
+        if (key > prefix) slot = (int)(gb++);
+        else if (key == prefix) { if (eb < want) slot = (int)(gtot + eb); eb++; }
+        if (slot >= 0 && slot < SMP_CAP) cand[slot] = ((uint64_t)key << 32) | (uint64_t)(~(uint32_t)n);
+    }
+    if (tid == 0) ncand = k;
+    for (int i = k + tid; i < SMP_CAP; i += blockDim.x) cand[i] = 0;
+    __syncthreads();
+    // bitonic sort descending (value, then lowest index): keys are distinct
+    for (int size = 2; size <= SMP_CAP; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int q = tid; q < SMP_CAP / 2; q += blockDim.x) {
+                const int i = (q / stride) * (stride * 2) + (q % stride), j = i + stride;
+                const bool desc = (i & size) == 0;
+                const uint64_t x = cand[i], y = cand[j];
+                if ((x < y) == desc) { cand[i] = y; cand[j] = x; }
+            }
+            __syncthreads();
+        }
+    }
+    const int n = ncand;
+    const float invT = 1.0f / a.temperature;
+    for (int i = tid; i < n; i += blockDim.x) {
+        const uint32_t key = (uint32_t)(cand[i] >> 32);
+        const uint32_t u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+        prob[i] = expf((__uint_as_float(u) - M) * invT);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float total = 0.0f;
+        for (int i = 0; i < n; i++) total += prob[i];
+        int cut = n;
+        if (a.min_p > 0.0f) { const float th = a.min_p * prob[0]; for (int i = 0; i < n; i++) if (prob[i] < th) { cut = i; break; } }
+        if (a.top_p < 1.0f) { float acc = 0.0f; for (int i = 0; i < cut; i++) { acc += prob[i] / total; if (acc >= a.top_p) { cut = i + 1; break; } } }
+        cut = max(1, cut);
+        float tot = 0.0f;
+        for (int i = 0; i < cut; i++) tot += prob[i];
+        uint64_t st = a.rng[0];
+        st ^= st << 13; st ^= st >> 7; st ^= st << 17;
+        a.rng[0] = st;
+        float r = (float)(st >> 40) * (1.0f / 16777216.0f);
+        int chosen = (int)(~(uint32_t)cand[cut - 1]);
+        for (int i = 0; i < cut; i++) { r -= prob[i] / tot; if (r <= 0.0f) { chosen = (int)(~(uint32_t)cand[i]); break; } }
+        if (a.diag) { a.diag[0] = n; a.diag[1] = 1; }
+        smp_emit(a, pos, chosen, 0);
+    }
+}
+
+hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
+    const int nb = (a.V + SMP_BLK - 1) / SMP_BLK;
+    hipLaunchKernelGGL(sample_blocks_kernel, dim3((nb + 3) / 4), dim3(256), 0, s, (const float*)a.logits, a.V, a.bmax, a.barg);
+    hipLaunchKernelGGL(sample_token_kernel, dim3(1), dim3(1024), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace mlxr

@@ -1,0 +1,332 @@
+// Decode matvec (T == 1) and small-batch matmul (T = 2..8) over MLX affine-quantized weights.
+//
+// Semantics follow the reference's fused decode kernel (Kernels.swift:204-318, `qmv`) and its
+// generic `qmm` (Kernels.swift:60-113): y[o] = sum over groups of s * (sum_j q_j x_j) + b * (sum_j x_j),
+// fp32 accumulation, rows of up to three matrices [A | B | C] concatenated, optional per-row bias.
+//
+// MI355X layout: a 256-thread workgroup (4 waves of 64) owns ROWS rows per wave. A lane consumes one
+// 32-code chunk of a row per step (4*BITS bytes: one 16-byte load at 4 bits), so a wave streams a
+// contiguous 64*4*BITS-byte span of the row per load instruction (fully coalesced), and every row of
+// the wave reuses the lane's 32 x values. Codes are extracted without shifts where possible: at
+// 4 bits the dword is split into low/high nibbles of its four bytes and each byte converted with the
+// byte-to-float conversion. The workgroup can normalise x itself (RMSNorm of the residual stream
+// times the norm weight, written to LDS) so the norm needs no kernel of its own.
+#include "kernels.h"
+
+namespace mlxr {
+
+constexpr int QMV_WAVES = 4;
+constexpr int QMV_ROWS = 4;   // rows per wave
+
+struct QmvDev {
+    const uint8_t* w[3]; const uint16_t* s[3]; const uint16_t* b[3]; const uint16_t* bias[3];
+    int o1, o2;               // rows of A, B (C gets the rest)
+    int K, gs, O, epi, hasBias;
+    const float* x; const float* norm_w; float eps; float* y;
+};
+
+// 32 codes of one chunk (BITS dwords) dotted with 32 x values.
+template <int BITS>
+__device__ __forceinline__ float chunk_dot(const uint32_t* w, const float* x) {
+    float d = 0.0f;
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+            const float* xp = x + 8 * i;
+            d = fmaf((float)(lo & 0xFFu), xp[0], d);
+            d = fmaf((float)(hi & 0xFFu), xp[1], d);
+            d = fmaf((float)((lo >> 8) & 0xFFu), xp[2], d);
+            d = fmaf((float)((hi >> 8) & 0xFFu), xp[3], d);
+            d = fmaf((float)((lo >> 16) & 0xFFu), xp[4], d);
+            d = fmaf((float)((hi >> 16) & 0xFFu), xp[5], d);
+            d = fmaf((float)(lo >> 24), xp[6], d);
+            d = fmaf((float)(hi >> 24), xp[7], d);
+        }
+    } else if constexpr (BITS == 8) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float* xp = x + 4 * i;
+            d = fmaf((float)(w[i] & 0xFFu), xp[0], d);
+            d = fmaf((float)((w[i] >> 8) & 0xFFu), xp[1], d);
+            d = fmaf((float)((w[i] >> 16) & 0xFFu), xp[2], d);
+            d = fmaf((float)(w[i] >> 24), xp[3], d);
+        }
+    } else {
+        constexpr uint32_t M = (1u << BITS) - 1u;
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const int bit = j * BITS, wi = bit >> 5, off = bit & 31;
+            uint32_t q;
+            if (off + BITS <= 32) q = (w[wi] >> off) & M;
+            else q = ((w[wi] >> off) | (w[wi + 1] << (32 - off))) & M;
+            d = fmaf((float)q, x[j], d);
+        }
+    }
+    return d;
+}
+
+template <int BITS>
+__device__ __forceinline__ void load_chunk(const uint8_t* p, uint32_t* w) {
+    if constexpr (BITS == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (BITS == 8) {
+        const uint4 a = reinterpret_cast<const uint4*>(p)[0], b = reinterpret_cast<const uint4*>(p)[1];
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    } else {
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+        for (int i = 0; i < BITS; i++) w[i] = q[i];
+    }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+// XNORM: x is normalised into LDS by the workgroup (K floats).
+template <int BITS, int ST, bool XNORM>
+__global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
+    extern __shared__ float xs_lds[];
+    __shared__ float red[QMV_WAVES];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = a.K;
+    const float* xsrc = a.x;
+    if constexpr (XNORM) {
+        float ss = 0.0f;
+        for (int i = threadIdx.x * 4; i < K; i += 256 * 4) {
+            const float4 v = *reinterpret_cast<const float4*>(a.x + i);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        const float tot = red[0] + red[1] + red[2] + red[3];
+        const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
+        for (int i = threadIdx.x * 4; i < K; i += 256 * 4) {
+            const float4 v = *reinterpret_cast<const float4*>(a.x + i);
+            const float4 w = *reinterpret_cast<const float4*>(a.norm_w + i);
+            float4 o; o.x = v.x * inv * w.x; o.y = v.y * inv * w.y; o.z = v.z * inv * w.z; o.w = v.w * inv * w.w;
+            *reinterpret_cast<float4*>(xs_lds + i) = o;
+        }
+        __syncthreads();
+        xsrc = xs_lds;
+    }
+    const bool gated = a.epi == EPI_GATED;
+    const int rows_per_wave = QMV_ROWS;
+    const int slot0 = (blockIdx.x * QMV_WAVES + wave) * (gated ? rows_per_wave / 2 : rows_per_wave);
+    if (slot0 >= a.O) return;
+    const int64_t rowBytes = (int64_t)K * BITS / 8;
+    const int gpr = K / a.gs;
+    const uint8_t* wp[QMV_ROWS]; const uint16_t* sp[QMV_ROWS]; const uint16_t* bp[QMV_ROWS];
+    bool valid[QMV_ROWS];
+    int outIdx[QMV_ROWS];
+#pragma unroll
+    for (int r = 0; r < QMV_ROWS; r++) {
+        int part, row;
+        if (gated) {
+            const int o = slot0 + (r % (QMV_ROWS / 2));
+            part = r < QMV_ROWS / 2 ? 0 : 1; row = o; valid[r] = o < a.O; outIdx[r] = o;
+        } else {
+            const int gr = slot0 + r;
+            valid[r] = gr < a.O; outIdx[r] = gr;
+            if (gr < a.o1) { part = 0; row = gr; }
+            else if (gr < a.o1 + a.o2) { part = 1; row = gr - a.o1; }
+            else { part = 2; row = gr - a.o1 - a.o2; }
+        }
+        if (!valid[r]) { part = 0; row = 0; }
+        wp[r] = a.w[part] + row * rowBytes;
+        sp[r] = a.s[part] + (int64_t)row * gpr;
+        bp[r] = a.b[part] + (int64_t)row * gpr;
+        // bias pointer reuse: keep per-row bias in outIdx decode below
+        outIdx[r] = valid[r] ? outIdx[r] : -1;
+        (void)part;
+    }
+    float acc[QMV_ROWS];
+#pragma unroll
+    for (int r = 0; r < QMV_ROWS; r++) acc[r] = 0.0f;
+    const int nchunks = K >> 5;
+    for (int c = lane; c < nchunks; c += 64) {
+        const int k0 = c << 5;
+        uint32_t w[QMV_ROWS][BITS];
+#pragma unroll
+        for (int r = 0; r < QMV_ROWS; r++) load_chunk<BITS>(wp[r] + (int64_t)c * (4 * BITS), w[r]);
+        float x[32];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = *reinterpret_cast<const float4*>(xsrc + k0 + 4 * i);
+            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+        }
+        float xsum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) xsum += x[j];
+        const int g = k0 / a.gs;
+#pragma unroll
+        for (int r = 0; r < QMV_ROWS; r++) {
+            const float s = ld_scale<ST>(sp[r] + g), b = ld_scale<ST>(bp[r] + g);
+            const float d = chunk_dot<BITS>(w[r], x);
+            acc[r] += s * d + b * xsum;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < QMV_ROWS; r++) acc[r] = wave_sum(acc[r]);
+    if (lane != 0) return;
+    if (gated) {
+#pragma unroll
+        for (int r = 0; r < QMV_ROWS / 2; r++) {
+            const int o = outIdx[r];
+            if (o < 0) continue;
+            float g = acc[r], u = acc[r + QMV_ROWS / 2];
+            if (a.hasBias) { g += ld_scale<ST>(a.bias[0] + o); u += ld_scale<ST>(a.bias[1] + o); }
+            a.y[o] = silu_mul(g, u);
+        }
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < QMV_ROWS; r++) {
+        const int gr = outIdx[r];
+        if (gr < 0) continue;
+        float v = acc[r];
+        if (a.hasBias) {
+            int part, row;
+            if (gr < a.o1) { part = 0; row = gr; }
+            else if (gr < a.o1 + a.o2) { part = 1; row = gr - a.o1; }
+            else { part = 2; row = gr - a.o1 - a.o2; }
+            v += ld_scale<ST>(a.bias[part] + row);
+        }
+        if (a.epi == EPI_ADD) a.y[gr] += v; else a.y[gr] = v;
+    }
+}
+
+template <int BITS, int ST, bool XNORM>
+static hipError_t qmv_launch(const QmvDev& d, int grid, size_t lds, hipStream_t s) {
+    hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM>), dim3(grid), dim3(256), lds, s, d);
+    return hipGetLastError();
+}
+
+template <int BITS>
+static hipError_t qmv_dispatch_st(const QmvDev& d, int st, bool xn, int grid, size_t lds, hipStream_t s) {
+    if (st == 0) return xn ? qmv_launch<BITS, 0, true>(d, grid, lds, s) : qmv_launch<BITS, 0, false>(d, grid, lds, s);
+    return xn ? qmv_launch<BITS, 1, true>(d, grid, lds, s) : qmv_launch<BITS, 1, false>(d, grid, lds, s);
+}
+
+hipError_t launch_qmv(const QmvArgs& a, hipStream_t s) {
+    QmvDev d{};
+    for (int i = 0; i < 3; i++) {
+        const QMat& m = a.part[i < a.nparts ? i : a.nparts - 1];
+        d.w[i] = m.w; d.s[i] = m.s; d.b[i] = m.b; d.bias[i] = m.bias;
+    }
+    d.o1 = a.part[0].O; d.o2 = a.nparts > 1 ? a.part[1].O : 0;
+    d.K = a.K; d.gs = a.gs; d.O = a.O; d.epi = a.epi; d.hasBias = a.part[0].bias != nullptr;
+    d.x = a.x; d.norm_w = a.norm_w; d.eps = a.eps; d.y = a.y;
+    const int per_wg = QMV_WAVES * (a.epi == EPI_GATED ? QMV_ROWS / 2 : QMV_ROWS);
+    const int grid = (a.O + per_wg - 1) / per_wg;
+    const bool xn = a.norm_w != nullptr;
+    const size_t lds = xn ? (size_t)a.K * sizeof(float) : 0;
+    switch (a.bits) {
+        case 2: return qmv_dispatch_st<2>(d, a.st, xn, grid, lds, s);
+        case 3: return qmv_dispatch_st<3>(d, a.st, xn, grid, lds, s);
+        case 4: return qmv_dispatch_st<4>(d, a.st, xn, grid, lds, s);
+        case 5: return qmv_dispatch_st<5>(d, a.st, xn, grid, lds, s);
+        case 6: return qmv_dispatch_st<6>(d, a.st, xn, grid, lds, s);
+        case 8: return qmv_dispatch_st<8>(d, a.st, xn, grid, lds, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Small batch: TT tokens per wave pass (weights unpacked once, reused for every token).
+constexpr int QMM_TT = 8;
+
+struct QmmDev {
+    const uint8_t* w[3]; const uint16_t* s[3]; const uint16_t* b[3]; const uint16_t* bias[3];
+    int o1, o2, K, gs, O, T, hasBias, xs, ys;
+    const float* x; float* y;
+};
+
+template <int BITS, int ST>
+__global__ __launch_bounds__(256) void qmm_small_kernel(QmmDev a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gr0 = (blockIdx.x * QMV_WAVES + wave) * QMV_ROWS;
+    if (gr0 >= a.O) return;
+    const int K = a.K;
+    const int64_t rowBytes = (int64_t)K * BITS / 8;
+    const int gpr = K / a.gs;
+    const uint8_t* wp[QMV_ROWS]; const uint16_t* sp[QMV_ROWS]; const uint16_t* bp[QMV_ROWS]; int gr[QMV_ROWS];
+#pragma unroll
+    for (int r = 0; r < QMV_ROWS; r++) {
+        int g = gr0 + r; gr[r] = g < a.O ? g : -1; if (g >= a.O) g = gr0;
+        int part, row;
+        if (g < a.o1) { part = 0; row = g; } else if (g < a.o1 + a.o2) { part = 1; row = g - a.o1; } else { part = 2; row = g - a.o1 - a.o2; }
+        wp[r] = a.w[part] + row * rowBytes; sp[r] = a.s[part] + (int64_t)row * gpr; bp[r] = a.b[part] + (int64_t)row * gpr;
+    }
+    float acc[QMV_ROWS][QMM_TT];
+#pragma unroll
+    for (int r = 0; r < QMV_ROWS; r++)
+#pragma unroll
+        for (int t = 0; t < QMM_TT; t++) acc[r][t] = 0.0f;
+    const int nchunks = K >> 5;
+    for (int c = lane; c < nchunks; c += 64) {
+        const int k0 = c << 5;
+        const int g = k0 / a.gs;
+        uint32_t w[QMV_ROWS][BITS];
+        float sc[QMV_ROWS], bi[QMV_ROWS];
+#pragma unroll
+        for (int r = 0; r < QMV_ROWS; r++) {
+            load_chunk<BITS>(wp[r] + (int64_t)c * (4 * BITS), w[r]);
+            sc[r] = ld_scale<ST>(sp[r] + g); bi[r] = ld_scale<ST>(bp[r] + g);
+        }
+#pragma unroll
+        for (int t = 0; t < QMM_TT; t++) {
+            if (t >= a.T) break;
+            float x[32];
+            const float* xp = a.x + (int64_t)t * a.xs + k0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 v = *reinterpret_cast<const float4*>(xp + 4 * i);
+                x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+            }
+            float xsum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 32; j++) xsum += x[j];
+#pragma unroll
+            for (int r = 0; r < QMV_ROWS; r++) acc[r][t] += sc[r] * chunk_dot<BITS>(w[r], x) + bi[r] * xsum;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < QMV_ROWS; r++)
+#pragma unroll
+        for (int t = 0; t < QMM_TT; t++) {
+            if (t >= a.T) break;
+            const float v0 = wave_sum(acc[r][t]);
+            if (lane == 0 && gr[r] >= 0) {
+                float v = v0;
+                if (a.hasBias) {
+                    const int g = gr[r]; int part, row;
+                    if (g < a.o1) { part = 0; row = g; } else if (g < a.o1 + a.o2) { part = 1; row = g - a.o1; } else { part = 2; row = g - a.o1 - a.o2; }
+                    v += ld_scale<ST>(a.bias[part] + row);
+                }
+                a.y[(int64_t)t * a.ys + gr[r]] = v;
+            }
+        }
+}
+
+hipError_t launch_qmm_small(const QmmSmallArgs& a, hipStream_t s) {
+    QmmDev d{};
+    for (int i = 0; i < 3; i++) {
+        const QMat& m = a.part[i < a.nparts ? i : a.nparts - 1];
+        d.w[i] = m.w; d.s[i] = m.s; d.b[i] = m.b; d.bias[i] = m.bias;
+    }
+    d.o1 = a.part[0].O; d.o2 = a.nparts > 1 ? a.part[1].O : 0;
+    d.K = a.K; d.gs = a.gs; d.O = a.O; d.T = a.T; d.hasBias = a.part[0].bias != nullptr;
+    d.xs = a.x_stride; d.ys = a.y_stride; d.x = a.x; d.y = a.y;
+    const int grid = (a.O + QMV_WAVES * QMV_ROWS - 1) / (QMV_WAVES * QMV_ROWS);
+#define QMM_CASE(B) case B: \
+    if (a.st == 0) hipLaunchKernelGGL((qmm_small_kernel<B, 0>), dim3(grid), dim3(256), 0, s, d); \
+    else hipLaunchKernelGGL((qmm_small_kernel<B, 1>), dim3(grid), dim3(256), 0, s, d); \
+    return hipGetLastError();
+    switch (a.bits) { QMM_CASE(2) QMM_CASE(3) QMM_CASE(4) QMM_CASE(5) QMM_CASE(6) QMM_CASE(8) }
+#undef QMM_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace mlxr

@@ -1,0 +1,452 @@
+"""Kernel parity on the MI355X through libmlxr's C ABI, against the CPU oracle.
+
+Mirrors the reference's kernel tests (Tests/MLXEngineTests/KernelTests.swift,
+SparseAttentionTests.swift): same shapes, same generators, the same closeness metric
+(|a-b| / max(1, |b|)), with the north-star tolerance 1e-3 for the fp32 matvec paths.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from qfix import QuantFixture, XorShift, bf16_round, bf16_to_f32, max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3          # matvec / GEMM vs the oracle in the same declared precision (north star)
+
+
+def qmv(mlxr, fixtures, x, norm_w=None, eps=1e-6, epi=0, y0=None):
+    parts = (mlxr.QMat * len(fixtures))(*[f.device(mlxr) for f in fixtures])
+    f0 = fixtures[0]
+    O = sum(f.O for f in fixtures) if epi != 2 else f0.O
+    dx = mlxr.DeviceArray.from_numpy(np.asarray(x, np.float32))
+    dy = mlxr.DeviceArray.from_numpy(np.zeros(O, np.float32) if y0 is None else np.asarray(y0, np.float32))
+    dn = mlxr.DeviceArray.from_numpy(np.asarray(norm_w, np.float32)) if norm_w is not None else None
+    mlxr.check(mlxr.lib.mlxr_k_qmv(parts, len(fixtures), f0.K, f0.bits, f0.gs, 0 if f0.st == "bf16" else 1, dx.ptr,
+                                   dn.ptr if dn else None, eps, dy.ptr, epi))
+    mlxr.synchronize()
+    return dy.numpy()
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_qmv_all_bits_groups_dtypes(gpu, bits):
+    """quantizedMatchesReference at T = 1 (KernelTests.swift:128-146): K 512, O 40."""
+    K, O = 512, 40
+    for gs in (32, 64, 128):
+        for st in ("f16", "bf16"):
+            fx = QuantFixture(O, K, bits, gs, st=st)
+            rng = XorShift(1 * 31 + bits)
+            x = rng.floats(K)
+            got = qmv(gpu, [fx], x)
+            ref = fx.oracle(oracle).matmul_f64(x)[0]
+            assert max_rel_err(got, ref) < TOL, (bits, gs, st)
+            # the oracle itself agrees with the float64 numpy product of the dequantized matrix
+            assert max_rel_err(ref, fx.reference(x)[0]) < 1e-6
+
+
+@pytest.mark.parametrize("K", [1152, 1536, 2304, 2560, 896, 1664, 6912])
+def test_qmv_partial_passes(gpu, K):
+    """fourBitDecodeWithPartialPass (KernelTests.swift:188-199): K not a multiple of 1024."""
+    O = 24
+    for gs in (32, 64, 128):
+        if K % gs:
+            continue
+        fx = QuantFixture(O, K, 4, gs, seed=K, fast=True)
+        x = XorShift(K).floats(K)
+        assert max_rel_err(qmv(gpu, [fx], x), fx.oracle(oracle).matmul_f64(x)[0]) < TOL
+
+
+def test_fused_qkv_with_bias_matches_separate(gpu):
+    """fusedDecodeWithBiasMatchesSeparate (KernelTests.swift:214-227)."""
+    K = 256
+    parts = [QuantFixture(o, K, 4, 64, with_bias=True, seed=s) for o, s in ((64, 1), (16, 2), (16, 3))]
+    x = XorShift(99).floats(K)
+    got = qmv(gpu, parts, x)
+    ref = np.concatenate([p.oracle(oracle).matmul_f64(x)[0] for p in parts])
+    assert max_rel_err(got, ref) < TOL
+
+
+def test_qmv_normalised_input_and_epilogues(gpu):
+    """x = RMSNorm(h) * w inside the matvec; accumulate (residual) and SiLU-gated epilogues."""
+    K, O = 1024, 96
+    rng = np.random.default_rng(3)
+    h = rng.normal(0, 1, K).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    fa, fb = QuantFixture(O, K, 4, 64, seed=11, fast=True), QuantFixture(O, K, 4, 64, seed=12, fast=True)
+    xn = oracle.rms_norm(h[None], w, 1e-6)[0]
+    ref_a = fa.oracle(oracle).matmul_f64(xn)[0]
+    assert max_rel_err(qmv(gpu, [fa], h, norm_w=w), ref_a) < TOL
+    y0 = rng.normal(0, 1, O).astype(np.float32)
+    assert max_rel_err(qmv(gpu, [fa], xn, epi=1, y0=y0), y0 + ref_a) < TOL
+    ref_b = fb.oracle(oracle).matmul_f64(xn)[0]
+    gated = np.array([oracle.lib.orc_silu_mul(float(g), float(u)) for g, u in zip(ref_a, ref_b)], np.float32)
+    assert max_rel_err(qmv(gpu, [fa, fb], h, norm_w=w, epi=2), gated) < TOL
+
+
+@pytest.mark.parametrize("bits", [3, 4, 6, 8])
+def test_qmm_small_batch(gpu, bits):
+    """T = 2..8 (qmm / qmvx4, KernelTests.swift:232-252) with padded strides (NaN padding never read)."""
+    K, O = 512, 44
+    fx = QuantFixture(O, K, bits, 64 if bits != 3 else 32, seed=K + O)
+    qm = (gpu.QMat * 1)(fx.device(gpu))
+    for T in (2, 3, 4, 5, 8):
+        xs, ys = K + 4, O + 3
+        x = np.full((T, xs), np.nan, np.float32)
+        x[:, :K] = np.random.default_rng(T).uniform(-1, 1, (T, K))
+        dx = gpu.DeviceArray.from_numpy(x)
+        dy = gpu.DeviceArray.from_numpy(np.zeros((T, ys), np.float32))
+        gpu.check(gpu.lib.mlxr_k_qmm(qm, 1, K, bits, fx.gs, 0, T, dx.ptr, xs, dy.ptr, ys))
+        gpu.synchronize()
+        got = dy.numpy()[:, :O]
+        assert max_rel_err(got, fx.oracle(oracle).matmul_f64(x[:, :K])) < TOL, T
+
+
+def qgemm(mlxr, fx, x):
+    T = x.shape[0]
+    qm = (mlxr.QMat * 1)(fx.device(mlxr))
+    dx = mlxr.DeviceArray.from_numpy(x)
+    dy = mlxr.DeviceArray.from_numpy(np.zeros((T, fx.O), np.float32))
+    mlxr.check(mlxr.lib.mlxr_k_qgemm(qm, fx.K, fx.bits, fx.gs, 0 if fx.st == "bf16" else 1, T, dx.ptr, fx.K, dy.ptr, fx.O))
+    mlxr.synchronize()
+    return dy.numpy()
+
+
+@pytest.mark.parametrize("bits", [3, 4, 8])
+def test_qgemm_prefill_tiles(gpu, bits):
+    """prefillTilesMatchReference shapes (KernelTests.swift:150-164), against the oracle in the
+    GEMM's declared precision (bf16 operands, fp32/f64 accumulation)."""
+    for T, O, K in ((64, 41, 1088), (128, 41, 576), (517, 41, 576), (96, 2050, 576), (128, 2050, 576), (517, 520, 576)):
+        fx = QuantFixture(O, K, bits, 32, seed=T + O, fast=True)
+        x = np.random.default_rng(T * 7 + bits).uniform(-1, 1, (T, K)).astype(np.float32)
+        got = qgemm(gpu, fx, x)
+        assert max_rel_err(got, fx.oracle(oracle).matmul_bf16(x)) < TOL, (T, O, K)
+        # distance to the fp32-operand product (the reference's precision): rounding x and each
+        # dequantized weight to bf16 changes each product by at most 2^-8 relative, so
+        # |got - exact| <= 2^-8 * sum_k |w_k x_k| (+ fp32 accumulation slack)
+        bound = 2.0 ** -8 * (np.abs(x).astype(np.float64) @ np.abs(fx.dense()).astype(np.float64).T) + 1e-4
+        assert np.all(np.abs(got - fx.oracle(oracle).matmul_f64(x)) <= bound)
+
+
+def test_qgemm_batch_invariant(gpu):
+    """prefillTilesAgreeBitwise (KernelTests.swift:168-184): a token's output does not depend on T."""
+    O, K = 2050, 1024
+    fx = QuantFixture(O, K, 4, 64, seed=3, fast=True)
+    x = np.random.default_rng(11).uniform(-1, 1, (256, K)).astype(np.float32)
+    full = qgemm(gpu, fx, x)
+    for T in (9, 16, 33, 96):
+        assert np.array_equal(qgemm(gpu, fx, x[:T]).view(np.uint32), full[:T].view(np.uint32)), T
+
+
+def test_qembed(gpu):
+    """quantizedEmbeddingLookup (KernelTests.swift:287-296), tol 1e-5."""
+    K, V = 128, 16
+    fx = QuantFixture(V, K, 4, 64)
+    ids = np.array([3, 0, 15, 7], np.int32)
+    qm = (gpu.QMat * 1)(fx.device(gpu))
+    did = gpu.DeviceArray.from_numpy(ids)
+    out = gpu.DeviceArray.zeros((4, K), np.float32)
+    gpu.check(gpu.lib.mlxr_k_qembed(qm, K, 4, 64, 0, did.ptr, 4, out.ptr))
+    gpu.synchronize()
+    q = fx.oracle(oracle)
+    ref = np.stack([q.dequant_row(int(i)) for i in ids])
+    assert np.max(np.abs(out.numpy() - ref)) <= 1e-5
+    bad = gpu.DeviceArray.from_numpy(np.array([16], np.int32))
+    with pytest.raises(gpu.EngineError):
+        gpu.check(gpu.lib.mlxr_k_qembed(qm, K, 4, 64, 0, bad.ptr, 1, out.ptr))
+
+
+def test_rms_norm_and_add(gpu):
+    rng = np.random.default_rng(5)
+    for dim, rows in ((1024, 3), (4096, 2), (5120, 1)):
+        x = rng.normal(0, 2, (rows, dim)).astype(np.float32)
+        r = rng.normal(0, 1, (rows, dim)).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, dim).astype(np.float32)
+        dx, dr, dy, dw = (gpu.DeviceArray.from_numpy(a) for a in (x, r, np.zeros_like(x), w))
+        gpu.check(gpu.lib.mlxr_k_rms_norm(dx.ptr, None, dy.ptr, dw.ptr, dim, rows, 1e-6))
+        gpu.synchronize()
+        assert max_rel_err(dy.numpy(), oracle.rms_norm(x, w, 1e-6)) < 1e-5
+        gpu.check(gpu.lib.mlxr_k_rms_norm(dx.ptr, dr.ptr, dy.ptr, dw.ptr, dim, rows, 1e-6))
+        gpu.synchronize()
+        assert max_rel_err(dx.numpy(), x + r) < 1e-6
+        assert max_rel_err(dy.numpy(), oracle.rms_norm(x + r, w, 1e-6)) < 1e-5
+
+
+def to_paged(c, page=64):
+    """[nKV][max_seq][D] -> the library's cache layout [max_seq/64][nKV][64][D]."""
+    nKV, S, D = c.shape
+    return np.ascontiguousarray(c.reshape(nKV, S // page, page, D).transpose(1, 0, 2, 3))
+
+
+def from_paged(c, nKV, D, page=64):
+    pages = c.size // (nKV * page * D)
+    return np.ascontiguousarray(c.reshape(pages, nKV, page, D).transpose(1, 0, 2, 3).reshape(nKV, pages * page, D))
+
+
+@pytest.mark.parametrize("qk_norm,traditional", [(True, False), (False, False), (True, True)])
+def test_qkv_post(gpu, qk_norm, traditional):
+    nH, nKV, D, S, T, off = 4, 2, 128, 128, 5, 37
+    rng = np.random.default_rng(7)
+    cols = (nH + 2 * nKV) * D
+    qkv = rng.normal(0, 1, (T, cols)).astype(np.float32)
+    invf = oracle.inv_freq(1e6, D)
+    qn = rng.uniform(0.5, 1.5, D).astype(np.float32) if qk_norm else None
+    kn = rng.uniform(0.5, 1.5, D).astype(np.float32) if qk_norm else None
+    dq = gpu.DeviceArray.from_numpy(qkv)
+    dk = gpu.DeviceArray.zeros(S * nKV * D, np.uint16)
+    dv = gpu.DeviceArray.zeros(S * nKV * D, np.uint16)
+    di = gpu.DeviceArray.from_numpy(invf)
+    dqn = gpu.DeviceArray.from_numpy(qn) if qk_norm else None
+    dkn = gpu.DeviceArray.from_numpy(kn) if qk_norm else None
+    gpu.check(gpu.lib.mlxr_k_qkv_post(dq.ptr, cols, di.ptr, dk.ptr, dv.ptr, S, dqn.ptr if dqn else None, dkn.ptr if dkn else None,
+                                      D, nH, nKV, D, int(traditional), off, T, 1e-6))
+    gpu.synchronize()
+    got_q = dq.numpy()
+    kc = bf16_to_f32(from_paged(dk.numpy(), nKV, D))
+    vc = bf16_to_f32(from_paged(dv.numpy(), nKV, D))
+    for t in range(T):
+        pos = off + t
+        for h in range(nH + nKV):
+            v = qkv[t, h * D:(h + 1) * D]
+            if qk_norm:
+                v = oracle.rms_norm(v[None], qn if h < nH else kn, 1e-6)[0]
+            ref = oracle.rope(v, pos, invf, traditional=traditional)
+            if h < nH:
+                assert np.max(np.abs(got_q[t, h * D:(h + 1) * D] - ref)) < 2e-5
+            else:
+                assert np.array_equal(kc[h - nH, pos], bf16_to_f32(bf16_round(ref))) or \
+                    np.max(np.abs(kc[h - nH, pos] - ref)) <= np.max(np.abs(ref)) * 2 ** -8
+        for h in range(nKV):
+            assert np.array_equal(vc[h, pos], bf16_to_f32(bf16_round(qkv[t, (nH + nKV + h) * D:(nH + nKV + h + 1) * D])))
+
+
+def run_attention(mlxr, q, kc, vc, nH, nKV, offset, T, scale, lists=None, count=0, list_stride=0, nsplit=32):
+    D = q.shape[-1]
+    S = kc.shape[1]
+    dq = mlxr.DeviceArray.from_numpy(q.reshape(T, nH * D))
+    dk = mlxr.DeviceArray.from_numpy(bf16_round(to_paged(kc)))
+    dv = mlxr.DeviceArray.from_numpy(bf16_round(to_paged(vc)))
+    out = mlxr.DeviceArray.zeros((T, nH * D), np.float32)
+    dl = mlxr.DeviceArray.from_numpy(np.asarray(lists, np.int32)) if lists is not None else None
+    mlxr.check(mlxr.lib.mlxr_k_attention(dq.ptr, nH * D, dk.ptr, dv.ptr, S, D, nH, nKV, offset, T, scale, out.ptr, nH * D,
+                                         dl.ptr if dl else None, count, list_stride, nsplit))
+    mlxr.synchronize()
+    return out.numpy().reshape(T, nH, D)
+
+
+@pytest.mark.parametrize("nH,nKV", [(4, 2), (10, 2), (32, 8), (40, 8)])
+def test_attention_decode_and_split(gpu, nH, nKV):
+    """kernelsMatchReference (KernelTests.swift:540-586): decode at position 100 of a 128-row cache;
+    single-range and split results agree; over a bf16 cache (values rounded as stored)."""
+    D, S = 128, 128
+    rng = XorShift(D * 31)
+    kc = bf16_to_f32(bf16_round(np.random.default_rng(nH).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
+    vc = bf16_to_f32(bf16_round(np.random.default_rng(nH + 1).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
+    q = np.random.default_rng(nH + 2).uniform(-1, 1, (nH, D)).astype(np.float32)
+    scale = 3 / np.sqrt(D)
+    ref = oracle.attention(q, kc, vc, nH, nKV, 100, scale)
+    one = run_attention(gpu, q, kc, vc, nH, nKV, 100, 1, scale, nsplit=1)[0]
+    split = run_attention(gpu, q, kc, vc, nH, nKV, 100, 1, scale, nsplit=32)[0]
+    assert max_rel_err(one, ref) < 2e-5
+    assert max_rel_err(split, ref) < 2e-5
+    # several query tokens (positions 100..104) run as decode steps
+    q5 = np.random.default_rng(9).uniform(-1, 1, (5, nH, D)).astype(np.float32)
+    got5 = run_attention(gpu, q5, kc, vc, nH, nKV, 100, 5, scale)
+    for t in range(5):
+        assert max_rel_err(got5[t], oracle.attention(q5[t], kc, vc, nH, nKV, 100 + t, scale)) < 2e-5
+    del rng
+
+
+@pytest.mark.parametrize("nH,nKV", [(4, 2), (8, 2), (10, 2)])
+def test_attention_over_lists(gpu, nH, nKV):
+    """attentionOverTheList (SparseAttentionTests.swift:214-297): the full list is bit-identical to
+    split attention; subsets and clamped entries match the reference attention over those positions."""
+    D, S, offset = 128, 128, 100
+    L = offset + 1
+    kc = bf16_to_f32(bf16_round(np.random.default_rng(1).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
+    vc = bf16_to_f32(bf16_round(np.random.default_rng(2).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
+    q = np.random.default_rng(3).uniform(-1, 1, (nH, D)).astype(np.float32)
+    scale = 3 / np.sqrt(D)
+    split = run_attention(gpu, q, kc, vc, nH, nKV, offset, 1, scale)
+    full = run_attention(gpu, q, kc, vc, nH, nKV, offset, 1, scale, lists=np.arange(L), count=L, list_stride=0)
+    assert np.array_equal(full.view(np.uint32), split.view(np.uint32))
+    subset = np.array([0, 1, 2, 3, 20, 21, 22, 23, 52, 53, 54, 55] + list(range(90, L)), np.int32)
+    got = run_attention(gpu, q, kc, vc, nH, nKV, offset, 1, scale, lists=subset, count=subset.size)[0]
+    assert max_rel_err(got, oracle.attention_list(q, kc, vc, nH, nKV, offset, scale, subset, subset.size, 0)) < 2e-5
+    clamped = np.concatenate([subset, [L + 5, -3]]).astype(np.int32)
+    got_c = run_attention(gpu, q, kc, vc, nH, nKV, offset, 1, scale, lists=clamped, count=clamped.size)[0]
+    ref_c = np.sort(np.concatenate([subset, [L - 1, 0]])).astype(np.int32)
+    assert max_rel_err(got_c, run_attention(gpu, q, kc, vc, nH, nKV, offset, 1, scale, lists=ref_c, count=ref_c.size)[0]) < 1e-5
+
+    def head_list(kvh):
+        lst = [0, 1, 2, 3]
+        for b in range(3):
+            start = 8 + 4 * (kvh + 5 * b)
+            lst += list(range(start, start + 4))
+        return lst + list(range(90, L))
+    lists = np.stack([np.array(head_list(h), np.int32) for h in range(nKV)])
+    cnt = lists.shape[1]
+    got_h = run_attention(gpu, q, kc, vc, nH, nKV, offset, 1, scale, lists=lists.reshape(-1), count=cnt, list_stride=cnt)[0]
+    ref_h = oracle.attention_list(q, kc, vc, nH, nKV, offset, scale, lists.reshape(-1), cnt, cnt)
+    assert max_rel_err(got_h, ref_h) < 2e-5
+
+
+def test_sparse_index_is_block_mean(gpu):
+    """indexIsTheMeanOfEachBlock (SparseAttentionTests.swift:60-85)."""
+    nKV, D, S = 2, 128, 64
+    k = bf16_to_f32(bf16_round(XorShift(11).floats(nKV * S * D).reshape(nKV, S, D)))
+    dk = gpu.DeviceArray.from_numpy(bf16_round(to_paged(k)))
+    sentinel = bf16_round(np.array([7.0], np.float32))[0]
+    idx = gpu.DeviceArray.from_numpy(np.full(S // 4 * nKV * D, sentinel, np.uint16))
+    gpu.check(gpu.lib.mlxr_k_sparse_index(dk.ptr, S, nKV, D, 12, 28, idx.ptr))   # blocks 3 .. 9
+    gpu.synchronize()
+    got = bf16_to_f32(idx.numpy()).reshape(S // 4, nKV, D)
+    ref = oracle.sparse_index(k, nKV, D, S, 3, 7)
+    for b in range(S // 4):
+        if 3 <= b < 10:
+            assert np.array_equal(got[b], ref[b])
+        else:
+            assert np.all(got[b] == 7.0)
+
+
+@pytest.mark.parametrize("nH,nKV", [(8, 2), (16, 8), (32, 8), (40, 8), (12, 6)])
+def test_sparse_scores(gpu, nH, nKV):
+    """scoresSumTheHeadsDotProducts (SparseAttentionTests.swift:88-121), tol 1e-3 * max(1, |s|)."""
+    D, b0, nb = 128, 2, 150
+    rng = XorShift(nH * 1000 + D)
+    q = rng.floats(nH * D).reshape(nH, D)
+    idxf = bf16_to_f32(bf16_round(rng.floats((b0 + nb) * nKV * D))).reshape(b0 + nb, nKV, D)
+    dq, di = gpu.DeviceArray.from_numpy(q), gpu.DeviceArray.from_numpy(bf16_round(idxf))
+    for rows in (1, nKV):
+        ds = gpu.DeviceArray.zeros(rows * nb, np.float32)
+        gpu.check(gpu.lib.mlxr_k_sparse_score(dq.ptr, di.ptr, nH, nKV, D, b0, nb, rows, ds.ptr))
+        gpu.synchronize()
+        ref = oracle.sparse_score(q, idxf, nH, nKV, D, b0, nb, rows)
+        assert np.all(np.abs(ds.numpy().reshape(rows, nb) - ref) <= 1e-3 * np.maximum(1, np.abs(ref)))
+
+
+SELECT_CASES = [(1000, 100, None), (777, 777, None), (5000, 512, [-1, 0, 0.5, 2]), (33, 1, None), (4096, 3, [-3, -2.5]),
+                (3, 2, [1])]
+
+
+@pytest.mark.parametrize("N,p,values", SELECT_CASES)
+def test_sparse_select_exact(gpu, N, p, values):
+    """selectKeepsTheTopBlocksInPositionOrder (SparseAttentionTests.swift:124-166): exact lists."""
+    sink_end, b0 = 4, 1
+    win_start = (b0 + N) * 4
+    L = win_start + 37
+    rng = XorShift(N * 7 + p)
+    if values is None:
+        scores = np.array([rng.float(-10, 10) for _ in range(N)], np.float32)
+    else:
+        scores = np.array([values[rng.next() % len(values)] for _ in range(N)], np.float32)
+    plan = oracle.SparsePlan(4, b0, N, p, sink_end, win_start, L, sink_end + p * 4 + (L - win_start))
+    ref = oracle.sparse_select(scores, plan)
+    # the reference test's own restatement: sort by (key desc, index asc), keep p, back to position order
+    keys = [oracle.sparse_key(float(s)) for s in scores]
+    kept = sorted(sorted(range(N), key=lambda i: (-keys[i], i))[:p])
+    expect = list(range(sink_end)) + [(b0 + n) * 4 + i for n in kept for i in range(4)] + list(range(win_start, L))
+    assert ref.tolist() == expect
+    ds = gpu.DeviceArray.from_numpy(scores)
+    dl = gpu.DeviceArray.from_numpy(np.full(L + 8, -1, np.int32))
+    gpu.check(gpu.lib.mlxr_k_sparse_select(ds.ptr, 1, b0, N, p, sink_end, win_start, L, dl.ptr, 0))
+    gpu.synchronize()
+    got = dl.numpy()
+    assert got[:plan.count].tolist() == expect
+    assert np.all(got[plan.count:] == -1)
+
+
+def test_sparse_select_rows_independent(gpu):
+    """selectRowsAreIndependent (SparseAttentionTests.swift:170-209)."""
+    N, p, rows = 700, 64, 3
+    b0, sink_end = 1, 4
+    win_start = (b0 + N) * 4
+    L = win_start + 21
+    stride = L + 50
+    rng = XorShift(77)
+    scores = np.array([rng.float(-10, 10) for _ in range(rows * N)], np.float32)
+    ds = gpu.DeviceArray.from_numpy(scores)
+    dl = gpu.DeviceArray.from_numpy(np.full(rows * stride, -1, np.int32))
+    gpu.check(gpu.lib.mlxr_k_sparse_select(ds.ptr, rows, b0, N, p, sink_end, win_start, L, dl.ptr, stride))
+    gpu.synchronize()
+    got = dl.numpy().reshape(rows, stride)
+    count = sink_end + p * 4 + (L - win_start)
+    plan = oracle.SparsePlan(4, b0, N, p, sink_end, win_start, L, count)
+    for r in range(rows):
+        assert got[r, :count].tolist() == oracle.sparse_select(scores[r * N:(r + 1) * N], plan).tolist()
+        assert np.all(got[r, count:] == -1)
+
+
+def sample_gpu(mlxr, logits, params, history=(), draws=1, seed=1):
+    V = len(logits)
+    hist = np.zeros(len(history) + 2, np.int32)
+    hist[:len(history)] = history
+    dh = mlxr.DeviceArray.from_numpy(hist)
+    st = mlxr.DeviceArray.zeros(len(history) + 2, np.int32)
+    rng = mlxr.DeviceArray.from_numpy(np.array([seed, 0], np.uint64))
+    pos = max(0, len(history) - 1)
+    toks = []
+    for _ in range(draws):
+        dl = mlxr.DeviceArray.from_numpy(np.asarray(logits, np.float32))
+        sp = params.params(V)
+        mlxr.check(mlxr.lib.mlxr_k_sample(dl.ptr, V, dh.ptr, st.ptr, rng.ptr, pos, ctypes.byref(sp)))
+        mlxr.synchronize()
+        toks.append(int(dh.numpy()[pos + 1]))
+    return toks, st.numpy()[pos + 1]
+
+
+def test_logits(V, seed=3):
+    rng = XorShift(seed)
+    l = np.array([-12 + 6 * rng.float() for _ in range(V)], np.float32)
+    for i in range(0, V, 97):
+        l[i] += 8 + 4 * rng.float()
+    l[5] = 7.25; l[777 % V] = 7.25; l[V - 1] = 7.25
+    return l
+
+
+test_logits.__test__ = False
+
+
+def test_greedy_ties_and_penalty(gpu):
+    """greedyMatchesCPUArgmaxIncludingTiesAndPenalty (KernelTests.swift:355-375)."""
+    for V in (1000, 32768, 151936):
+        l = test_logits(V)
+        l[300] = 30; l[9] = 30
+        p = gpu.SamplingParameters(temperature=0, repetition_penalty=1)
+        assert sample_gpu(gpu, l, p)[0] == [9]
+        assert oracle.argmax(l) == 9
+        p = gpu.SamplingParameters(temperature=0, repetition_penalty=1.3, repetition_window=64)
+        hist = [1, 2, 9, 9, 4]
+        ids, _ = oracle.sample_distribution(l, hist[-64:], 0, 40, 1, 0, 1.3)
+        assert ids[0] == 300
+        assert sample_gpu(gpu, l, p, history=hist)[0] == [300]
+
+
+def test_non_finite_logits_reported(gpu):
+    l = test_logits(4096)
+    l[7] = np.inf
+    toks, status = sample_gpu(gpu, l, gpu.SamplingParameters())
+    assert status == 1 and toks == [0]
+
+
+@pytest.mark.parametrize("top_k,top_p,min_p", [(40, 0.95, 0.0), (0, 1.0, 0.0), (200, 0.8, 0.05), (5, 1.0, 0.0)])
+def test_sampled_distribution(gpu, top_k, top_p, min_p):
+    """sampledDistributionMatchesCPU (KernelTests.swift:394-419): same support, frequencies within 4.5 sigma."""
+    V = 32768
+    l = test_logits(V, seed=11)
+    hist = [i * 97 for i in range(40)]
+    p = gpu.SamplingParameters(temperature=0.9, top_k=top_k, top_p=top_p, min_p=min_p, repetition_penalty=1.1)
+    ids, probs = oracle.sample_distribution(l, hist[-64:], 0.9, top_k, top_p, min_p, 1.1)
+    cpu = dict(zip(ids.tolist(), probs.tolist()))
+    draws = 3000
+    toks, _ = sample_gpu(gpu, l, p, history=hist, draws=draws)
+    freq = {}
+    for t in toks:
+        freq[t] = freq.get(t, 0) + 1
+    for t in freq:
+        assert t in cpu, t
+    for t, pr in cpu.items():
+        if pr > 0.01:
+            f = freq.get(t, 0) / draws
+            assert abs(f - pr) < 4.5 * np.sqrt(pr * (1 - pr) / draws) + 0.002, (t, pr, f)
