@@ -1,0 +1,193 @@
+"""Benchmark of the token loop on one MI355X (BASELINE.json metric).
+
+Default workload: a random-init Qwen3-8B-shaped model, MLX affine 4-bit
+group 64 (bf16 scale/bias), bf16 KV cache; a 4096-token prompt of random ids is prefilled, then
+batch-1 greedy decode. A "step" is one decode token: W untimed steps, then K timed steps issued as
+the reference's pipelined loop does (step n+1 committed before step n is read back, Engine.swift:740-763),
+bracketed by device synchronisation. value = decode tokens/s of the whole job (one GPU).
+
+Extra objects on the JSON line:
+- roofline: the dominant decode kernel (the fused gate|up matvec with SiLU epilogue) timed with HIP
+  events on the model's stream over its own timed region (launches cycling through the 36 layers),
+  achieved = algorithmic bytes per launch / mean launch time, against the 8 TB/s HBM peak;
+- step_roofline: the same accounting for the whole decode step (bytes per token at the mean context);
+- prefill: prompt tokens/s of the 4096-token prefill (the config's second metric);
+- cpu_baseline: the CPU oracle (C restatement of the reference's semantics, all host cores) timed on
+  a bounded sample: decode steps at the same context, starting from the GPU-built KV cache.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "mlx-runner_amd"), os.path.join(ROOT, "oracle")]
+
+import configs  # noqa: E402
+import mlxr  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def model_dir(name, seed):
+    base = os.environ.get("MLXR_BENCH_DIR", os.path.join(os.environ.get("TMPDIR", "/tmp"), "mlxr_bench"))
+    d = os.path.join(base, f"{name}-s{seed}")
+    marker = os.path.join(d, ".complete")
+    if not os.path.exists(marker):
+        t = time.time()
+        log(f"[bench] writing synthetic {name} (seed {seed}) to {d}")
+        mlxr.synth_write(configs.CONFIGS[name], seed=seed, directory=d)
+        open(marker, "w").write("ok")
+        log(f"[bench] synthetic model written in {time.time() - t:.1f}s")
+    return d
+
+
+def weight_bytes(cfg):
+    """Quantized bytes of every projection + lm_head (bits/8 + 4/gs bytes per weight)."""
+    H, I, L, V = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"], cfg["vocab_size"]
+    D, nH, nKV = cfg["head_dim"], cfg["num_attention_heads"], cfg["num_key_value_heads"]
+    q = cfg["quantization"]
+    bpw = q["bits"] / 8 + 4 / q["group_size"]
+    per_layer = H * (nH + 2 * nKV) * D + nH * D * H + 3 * H * I
+    return (L * per_layer + V * H) * bpw
+
+
+def step_bytes(cfg, ctx):
+    """Algorithmic HBM bytes of one decode token at context ctx (SURVEY 8d accounting): weights,
+    the bf16 K/V read (2 * nKV * D * ctx * 2 bytes per layer), the KV append, the embedding row and
+    the logits write+read."""
+    L, D, nKV, V, H = cfg["num_hidden_layers"], cfg["head_dim"], cfg["num_key_value_heads"], cfg["vocab_size"], cfg["hidden_size"]
+    q = cfg["quantization"]
+    kv = L * 2 * nKV * D * ctx * 2 + L * 2 * nKV * D * 2
+    return weight_bytes(cfg) + kv + H * (q["bits"] / 8 + 4 / q["group_size"]) + V * 4 * 2
+
+
+def cpu_baseline(d, model, cfg, ctx, tokens, budget_s):
+    import oracle
+    t0 = time.time()
+    ref = oracle.Model(d, model.max_seq)
+    L, nKV, D = cfg["num_hidden_layers"], cfg["num_key_value_heads"], cfg["head_dim"]
+    for layer in range(L):
+        k, v = model.read_kv(layer, ctx, nKV, D)
+        ref.set_kv(layer, k, v)
+    log(f"[bench] oracle loaded with the GPU's KV cache in {time.time() - t0:.1f}s")
+    done, t = 0, time.time()
+    pos = ctx
+    while done < tokens:
+        ref.forward(np.array([7 + done], np.int32), pos)
+        pos += 1
+        done += 1
+        if time.time() - t > budget_s:
+            break
+    el = time.time() - t
+    ref.close()
+    return {"value": done / el, "unit": "tok/s", "cores": oracle.threads(), "kind": "port",
+            "sample": f"{done} greedy decode token(s) of the same model at context {ctx} (KV cache copied from the GPU run), "
+                      f"fp32 C oracle, OpenMP over {oracle.threads()} host threads; {el:.1f}s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", default="qwen3-8b", choices=sorted(configs.CONFIGS))
+    ap.add_argument("--context", type=int, default=4096, help="prefilled prompt tokens")
+    ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--cpu-tokens", type=int, default=2)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-iters", type=int, default=360)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: multi-GPU runs are not part of it (see DESIGN.md, sharding)",
+                          "n_gpus": a.gpus}))
+        sys.exit(2)
+    if mlxr.device_count() < 1:
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    cfg = configs.CONFIGS[a.config]
+    d = model_dir(a.config, a.seed)
+    need = a.context + a.warmup + a.steps + 8
+    t = time.time()
+    model = mlxr.Transformer(d, context_length=need)
+    log(f"[bench] model loaded in {time.time() - t:.1f}s ({model.weight_bytes / 1e9:.2f} GB of weights, {model.quant_description})")
+    greedy = mlxr.SamplingParameters.greedy()
+    prompt = np.random.default_rng(a.seed).integers(0, model.vocab_size, a.context).astype(np.int32)
+
+    # prefill (timed separately; warm the kernels once on a short prompt first)
+    model.prefill(prompt[:64], 0, greedy)
+    mlxr.synchronize()
+    t = time.perf_counter()
+    first = model.prefill(prompt, 0, greedy)
+    mlxr.synchronize()
+    prefill_s = time.perf_counter() - t
+    log(f"[bench] prefill {a.context} tokens: {prefill_s * 1e3:.1f} ms ({a.context / prefill_s:.0f} tok/s)")
+
+    # decode: warmup, then K timed steps, two in flight
+    pos = a.context
+
+    def run(n, pos):
+        toks = []
+        cur = model.begin_decode_step(pos, greedy)
+        for i in range(n):
+            nxt = model.begin_decode_step(cur.offset + 1, greedy) if i + 1 < n else None
+            toks.append(model.finish(cur))
+            cur = nxt
+        return toks
+
+    run(a.warmup, pos)
+    pos += a.warmup
+    mlxr.synchronize()
+    t = time.perf_counter()
+    toks = run(a.steps, pos)
+    mlxr.synchronize()
+    el = time.perf_counter() - t
+    tok_s = a.steps / el
+    mean_ctx = pos + a.steps / 2
+    sb = step_bytes(cfg, mean_ctx)
+    log(f"[bench] decode {a.steps} steps: {el * 1e3:.1f} ms, {tok_s:.1f} tok/s, {sb * tok_s / 1e9:.0f} GB/s algorithmic")
+
+    # dominant kernel: gate|up matvec over every layer's weights, HIP events on the model stream
+    kern = {}
+    for kind in ("gateup", "down", "qkv", "o", "head", "attn"):
+        iters = a.kernel_iters if kind != "head" else 20
+        ms, b = model.profile_kernel(kind, iters, int(mean_ctx))
+        kern[kind] = {"ms": ms, "bytes": b, "GBs": b / (ms * 1e-3) / 1e9}
+        log(f"[bench] kernel {kind:7s}: {ms * 1e3:8.1f} us  {b / 1e6:8.2f} MB  {kern[kind]['GBs']:7.0f} GB/s")
+    g = kern["gateup"]
+
+    result = {
+        "metric": "decode tok/s (bs1, 8B-shape 4-bit g64) + % HBM roofline; prefill tok/s",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(el * 1e3 / a.steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u4 weights (affine g64, bf16 scale/bias), fp32 activations, bf16 KV",
+        "data": "synthetic: random-init weights N(0,0.02) from a seed, uniform random prompt ids",
+        "config": {"workload": f"{a.config}: {a.context}-token prefilled context + greedy decode (configs[1])",
+                   "model": a.config, "global_batch": 1, "seq_len": a.context + a.warmup + a.steps, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "qmv gate|up + SiLU (fused decode matvec, 4-bit g64, K=4096 -> 2x12288)",
+                     "achieved": round(g["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(g["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": round(g["ms"] * 1e3, 2), "bytes_per_launch": g["bytes"]},
+        "step_roofline": {"achieved": round(sb * tok_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(sb * tok_s / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_token": int(sb),
+                          "tok_s_at_100pct": round(HBM_PEAK_GBS * 1e9 / sb, 1)},
+        "prefill": {"tokens": a.context, "tok_s": round(a.context / prefill_s, 1), "ms": round(prefill_s * 1e3, 1)},
+        "kernels_us": {k: round(v["ms"] * 1e3, 2) for k, v in kern.items()},
+        "first_tokens": [first] + toks[:8],
+    }
+    if not a.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(d, model, cfg, pos + a.steps, a.cpu_tokens, a.cpu_budget)
+    model.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

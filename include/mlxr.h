@@ -108,6 +108,11 @@ int mlxr_set_sparse(mlxr_model* m, const mlxr_sparse_cfg* cfg);
 double mlxr_last_gpu_time(const mlxr_model* m);
 /* Host copies of one layer's KV cache, positions [0, rows): k/v as fp32 [nKV][rows][D]. */
 int mlxr_read_kv(mlxr_model* m, int layer, int rows, float* k_out, float* v_out);
+/* Times one decode kernel class on the model's weights (kind: "qkv", "o", "gateup", "down", "head",
+ * "attn" at `context` keys): `iters` launches cycling through the layers, HIP events around them on
+ * the model's stream. avg_ms: mean launch duration; bytes: algorithmic bytes per launch. Profiling
+ * hook in the spirit of Transformer.profile() (Transformer.swift:1696-1798). */
+int mlxr_profile_kernel(mlxr_model* m, const char* kind, int iters, int context, double* avg_ms, int64_t* bytes);
 /* Decode steps with the whole step captured as a hipGraph (1, default) or launched kernel by kernel (0). */
 int mlxr_set_graphs(mlxr_model* m, int enabled);
 

@@ -133,6 +133,10 @@ int mlxr_read_kv(mlxr_model* m, int layer, int rows, float* k_out, float* v_out)
     if (!m || !k_out || !v_out) return set_error(MLXR_E_INVALID_ARG, "null argument");
     return model_read_kv(m->m, layer, rows, k_out, v_out);
 }
+int mlxr_profile_kernel(mlxr_model* m, const char* kind, int iters, int context, double* avg_ms, int64_t* bytes) {
+    if (!m || !avg_ms || !bytes) return set_error(MLXR_E_INVALID_ARG, "null argument");
+    return model_profile(m->m, kind, iters, context, avg_ms, bytes);
+}
 int mlxr_set_graphs(mlxr_model* m, int enabled) { if (!m) return MLXR_E_INVALID_ARG; m->m->use_graphs = enabled != 0; return MLXR_OK; }
 
 int mlxr_synth_write(const char* config_json, uint64_t seed, float std_, const char* dir) {

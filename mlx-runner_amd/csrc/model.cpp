@@ -11,6 +11,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 #include "json.h"
+#include <functional>
 
 namespace mlxr {
 
@@ -337,6 +338,17 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
     m->max_seq = seq; m->n_pages = seq / MLXR_PAGE;
     Store st;
     if (int rc = load_store(dir, st)) return fail(rc);   // files are validated before any device work
+    {
+        std::vector<std::string> need = {"model.embed_tokens.weight", "model.embed_tokens.scales", "model.embed_tokens.biases", "model.norm.weight"};
+        for (int i = 0; i < c.L; i++) {
+            const std::string p = "model.layers." + std::to_string(i);
+            for (const char* l : {".self_attn.q_proj", ".self_attn.k_proj", ".self_attn.v_proj", ".self_attn.o_proj", ".mlp.gate_proj", ".mlp.up_proj", ".mlp.down_proj"})
+                for (const char* suf : {".weight", ".scales", ".biases"}) need.push_back(p + l + suf);
+            need.push_back(p + ".input_layernorm.weight");
+            need.push_back(p + ".post_attention_layernorm.weight");
+        }
+        for (auto& n : need) if (!st.get(n)) return fail(set_error(MLXR_E_MISSING_TENSOR, n));
+    }
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) return fail(set_error(MLXR_E_NO_DEVICE, "no HIP GPU available"));
     // weight arena
@@ -776,6 +788,62 @@ int model_read_kv(Model* m, int layer, int rows, float* k, float* v) {
                 v[((size_t)h * rows + j) * c.D + d] = bf16_to_f32(vh[src + d]);
             }
         }
+    return MLXR_OK;
+}
+
+// Times one decode kernel class over the model's own weights, cycling through the layers so every
+// launch streams its matrices from HBM (the whole model is far larger than the 256 MB MALL).
+// Events are recorded on the model stream, around the launches only. `bytes`: algorithmic bytes
+// of one launch (quantized weights + scales/biases + activations read and written).
+int model_profile(Model* m, const char* kind_c, int iters, int context, double* avg_ms, int64_t* bytes) {
+    const Config& c = m->cfg;
+    const std::string kind = kind_c ? kind_c : "";
+    if (iters < 1 || context < 1 || context > m->max_seq) return set_error(MLXR_E_INVALID_ARG, "iters / context");
+    auto lin_bytes_of = [](const Lin& l) { return (int64_t)l.O * ((int64_t)l.K * l.bits / 8 + 2 * 2 * (l.K / l.gs)) + (l.m.bias ? (int64_t)l.O * 2 : 0); };
+    std::function<int(int)> launch;
+    int64_t b = 0;
+    hipStream_t s = m->stream;
+    if (kind == "qkv") {
+        const Layer& l0 = m->layers[0];
+        b = lin_bytes_of(l0.q) + lin_bytes_of(l0.k) + lin_bytes_of(l0.v) + (int64_t)c.H * 4 * 2 + (int64_t)m->qkv_cols * 4;
+        launch = [&](int i) { const Layer& ly = m->layers[i % c.L]; const Lin p[3] = {ly.q, ly.k, ly.v};
+            return (int)launch_qmv(qmv_args(p, 3, m->h, ly.in_norm, c.eps, m->qkv, EPI_STORE), s); };
+    } else if (kind == "o") {
+        b = lin_bytes_of(m->layers[0].o) + (int64_t)c.nH * c.D * 4 + (int64_t)c.H * 4 * 2;
+        launch = [&](int i) { const Layer& ly = m->layers[i % c.L]; return (int)launch_qmv(qmv_args(&ly.o, 1, m->attn, nullptr, 0, m->tmp, EPI_ADD), s); };
+    } else if (kind == "gateup") {
+        const Layer& l0 = m->layers[0];
+        b = lin_bytes_of(l0.gate) + lin_bytes_of(l0.up) + (int64_t)c.H * 4 * 2 + (int64_t)c.I * 4;
+        launch = [&](int i) { const Layer& ly = m->layers[i % c.L]; const Lin p[2] = {ly.gate, ly.up};
+            return (int)launch_qmv(qmv_args(p, 2, m->h, ly.post_norm, c.eps, m->mlp, EPI_GATED), s); };
+    } else if (kind == "down") {
+        b = lin_bytes_of(m->layers[0].down) + (int64_t)c.I * 4 + (int64_t)c.H * 4 * 2;
+        launch = [&](int i) { const Layer& ly = m->layers[i % c.L]; return (int)launch_qmv(qmv_args(&ly.down, 1, m->mlp, nullptr, 0, m->tmp, EPI_ADD), s); };
+    } else if (kind == "head") {
+        b = lin_bytes_of(m->head) + (int64_t)c.H * 4 * 2 + (int64_t)c.V * 4;
+        launch = [&](int) { return (int)launch_qmv(qmv_args(&m->head, 1, m->h, m->final_norm, c.eps, m->logits, EPI_STORE), s); };
+    } else if (kind == "attn") {
+        b = (int64_t)2 * c.nKV * context * c.D * 2 + (int64_t)c.nH * c.D * 4 * 2;
+        if (int rc = set_dpos(m, context - 1)) return rc;
+        launch = [&](int i) {
+            const Layer& ly = m->layers[i % c.L];
+            AttnArgs aa; aa.q = m->qkv; aa.q_stride = m->qkv_cols; aa.kc = ly.kc; aa.vc = ly.vc; aa.pt = m->page_table;
+            aa.out = m->attn; aa.out_stride = c.nH * c.D; aa.part = m->part; aa.D = c.D; aa.nH = c.nH; aa.nKV = c.nKV; aa.T = 1;
+            aa.nsplit = m->nsplit_dec; aa.dpos = m->dpos; aa.scale = c.query_scale;
+            return (int)launch_attn_decode(aa, s);
+        };
+    } else {
+        return set_error(MLXR_E_INVALID_ARG, "kind: qkv, o, gateup, down, head, attn");
+    }
+    for (int i = 0; i < std::min(iters, 4); i++) if (launch(i)) return set_error(MLXR_E_GPU, "launch");
+    HIPCHECK(hipEventRecord(m->slots[0].start, s));
+    for (int i = 0; i < iters; i++) if (launch(i)) return set_error(MLXR_E_GPU, "launch");
+    HIPCHECK(hipEventRecord(m->slots[0].stop, s));
+    HIPCHECK(hipEventSynchronize(m->slots[0].stop));
+    float ms = 0;
+    HIPCHECK(hipEventElapsedTime(&ms, m->slots[0].start, m->slots[0].stop));
+    *avg_ms = ms / iters;
+    *bytes = b;
     return MLXR_OK;
 }
 

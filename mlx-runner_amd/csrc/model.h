@@ -111,5 +111,6 @@ int model_seed(Model* m, uint64_t seed);
 int model_set_sparse(Model* m, const mlxr_sparse_cfg* cfg);
 int model_read_kv(Model* m, int layer, int rows, float* k, float* v);
 void sparse_clamp(mlxr_sparse_cfg& c);
+int model_profile(Model* m, const char* kind, int iters, int context, double* avg_ms, int64_t* bytes);
 
 }  // namespace mlxr

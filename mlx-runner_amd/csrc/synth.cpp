@@ -82,7 +82,11 @@ void rand_vec_tensor(const std::string& name, uint64_t seed, uint64_t tid, int n
 int synth_write(const char* config_json, uint64_t seed, float std_, const char* dir) {
     Json cfg; std::string err;
     if (!Json::parse(config_json, strlen(config_json), cfg, err) || cfg.t != Json::Obj) return set_error(MLXR_E_INVALID_ARG, "config: " + err);
-    mkdir(dir, 0755);
+    {   // mkdir -p
+        std::string path = dir;
+        for (size_t i = 1; i <= path.size(); i++)
+            if (i == path.size() || path[i] == '/') mkdir(path.substr(0, i).c_str(), 0755);
+    }
     {
         FILE* f = fopen((std::string(dir) + "/config.json").c_str(), "wb");
         if (!f) return set_error(MLXR_E_INVALID_FILE, std::string("cannot write ") + dir);

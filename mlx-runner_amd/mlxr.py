@@ -69,6 +69,7 @@ def _load():
         "mlxr_reusable_prefix": (I, [P, I, I]), "mlxr_reset_write_tracking": (V, [P]),
         "mlxr_seed_sampler": (I, [P, C.c_uint64]), "mlxr_set_sparse": (I, [P, C.POINTER(SparseCfg)]),
         "mlxr_last_gpu_time": (C.c_double, [P]), "mlxr_read_kv": (I, [P, I, I, P, P]), "mlxr_set_graphs": (I, [P, I]),
+        "mlxr_profile_kernel": (I, [P, C.c_char_p, I, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
         "mlxr_synth_write": (I, [C.c_char_p, C.c_uint64, F, C.c_char_p]),
         "mlxr_quantize_row": (I, [P, I, I, I, P, P, P]),
         "mlxr_device_count": (I, []), "mlxr_device_name": (C.c_char_p, []),
@@ -272,6 +273,12 @@ class Transformer:
     def set_sparse(self, sparse: SparseAttention | None):
         cfg = sparse.cfg() if sparse is not None else None
         check(lib.mlxr_set_sparse(self._h, C.byref(cfg) if cfg is not None else None))
+
+    def profile_kernel(self, kind: str, iters: int = 100, context: int = 1):
+        """(mean launch ms, algorithmic bytes per launch) of one decode kernel class."""
+        ms, b = C.c_double(), C.c_int64()
+        check(lib.mlxr_profile_kernel(self._h, kind.encode(), iters, context, C.byref(ms), C.byref(b)))
+        return ms.value, b.value
 
     def set_graphs(self, on: bool):
         check(lib.mlxr_set_graphs(self._h, 1 if on else 0))

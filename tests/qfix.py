@@ -125,3 +125,35 @@ def max_rel_err(a, b):
     """assertClose's metric (KernelTests.swift:116-124): |a-b| / max(1, |b|)."""
     a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
     return float(np.max(np.abs(a - b) / np.maximum(1.0, np.abs(b)))) if a.size else 0.0
+
+
+def read_safetensors(path):
+    """Minimal reader (header JSON + raw little-endian data): bf16 tensors come back as uint16."""
+    import json
+    import struct
+    raw = open(path, "rb").read()
+    (hl,) = struct.unpack("<Q", raw[:8])
+    hdr = json.loads(raw[8:8 + hl])
+    data = memoryview(raw)[8 + hl:]
+    dt = {"U32": np.uint32, "BF16": np.uint16, "F16": np.float16, "F32": np.float32, "U8": np.uint8, "I32": np.int32}
+    out = {}
+    for k, v in hdr.items():
+        if k == "__metadata__":
+            continue
+        a, b = v["data_offsets"]
+        out[k] = np.frombuffer(data[a:b], dtype=dt[v["dtype"]]).reshape(v["shape"]).copy()
+    return out
+
+
+def write_safetensors(path, tensors, dtypes):
+    import json
+    import struct
+    hdr, off, blobs = {}, 0, []
+    for k, a in tensors.items():
+        b = np.ascontiguousarray(a).tobytes()
+        hdr[k] = {"dtype": dtypes[k], "shape": list(a.shape), "data_offsets": [off, off + len(b)]}
+        off += len(b)
+        blobs.append(b)
+    h = json.dumps(hdr).encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)) + h + b"".join(blobs))
