@@ -113,6 +113,18 @@ int mlxr_read_kv(mlxr_model* m, int layer, int rows, float* k_out, float* v_out)
  * the model's stream. avg_ms: mean launch duration; bytes: algorithmic bytes per launch. Profiling
  * hook in the spirit of Transformer.profile() (Transformer.swift:1696-1798). */
 int mlxr_profile_kernel(mlxr_model* m, const char* kind, int iters, int context, double* avg_ms, int64_t* bytes);
+/* Decode step implementation: 1 (default) = the persistent kernel (one launch per token, grid
+ * barriers between phases) where the model allows it, 0 = one kernel per operation. */
+int mlxr_set_decode_mode(mlxr_model* m, int mode);
+/* Runs one persistent greedy decode step at `offset` with wall-clock marks at every phase boundary:
+ * out[3e..3e+2] = mean start, mean end, latest end (us) of interval e over the workgroups
+ * (intervals alternate phase work / barrier wait). Returns the interval count or an error.
+ * max_intervals < 0: raw marks instead, out[w * 1024 + e] = time (us) of mark e of workgroup w
+ * (-1 where unset; marks 512 + 8 * layer + k are sub-phase points), out sized for every
+ * workgroup; returns the workgroup count. */
+int mlxr_profile_decode_phases(mlxr_model* m, int offset, double* out, int max_intervals);
+/* 1 when begin_decode runs the persistent kernel for dense steps. */
+int mlxr_decode_mode(const mlxr_model* m);
 /* Decode steps with the whole step captured as a hipGraph (1, default) or launched kernel by kernel (0). */
 int mlxr_set_graphs(mlxr_model* m, int enabled);
 

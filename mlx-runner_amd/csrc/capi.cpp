@@ -137,6 +137,12 @@ int mlxr_profile_kernel(mlxr_model* m, const char* kind, int iters, int context,
     if (!m || !avg_ms || !bytes) return set_error(MLXR_E_INVALID_ARG, "null argument");
     return model_profile(m->m, kind, iters, context, avg_ms, bytes);
 }
+int mlxr_set_decode_mode(mlxr_model* m, int mode) { return m ? model_set_decode_mode(m->m, mode) : set_error(MLXR_E_INVALID_ARG, "null model"); }
+int mlxr_decode_mode(const mlxr_model* m) { return m && m->m->mega_ok && m->m->decode_mode == 1 ? 1 : 0; }
+int mlxr_profile_decode_phases(mlxr_model* m, int offset, double* out, int max_intervals) {
+    if (!m || !out) return set_error(MLXR_E_INVALID_ARG, "null argument");
+    return model_phase_times(m->m, offset, out, max_intervals);
+}
 int mlxr_set_graphs(mlxr_model* m, int enabled) { if (!m) return MLXR_E_INVALID_ARG; m->m->use_graphs = enabled != 0; return MLXR_OK; }
 
 int mlxr_synth_write(const char* config_json, uint64_t seed, float std_, const char* dir) {

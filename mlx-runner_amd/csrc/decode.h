@@ -1,0 +1,56 @@
+// Persistent decode step (decode.hip): device-side descriptors.
+#pragma once
+#include <algorithm>
+#include "kernels.h"
+
+namespace mlxr {
+
+struct MvPhaseDesc {
+    const uint8_t* w[3]; const uint16_t* s[3]; const uint16_t* b[3]; const uint16_t* bias[3];
+    int o1, o2, rows, K, gs, gated;
+};
+
+struct LayerDev {
+    MvPhaseDesc qkv, o, gu, down;
+    const float* in_norm; const float* post_norm; const float* q_norm; const float* k_norm;
+    uint16_t* kc; uint16_t* vc;
+};
+
+// Grid-barrier state: per-XCD arrival counters (one 128-byte line each), the count of XCDs done,
+// and the release epoch every workgroup polls. Monotonic within a launch; reset by the last
+// workgroup to leave the kernel.
+struct MegaSync {
+    unsigned count;      // XCD groups arrived
+    unsigned abort;      // set when a barrier wait expires
+    unsigned gen;        // released epoch
+    unsigned pad0[29];
+    unsigned xcd[8][32]; // arrivals per XCD group (blockIdx % 8)
+};
+
+struct MegaArgs {
+    const LayerDev* layers; int L;
+    MvPhaseDesc head;
+    const uint8_t* embed_w; const uint16_t* embed_s; const uint16_t* embed_b; int embed_gs;
+    const float* final_norm; const float* inv_freq;
+    int H, nH, nKV, I, rot_dim, traditional;
+    float eps, scale;
+    const int* pt;
+    int* hist; int* status; int* dpos;
+    float *h, *qkv, *attn, *mlp, *logits, *part;
+    float* wg_best; int* wg_idx;
+    unsigned* kv_done; unsigned* head_done;
+    MegaSync* sync;
+    int select;                       // 1: greedy token selection fused (writes hist / ring, advances *dpos)
+    int* ring_tok; int* ring_status; int ring_mask;
+    unsigned long long* prof;         // optional: per workgroup, wall-clock at every phase start / end
+};
+constexpr int MEGA_PROF_EVENTS = 1024;
+
+size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split);
+hipError_t launch_decode_step(const MegaArgs& a, int nwg, size_t lds, hipStream_t s);
+hipError_t mega_set_lds_limit(size_t lds);
+int mega_threads();
+int mega_wave_row_cap();   // rows of one phase one wave may own
+int mega_wg_row_cap();     // rows of an accumulate phase one workgroup may own
+
+}  // namespace mlxr

@@ -322,6 +322,83 @@ void sparse_clamp(mlxr_sparse_cfg& c) {   // SparseAttention.init (SparseAttenti
     c.per_head = c.per_head ? 1 : 0;
 }
 
+// The persistent decode step (decode.hip) covers 4-bit bf16-scaled models with head_dim 128,
+// at most 8 query heads per KV head and a KV-head count dividing the workgroup count.
+static int mega_setup(Model* m) {
+    const Config& c = m->cfg;
+    auto no = [&](const std::string& why) { m->mega_ok = false; m->mega_reason = why; return MLXR_OK; };
+    auto four_bf16 = [](const Lin& l) { return l.bits == 4 && l.st == 0 && l.K % 32 == 0; };
+    if (!four_bf16(m->embed) || !four_bf16(m->head)) return no("embedding / lm_head not 4-bit bf16");
+    for (auto& ly : m->layers)
+        for (const Lin* l : {&ly.q, &ly.k, &ly.v, &ly.o, &ly.gate, &ly.up, &ly.down})
+            if (!four_bf16(*l)) return no("a projection is not 4-bit with bf16 scales");
+    if (c.D != 128 || c.nH / c.nKV > 8 || c.rot_dim > 128) return no("head shape");
+    hipDeviceProp_t prop;
+    HIPCHECK(hipGetDeviceProperties(&prop, 0));
+    int cus = prop.multiProcessorCount;
+    const int nwg = cus / c.nKV * c.nKV;
+    if (nwg < c.nKV) return no("too few compute units");
+    const int nsplit = nwg / c.nKV;
+    const int max_keys = (m->max_seq + nsplit - 1) / nsplit;
+    {
+        const int waves = nwg * (mega_threads() / 64);
+        const int rmax = std::max({c.V, (c.nH + 2 * c.nKV) * c.D, 2 * c.I, c.H});
+        if ((rmax + waves - 1) / waves + 2 > mega_wave_row_cap()) return no("too many rows per wave");
+        if ((c.H + nwg - 1) / nwg + 1 > mega_wg_row_cap()) return no("too many residual rows per workgroup");
+    }
+    MegaArgs& a = m->mega;
+    a.H = c.H; a.nH = c.nH; a.nKV = c.nKV; a.I = c.I; a.rot_dim = c.rot_dim; a.traditional = c.traditional;
+    const size_t lds = mega_lds_bytes(a, max_keys);
+    if (lds > 150 * 1024) return no("LDS need " + std::to_string(lds >> 10) + " KiB");
+    if (mega_set_lds_limit(lds) != hipSuccess) return no("LDS attribute");
+    auto desc = [](const Lin* parts, int n, bool gated) {
+        MvPhaseDesc d{};
+        for (int i = 0; i < 3; i++) {
+            const Lin& l = parts[i < n ? i : n - 1];
+            d.w[i] = l.m.w; d.s[i] = l.m.s; d.b[i] = l.m.b; d.bias[i] = l.m.bias;
+        }
+        d.o1 = parts[0].O; d.o2 = n > 1 ? parts[1].O : 0;
+        int rows = 0; for (int i = 0; i < n; i++) rows += parts[i].O;
+        d.rows = rows; d.K = parts[0].K; d.gs = parts[0].gs; d.gated = gated ? 1 : 0;
+        return d;
+    };
+    std::vector<LayerDev> host(c.L);
+    for (int i = 0; i < c.L; i++) {
+        const Layer& ly = m->layers[i];
+        const Lin qkv[3] = {ly.q, ly.k, ly.v}, gu[2] = {ly.gate, ly.up};
+        LayerDev& d = host[i];
+        d.qkv = desc(qkv, 3, false); d.o = desc(&ly.o, 1, false); d.gu = desc(gu, 2, true); d.down = desc(&ly.down, 1, false);
+        d.in_norm = ly.in_norm; d.post_norm = ly.post_norm; d.q_norm = ly.q_norm; d.k_norm = ly.k_norm;
+        d.kc = ly.kc; d.vc = ly.vc;
+    }
+    int rc;
+    if ((rc = dalloc(m, &m->mega_layers, c.L))) return rc;
+    HIPCHECK(hipMemcpy(m->mega_layers, host.data(), sizeof(LayerDev) * c.L, hipMemcpyHostToDevice));
+    a.layers = m->mega_layers; a.L = c.L;
+    a.head = desc(&m->head, 1, false);
+    a.embed_w = m->embed.m.w; a.embed_s = m->embed.m.s; a.embed_b = m->embed.m.b; a.embed_gs = m->embed.gs;
+    a.final_norm = m->final_norm; a.inv_freq = m->inv_freq;
+    a.eps = c.eps; a.scale = c.query_scale * c.rope_attention_factor * c.rope_attention_factor;
+    a.pt = m->page_table; a.hist = m->hist; a.status = m->status; a.dpos = m->dpos;
+    a.h = m->h; a.qkv = m->qkv; a.attn = m->attn; a.mlp = m->mlp; a.logits = m->logits;
+    if ((rc = dalloc(m, &a.part, (size_t)c.nH * nsplit * (c.D + 2))) || (rc = dalloc(m, &a.wg_best, nwg)) ||
+        (rc = dalloc(m, &a.wg_idx, nwg)) || (rc = dalloc(m, &a.kv_done, 64 * 32)) || (rc = dalloc(m, &a.head_done, 64)) ||
+        (rc = dalloc(m, &a.sync, 1)))
+        return rc;
+    HIPCHECK(hipMemset(a.kv_done, 0, 64 * 32 * 4));
+    HIPCHECK(hipMemset(a.head_done, 0, 64 * 4));
+    HIPCHECK(hipMemset(a.sync, 0, sizeof(MegaSync)));
+    a.ring_tok = m->ring_tok_dev; a.ring_status = m->ring_status_dev; a.ring_mask = Model::RING - 1;
+    m->mega_nwg = nwg; m->mega_lds = lds; m->mega_ok = true;
+    return MLXR_OK;
+}
+
+int model_set_decode_mode(Model* m, int mode) {
+    if (mode != 0 && mode != 1) return set_error(MLXR_E_INVALID_ARG, "decode mode: 0 (kernel per op) or 1 (persistent)");
+    m->decode_mode = mode;
+    return MLXR_OK;
+}
+
 int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse, Model** out) {
     *out = nullptr;
     std::string dir = dir_c;
@@ -448,6 +525,7 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
     HIPCHECK(hipHostGetDevicePointer((void**)&m->ring_status_dev, m->ring_status, 0));
     for (auto& s : m->slots) { HIPCHECK(hipEventCreate(&s.start)); HIPCHECK(hipEventCreate(&s.stop)); }
     if ((rc = model_seed(m, 0))) return fail(rc);
+    if ((rc = mega_setup(m))) return fail(rc);
     *out = m;
     return MLXR_OK;
 }
@@ -696,6 +774,16 @@ int model_prefill(Model* m, const int32_t* tokens, int n, int offset, const mlxr
     return read_ring(m, offset + n, tok);
 }
 
+// SparseAttention.plan(position:) != nil (SparseAttention.swift:80-94), on the host.
+static bool sparse_plan_valid(const mlxr_sparse_cfg& c, int position) {
+    const int pool = 4, L = position + 1;
+    if (position < 0 || L < c.min_context) return false;
+    const int sinkEnd = (c.sink + pool - 1) / pool * pool;
+    if (!(L - c.window > sinkEnd)) return false;
+    const int winStart = (L - c.window) / pool * pool;
+    return winStart / pool - sinkEnd / pool > 0;
+}
+
 int model_begin_decode(Model* m, int offset, const mlxr_sample_params* sp, mlxr_step* out) {
     if (offset < 0 || offset + 1 >= m->max_seq) return set_error(MLXR_E_CONTEXT_FULL, "The context window is full.");
     if (int rc = check_sample(sp)) return rc;
@@ -707,7 +795,20 @@ int model_begin_decode(Model* m, int offset, const mlxr_sample_params* sp, mlxr_
     if (int rc = set_dpos(m, offset)) return rc;
     HIPCHECK(hipEventRecord(slot.start, m->stream));
     const bool sparse = m->sparse_on;
-    if (m->use_graphs) {
+    const bool sparse_step = sparse && sparse_plan_valid(m->sparse, offset);
+    if (m->mega_ok && m->decode_mode == 1 && !sparse_step) {
+        const bool greedy = sp->temperature <= 0.001f && sp->penalty == 1.0f;
+        MegaArgs a = m->mega;
+        a.select = greedy ? 1 : 0;
+        HIPCHECK(launch_decode_step(a, m->mega_nwg, m->mega_lds, m->stream));
+        if (!greedy) {
+            const int V = std::min(sp->V > 0 ? (int)sp->V : m->cfg.V, m->cfg.V);
+            if (int rc = encode_sample(m, V, sp, true)) return rc;
+        }
+        if (m->sparse_alloc && (offset + 1) % 4 == 0)   // keep the sparse index of completed blocks
+            for (auto& ly : m->layers)
+                HIPCHECK(launch_sparse_index(ly.kc, m->page_table, ly.idx, m->cfg.nKV, m->cfg.D, m->dpos, -1, 1, m->stream));
+    } else if (m->use_graphs) {
         Model::GraphKey key{sp->window, sp->top_k, sparse ? 1 : 0, sp->penalty, sp->temperature, sp->top_p, sp->min_p};
         auto it = m->graphs.find(key);
         if (it == m->graphs.end()) {
@@ -744,6 +845,15 @@ int model_finish(Model* m, const mlxr_step* st, int32_t* tok) {
     slot.busy = false;
     if (e != hipSuccess) return set_error(MLXR_E_GPU, std::string("GPU error: ") + hipGetErrorString(e));
     record_gpu_time(m, slot);
+    if (m->mega_ok) {
+        MegaSync ms;
+        HIPCHECK(hipMemcpy(&ms, m->mega.sync, sizeof(MegaSync), hipMemcpyDeviceToHost));
+        if (ms.abort) {
+            m->mega_ok = false;   // fall back to the kernel-per-op step from now on
+            HIPCHECK(hipMemset(m->mega.sync, 0, sizeof(MegaSync)));
+            return set_error(MLXR_E_GPU, "persistent decode step: a grid barrier expired (step result discarded)");
+        }
+    }
     return read_ring(m, st->offset + 1, tok);
 }
 
@@ -845,6 +955,45 @@ int model_profile(Model* m, const char* kind_c, int iters, int context, double* 
     *avg_ms = ms / iters;
     *bytes = b;
     return MLXR_OK;
+}
+
+// Runs one persistent decode step at `offset` (greedy, token from hist[offset]) with per-phase
+// wall-clock marks: out[e * 3 + 0..2] = mean start, mean end, max end over workgroups of event
+// interval e, in microseconds from the earliest kernel start. Returns the number of intervals.
+int model_phase_times(Model* m, int offset, double* out, int max_intervals) {
+    if (!m->mega_ok) return set_error(MLXR_E_UNSUPPORTED, "persistent decode step not available: " + m->mega_reason);
+    if (offset < 0 || offset + 1 >= m->max_seq) return set_error(MLXR_E_CONTEXT_FULL, "context");
+    const int nwg = m->mega_nwg;
+    unsigned long long* prof = nullptr;
+    HIPCHECK(hipMalloc(&prof, (size_t)nwg * MEGA_PROF_EVENTS * 8));
+    HIPCHECK(hipMemset(prof, 0, (size_t)nwg * MEGA_PROF_EVENTS * 8));
+    if (int rc = set_dpos(m, offset)) { hipFree(prof); return rc; }
+    MegaArgs a = m->mega; a.select = 1; a.prof = prof;
+    HIPCHECK(launch_decode_step(a, nwg, m->mega_lds, m->stream));
+    m->dev_pos_known = offset + 1;
+    HIPCHECK(hipStreamSynchronize(m->stream));
+    std::vector<unsigned long long> h((size_t)nwg * MEGA_PROF_EVENTS);
+    HIPCHECK(hipMemcpy(h.data(), prof, h.size() * 8, hipMemcpyDeviceToHost));
+    hipFree(prof);
+    int nev = 0;
+    while (nev < MEGA_PROF_EVENTS && h[nev]) nev++;
+    unsigned long long t0 = ~0ull;
+    for (int w = 0; w < nwg; w++) if (h[(size_t)w * MEGA_PROF_EVENTS]) t0 = std::min(t0, h[(size_t)w * MEGA_PROF_EVENTS]);
+    if (max_intervals < 0) {
+        for (size_t i = 0; i < h.size(); i++) out[i] = h[i] ? (double)(h[i] - t0) * 0.01 : -1.0;
+        return nwg;
+    }
+    int n = 0;
+    for (int e = 0; e + 1 < nev && n < max_intervals; e++, n++) {
+        double s0 = 0, s1 = 0, mx = 0;
+        for (int w = 0; w < nwg; w++) {
+            const double a0 = (double)(h[(size_t)w * MEGA_PROF_EVENTS + e] - t0) * 0.01;   // 100 MHz clock
+            const double a1 = (double)(h[(size_t)w * MEGA_PROF_EVENTS + e + 1] - t0) * 0.01;
+            s0 += a0; s1 += a1; mx = std::max(mx, a1);
+        }
+        out[n * 3] = s0 / nwg; out[n * 3 + 1] = s1 / nwg; out[n * 3 + 2] = mx;
+    }
+    return n;
 }
 
 }  // namespace mlxr

@@ -7,6 +7,7 @@
 #include <tuple>
 #include <vector>
 #include "kernels.h"
+#include "decode.h"
 #include "../../include/mlxr.h"
 
 namespace mlxr {
@@ -82,6 +83,13 @@ struct Model {
     int dev_pos_known = -1;              // value *dpos will hold once queued work completes
     int written_high = 0;
     bool use_graphs = true;
+    // persistent decode step (decode.hip)
+    bool mega_ok = false;            // the model fits the persistent kernel's constraints
+    int decode_mode = 1;             // 1: persistent kernel when eligible, 0: kernel per op
+    MegaArgs mega{};
+    LayerDev* mega_layers = nullptr;
+    int mega_nwg = 0; size_t mega_lds = 0;
+    std::string mega_reason;
     double last_gpu_time = 0;
 
     struct StepSlot { hipEvent_t start = nullptr, stop = nullptr; int offset = -1; bool busy = false; };
@@ -111,6 +119,8 @@ int model_seed(Model* m, uint64_t seed);
 int model_set_sparse(Model* m, const mlxr_sparse_cfg* cfg);
 int model_read_kv(Model* m, int layer, int rows, float* k, float* v);
 void sparse_clamp(mlxr_sparse_cfg& c);
+int model_set_decode_mode(Model* m, int mode);
+int model_phase_times(Model* m, int offset, double* out, int max_intervals);
 int model_profile(Model* m, const char* kind, int iters, int context, double* avg_ms, int64_t* bytes);
 
 }  // namespace mlxr

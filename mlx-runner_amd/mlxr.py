@@ -18,7 +18,7 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libmlxr.so")
+LIB_PATH = os.environ.get("MLXR_LIB") or os.path.join(_HERE, "libmlxr.so")
 
 ERRORS = {
     -1: "noMetalDevice", -2: "invalidFile", -3: "missingTensor", -4: "unsupported", -5: "contextFull",
@@ -68,7 +68,7 @@ def _load():
         "mlxr_finish": (I, [P, C.POINTER(Step), C.POINTER(C.c_int32)]),
         "mlxr_reusable_prefix": (I, [P, I, I]), "mlxr_reset_write_tracking": (V, [P]),
         "mlxr_seed_sampler": (I, [P, C.c_uint64]), "mlxr_set_sparse": (I, [P, C.POINTER(SparseCfg)]),
-        "mlxr_last_gpu_time": (C.c_double, [P]), "mlxr_read_kv": (I, [P, I, I, P, P]), "mlxr_set_graphs": (I, [P, I]),
+        "mlxr_last_gpu_time": (C.c_double, [P]), "mlxr_read_kv": (I, [P, I, I, P, P]), "mlxr_set_graphs": (I, [P, I]), "mlxr_set_decode_mode": (I, [P, I]), "mlxr_decode_mode": (I, [P]), "mlxr_profile_decode_phases": (I, [P, I, P, I]),
         "mlxr_profile_kernel": (I, [P, C.c_char_p, I, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
         "mlxr_synth_write": (I, [C.c_char_p, C.c_uint64, F, C.c_char_p]),
         "mlxr_quantize_row": (I, [P, I, I, I, P, P, P]),
@@ -279,6 +279,29 @@ class Transformer:
         ms, b = C.c_double(), C.c_int64()
         check(lib.mlxr_profile_kernel(self._h, kind.encode(), iters, context, C.byref(ms), C.byref(b)))
         return ms.value, b.value
+
+    def set_decode_mode(self, persistent: bool):
+        check(lib.mlxr_set_decode_mode(self._h, 1 if persistent else 0))
+
+    @property
+    def persistent_decode(self) -> bool:
+        return bool(lib.mlxr_decode_mode(self._h))
+
+    def profile_decode_phases(self, offset: int):
+        """[(mean start, mean end, latest end) us] of each interval of one persistent decode step."""
+        out = np.zeros(3 * 1024, np.float64)
+        n = lib.mlxr_profile_decode_phases(self._h, offset, out.ctypes.data, 1024)
+        if n < 0:
+            check(n)
+        return out[:3 * n].reshape(n, 3)
+
+    def profile_decode_marks(self, offset: int):
+        """Raw wall-clock marks (us) of one persistent decode step: [workgroup][mark], -1 unset."""
+        out = np.zeros(4096 * 1024, np.float64)
+        n = lib.mlxr_profile_decode_phases(self._h, offset, out.ctypes.data, -1)
+        if n < 0:
+            check(n)
+        return out[:n * 1024].reshape(n, 1024)
 
     def set_graphs(self, on: bool):
         check(lib.mlxr_set_graphs(self._h, 1 if on else 0))

@@ -96,6 +96,26 @@ def test_graph_and_eager_decode_agree(gpu, models):
     assert a == b
 
 
+@pytest.mark.parametrize("name", ["qwen3", "qwen2", "llama"])
+def test_persistent_decode_matches_kernel_per_op(gpu, models, name):
+    """The persistent decode step (one launch per token) against the kernel-per-op step: same greedy
+    tokens (teacher-forced against the oracle where they part), logits within the 2e-2 gate."""
+    d = models[name]
+    toks = prompt(20, 1000, seed=12)
+    with mlxr.Transformer(d, context_length=512) as m:
+        assert m.persistent_decode, "the tiny model must take the persistent path"
+        a = m.generate(toks, 24, GREEDY)
+        m.set_decode_mode(False)
+        assert not m.persistent_decode
+        b = m.generate(toks, 24, GREEDY)
+        ref = oracle.Model(d, m.max_seq)
+        assert greedy_check(m, ref, toks, a) <= 2
+        if a != b:
+            i = next(k for k in range(len(a)) if a[k] != b[k])
+            logits = ref.forward(np.concatenate([toks, np.array(a[:i], np.int32)]), 0)
+            assert abs(logits[a[i]] - logits[b[i]]) < LOGIT_TOL
+
+
 def test_prefill_vs_incremental_decode(gpu, models):
     """ModelTests.swift:50-69: same argmax and max |d logit| < 0.1 (here: the 2e-2 gate)."""
     d = models["qwen3"]
