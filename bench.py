@@ -7,9 +7,12 @@ the reference's pipelined loop does (step n+1 committed before step n is read ba
 bracketed by device synchronisation. value = decode tokens/s of the whole job (one GPU).
 
 Extra objects on the JSON line:
-- roofline: the dominant decode kernel (the fused gate|up matvec with SiLU epilogue) timed with HIP
-  events on the model's stream over its own timed region (launches cycling through the 36 layers),
-  achieved = algorithmic bytes per launch / mean launch time, against the 8 TB/s HBM peak;
+- roofline: the dominant kernel, the persistent decode step (one launch per token: every layer,
+  lm_head and the greedy token), timed with HIP events on the model's stream over its own timed
+  region; achieved = algorithmic bytes per launch (every weight byte + K/V at the mean context) /
+  mean launch time, against the 8 TB/s HBM peak; traffic = HBM bytes per launch from rocprofv3
+  FETCH_SIZE + WRITE_SIZE (copy-kernel calibrated), read from profiles/decode_step_traffic.json
+  when that file is for the same config (null otherwise), with the context it was measured at;
 - step_roofline: the same accounting for the whole decode step (bytes per token at the mean context);
 - prefill: prompt tokens/s of the 4096-token prefill (the config's second metric);
 - cpu_baseline: the CPU oracle (C restatement of the reference's semantics, all host cores) timed on
@@ -105,7 +108,19 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=360)
+    ap.add_argument("--step-iters", type=int, default=64)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="only run 3 device-to-device copy kernels of MB MiB each (calibrates rocprofv3 byte counters)")
     a = ap.parse_args()
+    if a.copy_probe:
+        import torch
+        src = torch.empty(a.copy_probe << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": a.copy_probe << 20, "launches": 3}))
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: multi-GPU runs are not part of it (see DESIGN.md, sharding)",
                           "n_gpus": a.gpus}))
@@ -115,7 +130,7 @@ def main():
         sys.exit(1)
     cfg = configs.CONFIGS[a.config]
     d = model_dir(a.config, a.seed)
-    need = a.context + a.warmup + a.steps + 8
+    need = a.context + a.warmup + a.steps + a.step_iters + 16
     t = time.time()
     model = mlxr.Transformer(d, context_length=need)
     log(f"[bench] model loaded in {time.time() - t:.1f}s ({model.weight_bytes / 1e9:.2f} GB of weights, {model.quant_description})")
@@ -155,14 +170,26 @@ def main():
     sb = step_bytes(cfg, mean_ctx)
     log(f"[bench] decode {a.steps} steps: {el * 1e3:.1f} ms, {tok_s:.1f} tok/s, {sb * tok_s / 1e9:.0f} GB/s algorithmic")
 
-    # dominant kernel: gate|up matvec over every layer's weights, HIP events on the model stream
+    # dominant kernel: the persistent decode step, HIP events on the model stream (the context runs on
+    # from the last decoded position; steps overwrite the history after it)
+    step_ms, step_b = model.profile_kernel("step", a.step_iters, pos + a.steps)
+    step_gbs = step_b / (step_ms * 1e-3) / 1e9
+    log(f"[bench] kernel step   : {step_ms * 1e3:8.1f} us  {step_b / 1e6:8.2f} MB  {step_gbs:7.0f} GB/s")
+    traffic, traffic_ctx = None, None
+    tf = os.path.join(ROOT, "profiles", "decode_step_traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            t = json.load(f)
+        if t.get("config") == a.config:   # measured at the context it names (K/V is ~12% of the bytes)
+            traffic = int(t["bytes_per_launch"])
+            traffic_ctx = t.get("context")
+    # the kernel-per-op path's decode kernels (the graph fallback), for reference
     kern = {}
     for kind in ("gateup", "down", "qkv", "o", "head", "attn"):
         iters = a.kernel_iters if kind != "head" else 20
         ms, b = model.profile_kernel(kind, iters, int(mean_ctx))
         kern[kind] = {"ms": ms, "bytes": b, "GBs": b / (ms * 1e-3) / 1e9}
         log(f"[bench] kernel {kind:7s}: {ms * 1e3:8.1f} us  {b / 1e6:8.2f} MB  {kern[kind]['GBs']:7.0f} GB/s")
-    g = kern["gateup"]
 
     result = {
         "metric": "decode tok/s (bs1, 8B-shape 4-bit g64) + % HBM roofline; prefill tok/s",
@@ -172,10 +199,11 @@ def main():
         "data": "synthetic: random-init weights N(0,0.02) from a seed, uniform random prompt ids",
         "config": {"workload": f"{a.config}: {a.context}-token prefilled context + greedy decode (configs[1])",
                    "model": a.config, "global_batch": 1, "seq_len": a.context + a.warmup + a.steps, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "kernel": "qmv gate|up + SiLU (fused decode matvec, 4-bit g64, K=4096 -> 2x12288)",
-                     "achieved": round(g["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_launch_us": round(g["ms"] * 1e3, 2), "bytes_per_launch": g["bytes"]},
+        "roofline": {"bound": "hbm", "kernel": "decode_step_kernel (persistent: whole token step in one launch)",
+                     "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "avg_launch_us": round(step_ms * 1e3, 2), "bytes_per_launch": int(step_b),
+                     "context": pos + a.steps, "traffic_context": traffic_ctx},
         "step_roofline": {"achieved": round(sb * tok_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(sb * tok_s / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_token": int(sb),
                           "tok_s_at_100pct": round(HBM_PEAK_GBS * 1e9 / sb, 1)},

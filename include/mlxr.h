@@ -109,9 +109,11 @@ double mlxr_last_gpu_time(const mlxr_model* m);
 /* Host copies of one layer's KV cache, positions [0, rows): k/v as fp32 [nKV][rows][D]. */
 int mlxr_read_kv(mlxr_model* m, int layer, int rows, float* k_out, float* v_out);
 /* Times one decode kernel class on the model's weights (kind: "qkv", "o", "gateup", "down", "head",
- * "attn" at `context` keys): `iters` launches cycling through the layers, HIP events around them on
- * the model's stream. avg_ms: mean launch duration; bytes: algorithmic bytes per launch. Profiling
- * hook in the spirit of Transformer.profile() (Transformer.swift:1696-1798). */
+ * "attn" at `context` keys; "step": the persistent whole-token decode kernel, greedy steps from
+ * position context - 1, which overwrite the history after it): `iters` launches cycling through
+ * the layers, HIP events around them on the model's stream. avg_ms: mean launch duration; bytes:
+ * algorithmic bytes per launch. Profiling hook in the spirit of Transformer.profile()
+ * (Transformer.swift:1696-1798). */
 int mlxr_profile_kernel(mlxr_model* m, const char* kind, int iters, int context, double* avg_ms, int64_t* bytes);
 /* Decode step implementation: 1 (default) = the persistent kernel (one launch per token, grid
  * barriers between phases) where the model allows it, 0 = one kernel per operation. */

@@ -942,8 +942,35 @@ int model_profile(Model* m, const char* kind_c, int iters, int context, double* 
             aa.nsplit = m->nsplit_dec; aa.dpos = m->dpos; aa.scale = c.query_scale;
             return (int)launch_attn_decode(aa, s);
         };
+    } else if (kind == "step") {
+        // the persistent decode step (one launch per token): greedy steps from position context - 1,
+        // each advancing the device position; bytes = every weight byte read + K/V at the mean context
+        if (!m->mega_ok) return set_error(MLXR_E_UNSUPPORTED, "persistent decode step not available: " + m->mega_reason);
+        const int warm = std::min(iters, 4);
+        if (context - 1 + warm + iters + 1 >= m->max_seq) return set_error(MLXR_E_CONTEXT_FULL, "context + iters");
+        for (const Layer& ly : m->layers)
+            for (const Lin* l : {&ly.q, &ly.k, &ly.v, &ly.o, &ly.gate, &ly.up, &ly.down}) b += lin_bytes_of(*l);
+        b += lin_bytes_of(m->head) + (int64_t)c.H / 2 + 4 * (c.H / m->embed.gs);
+        const double mean_ctx = context + warm + (iters - 1) / 2.0;
+        b += (int64_t)(2.0 * c.L * c.nKV * mean_ctx * c.D * 2);
+        if (int rc = set_dpos(m, context - 1)) return rc;
+        launch = [&](int) {
+            MegaArgs a = m->mega; a.select = 1;
+            return (int)launch_decode_step(a, m->mega_nwg, m->mega_lds, s);
+        };
+        for (int i = 0; i < warm; i++) if (launch(i)) return set_error(MLXR_E_GPU, "launch");
+        HIPCHECK(hipEventRecord(m->slots[0].start, s));
+        for (int i = 0; i < iters; i++) if (launch(i)) return set_error(MLXR_E_GPU, "launch");
+        HIPCHECK(hipEventRecord(m->slots[0].stop, s));
+        HIPCHECK(hipEventSynchronize(m->slots[0].stop));
+        m->dev_pos_known = context - 1 + warm + iters;
+        float ms = 0;
+        HIPCHECK(hipEventElapsedTime(&ms, m->slots[0].start, m->slots[0].stop));
+        *avg_ms = ms / iters;
+        *bytes = b;
+        return MLXR_OK;
     } else {
-        return set_error(MLXR_E_INVALID_ARG, "kind: qkv, o, gateup, down, head, attn");
+        return set_error(MLXR_E_INVALID_ARG, "kind: qkv, o, gateup, down, head, attn, step");
     }
     for (int i = 0; i < std::min(iters, 4); i++) if (launch(i)) return set_error(MLXR_E_GPU, "launch");
     HIPCHECK(hipEventRecord(m->slots[0].start, s));
