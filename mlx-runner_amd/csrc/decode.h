@@ -5,10 +5,22 @@
 
 namespace mlxr {
 
+// A matvec phase over a repacked (DPack) matrix: rows of up to three concatenated matrices (o1, o2:
+// rows of parts 0 and 1), or gated (o1 = o2 = outputs; gate and up rows interleaved per tile).
 struct MvPhaseDesc {
-    const uint8_t* w[3]; const uint16_t* s[3]; const uint16_t* b[3]; const uint16_t* bias[3];
+    const uint8_t* code;                      // DPack stream (scale groups of scale + code blocks)
+    const uint16_t* bias[3];                  // optional per-row bias of each part (bf16)
+    int o1, o2, rows, K, gs, gated, tiles;
+};
+
+// Source of a repack: the MLX layout (codes [O][K/2], bf16 scales / biases [O][K/gs]) of each part.
+struct DPackSrc {
+    const uint8_t* w[3]; const uint16_t* s[3]; const uint16_t* b[3];
     int o1, o2, rows, K, gs, gated;
 };
+int dpack_tiles(const DPackSrc& s);
+size_t dpack_bytes(const DPackSrc& s);
+hipError_t launch_dpack(const DPackSrc& s, uint8_t* out, hipStream_t st);
 
 struct LayerDev {
     MvPhaseDesc qkv, o, gu, down;
@@ -50,7 +62,7 @@ size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split);
 hipError_t launch_decode_step(const MegaArgs& a, int nwg, size_t lds, hipStream_t s);
 hipError_t mega_set_lds_limit(size_t lds);
 int mega_threads();
-int mega_wave_row_cap();   // rows of one phase one wave may own
+int mega_tiles_per_wg_cap();   // 16-row tiles of one phase one workgroup may own
 int mega_wg_row_cap();     // rows of an accumulate phase one workgroup may own
 
 }  // namespace mlxr

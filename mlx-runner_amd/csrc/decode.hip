@@ -31,14 +31,10 @@ namespace mlxr {
 
 constexpr int MK_THREADS = 512;
 constexpr int MK_WAVES = MK_THREADS / 64;
-#ifndef MLXR_MK_DEPTH
-#define MLXR_MK_DEPTH 8
-#endif
-constexpr int MK_DEPTH = MLXR_MK_DEPTH;   // matvec units in flight per lane
 constexpr int MK_KV_PF = 4;          // attention: K/V rounds (32 keys each) prefetched per thread
 constexpr int MK_MAXG = 8;
 constexpr int MK_HOWN = 1024;        // residual rows of one workgroup in an accumulate phase (max)
-constexpr int MK_YCAP = 512;         // row results of one wave in a matvec phase (max)
+constexpr int MK_TPW = 64;           // 16-row tiles of one workgroup in a matvec phase (max)
 
 // ------------------------------------------------------------------------------- coherence
 // Data one workgroup writes and another reads within the launch (h, q|k|v, attention partials and
@@ -109,16 +105,34 @@ __device__ __forceinline__ void grid_wait(MegaSync* sync, unsigned epoch) {
 }
 
 // ------------------------------------------------------------------------------- matvec phase
-// MvPhaseDesc (decode.h): rows of up to three matrices; o1/o2 = rows of parts 0 and 1 (part 2 gets
-// the rest); gated: virtual row 2o is gate row o (part 0), 2o+1 is up row o (part 1).
+// Weights of the persistent step are a repacked copy (DPack, built once at load by dpack_kernel).
+// A matrix is cut into tiles of 16 rows; a tile is a sequence of scale groups, each covering 16
+// quantization groups (FB = gs / 8 code blocks of 128 codes) and stored as FB + 1 blocks of 1 KB
+// (one 16-byte slice per lane):
+//   block 0      (scale | bias << 16) of rows 4 (l >> 4) + i (i = slot dword), group 16 f + (l & 15):
+//                the accumulator layout of v_mfma_f32_16x16x32_f16;
+//   blocks 1..FB code block k: row 16 t + (l & 15), code dwords 16 kb + 4 j + (l >> 4) (j = slot
+//                dword, one per MFMA), kb = FB f + k - 1: the A-operand layout.
+// Gated phases put gate rows 8t..8t+7 in tile rows 0-7 and the matching up rows in rows 8-15.
+// A wave streams whole scale groups, so its loads walk one contiguous range and every ring slot
+// has a fixed role (slot 0: scales, slot k: code block k - 1).
+//
+// MFMA formulation: a nibble masked into the mantissa of the f16 1024.0 is the half 1024 + q (the
+// nibble at bits 4..7 gives 1024 + 16 q, met by x / 16 in the operand), so A is built with one
+// AND-OR per two codes. B is the chunk's x (f16) in the column of the chunk's group and zero in the
+// other 15, so the accumulator holds per-(row, group) sums sum (1024 + q) x = 1024 X'_g + sum q x
+// for 16 groups at once; the scale and bias are applied once per scale group:
+//   y_row += s_rg (D_rg - Cs_g) + b_rg Xs_g,   Cs_g = 1024 * sum of the group's stored halves.
+// Products of halves are exact and accumulate in fp32.
 typedef MvPhaseDesc MvPhase;
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // Global-address-space pointers: loads through them are global (not flat) loads, which count on
 // the memory counter only; a flat load also counts on the LDS counter, so every wait for an LDS
 // read would wait for it too.
 typedef const __attribute__((address_space(1))) uint8_t* gptr8;
-typedef const __attribute__((address_space(1))) uint16_t* gptr16;
 typedef const __attribute__((address_space(1))) u32x4_t* gptr128;
 // 16-byte streaming load (data read once: the nontemporal hint keeps it from displacing activations)
 __device__ __forceinline__ uint4 ld_stream16(gptr8 p) {
@@ -126,166 +140,79 @@ __device__ __forceinline__ uint4 ld_stream16(gptr8 p) {
     return uint4{v.x, v.y, v.z, v.w};
 }
 
-// Loaded units, kept exactly as loaded: no instruction touches a value before the unit is
-// consumed, so the memory-counter wait for a slot never drains the loads issued after it.
-struct Ring {
-    uint4 code[MK_DEPTH];
-    uint32_t s[MK_DEPTH], b[MK_DEPTH];   // bf16 scale / bias (zero-extended)
+// One scale group in flight per lane (FB + 1 slices of 16 bytes), kept exactly as loaded: no
+// instruction touches a slot before it is consumed, so the memory-counter wait for a slot never
+// drains the loads after it.
+template <int FB>
+struct Ring { uint4 u[FB + 1]; };
+
+// Geometry of a phase for this workgroup / wave.
+template <int FB>
+struct MvGeom {
+    int KBT, NF;            // code blocks and scale groups per tile
+    int t0, nt;             // this workgroup's tiles [t0, t0 + nt)
+    int f0, f1;             // this wave's scale groups [f0, f1) in the workgroup's tile-major order
 };
-
-// Branch-free (the row may differ between the halves of a wave).
-__device__ __forceinline__ void mv_locate(const MvPhase& p, int vr, int& part, int& row) {
-    const int a = vr >= p.o1 ? 1 : 0, b = vr >= p.o1 + p.o2 ? 1 : 0;
-    const int pn = a + b, rn = vr - (a ? p.o1 : 0) - (b ? p.o2 : 0);
-    part = p.gated ? (vr & 1) : pn;
-    row = p.gated ? (vr >> 1) : rn;
+template <int FB>
+__device__ __forceinline__ MvGeom<FB> mv_geom(const MvPhase& p, int wg, int nwg, int wave) {
+    MvGeom<FB> g;
+    g.KBT = p.K >> 7; g.NF = (g.KBT + FB - 1) / FB;
+    g.t0 = (int)((int64_t)p.tiles * wg / nwg);
+    g.nt = (int)((int64_t)p.tiles * (wg + 1) / nwg) - g.t0;
+    const int nfw = g.nt * g.NF;
+    g.f0 = nfw * wave / MK_WAVES; g.f1 = nfw * (wave + 1) / MK_WAVES;
+    return g;
+}
+// This lane's slice of the wave's first scale group.
+template <int FB>
+__device__ __forceinline__ gptr8 mv_base(const MvPhase& p, const MvGeom<FB>& g, int lane) {
+    return (gptr8)p.code + ((int64_t)g.t0 * g.NF + g.f0) * ((FB + 1) * 1024) + lane * 16;
 }
 
-// Element `part` of a 3-array by selects (dynamic indexing would move the array to scratch memory).
-// Mask arithmetic rather than a conditional, which the compiler turns into divergent branches.
-template <typename T>
-__device__ __forceinline__ T pick3(const T (&a)[3], int part) {
-    const uint64_t m0 = 0ull - (uint64_t)(part == 0), m1 = 0ull - (uint64_t)(part == 1), m2 = 0ull - (uint64_t)(part == 2);
-    return (T)(((uint64_t)a[0] & m0) | ((uint64_t)a[1] & m1) | ((uint64_t)a[2] & m2));
+template <int FB>
+__device__ __forceinline__ void mv_prefetch(const MvPhase p, int wg, int nwg, int wave, int lane, Ring<FB>& ring) {
+    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, wave);
+    if (g.f1 <= g.f0) return;
+    const gptr8 b = mv_base<FB>(p, g, lane);
+#pragma unroll
+    for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
 }
 
-// Work split of a wave's rows [r0, r1): rows go in pairs, lanes 0-31 take the pair's first row and
-// lanes 32-63 its second; a unit is one 32-code chunk per lane, (lane & 31) + 32 * ci. One pair
-// takes nci = ceil(chunks / 32) units, so a wave load reads two runs of 512 contiguous bytes, and a
-// row sum needs a 32-lane reduction once per nci units (DPP, no LDS round trip).
-// Load cursor: per-lane pointers advance by 32 chunks per unit and are recomputed once per pair.
-// Every unit issues its loads from a valid address (a lane past its row's last chunk, or on the
-// missing second row of an odd tail, re-reads its row's first chunk and is zeroed when consumed),
-// so the ring has no branches around loads and the memory-counter waits stay exact. Units past the
-// wave's last re-read the last one.
-struct Cursor {
-    gptr8 w; gptr16 s; gptr16 b;   // this lane's unit pointers
-    int pr, ci;                    // pair's first row, unit within the pair (wave-uniform)
-};
-
-__device__ __forceinline__ void cursor_pair(const MvPhase& p, int pr, int r1, int lane, int gsh, Cursor& c) {
-    int part, row; mv_locate(p, min(pr + (lane >> 5), r1 - 1), part, row);
-    const int gpr = p.K >> gsh, ch = lane & 31;
-    c.w = (gptr8)pick3(p.w, part) + (int64_t)row * (p.K >> 1) + ch * 16;
-    c.s = (gptr16)pick3(p.s, part) + (int64_t)row * gpr + ((ch << 5) >> gsh);
-    c.b = (gptr16)pick3(p.b, part) + (int64_t)row * gpr + ((ch << 5) >> gsh);
-    c.pr = pr; c.ci = 0;
+// Constants of the A-operand build, made opaque to constant folding (ORed with a per-lane register
+// that is 0 at run time) so that (w & m) | c becomes one v_and_or_b32 with the constants in registers rather
+// than an AND and an OR with literals. No inline assembly here: the compiler must see every VGPR
+// write that feeds an MFMA operand to insert the wait states the matrix core requires.
+struct DotConsts { uint32_t m_lo, m_hi, magic; };   // magic: two halves of 1024.0
+__device__ __forceinline__ DotConsts dot_consts(int zero) {
+    const uint32_t z = (uint32_t)zero;
+    return DotConsts{0x000F000Fu | z, 0x00F000F0u | z, 0x64006400u | z};
+}
+// A operand of one code dword: halves (n0, n4, 16 n1, 16 n5, n2, n6, 16 n3, 16 n7) + 1024.
+__device__ __forceinline__ f16x8_t a_operand(uint32_t w, const DotConsts& k) {
+    const uint32_t w8 = w >> 8;
+    const u32x4_t v = {(w & k.m_lo) | k.magic, (w & k.m_hi) | k.magic, (w8 & k.m_lo) | k.magic, (w8 & k.m_hi) | k.magic};
+    return __builtin_bit_cast(f16x8_t, v);
 }
 
-// FULL: every row has a multiple of 32 chunks (no lane is ever past its row's end).
-template <bool FULL>
-__device__ __forceinline__ void cursor_load(const Cursor& c, int lane, int nch, int gsh, uint4& code, uint32_t& sv, uint32_t& bv) {
-    if (FULL) { code = ld_stream16(c.w); sv = *c.s; bv = *c.b; return; }
-    const int ch = (lane & 31) + 32 * c.ci;
-    const bool ok = ch < nch;
-    const int back = ok ? 0 : c.ci * 512;                      // re-read the lane's first unit of the row
-    const int sback = ok ? 0 : ((c.ci * 1024) >> gsh);
-    code = ld_stream16(c.w - back);
-    sv = c.s[-sback]; bv = c.b[-sback];
-}
-
-// Whether the step to pair pr (from pr - 2) needs cursor_pair: a part boundary between a half's
-// old and new row, or a missing second row (odd tail). Wave-uniform.
-__device__ __forceinline__ bool pair_slow(const MvPhase& p, int pr, int r1) {
-    if (pr + 1 >= r1) return true;
-    if (p.gated) return false;
-    const int b1 = p.o1, b2 = p.o1 + p.o2;
-    return (b1 > pr - 2 && b1 <= pr + 1) || (b2 > pr - 2 && b2 <= pr + 1);
-}
-
-// Moves to the next unit unless `last` (stays on the wave's final unit). With FULL rows a pair's
-// units advance each lane's pointers by exactly one row, which is the next pair's row in a gated
-// phase (gate row o + 1, up row o + 1) and one row short of it otherwise.
-template <bool FULL>
-__device__ __forceinline__ void cursor_next(const MvPhase& p, int r1, int lane, int gsh, int nci, bool last, Cursor& c) {
-    if (last) return;
-    if (++c.ci == nci) {
-        if (FULL && !pair_slow(p, c.pr + 2, r1)) {
-            c.pr += 2; c.ci = 0;
-            if (!p.gated) { c.w += p.K >> 1; c.s += p.K >> gsh; c.b += p.K >> gsh; }
-            return;
-        }
-        cursor_pair(p, c.pr + 2, r1, lane, gsh, c);
-        return;
-    }
-    c.w += 512; c.s += 1024 >> gsh; c.b += 1024 >> gsh;
-}
-
-// Sum over each half-wave (lanes 0-31, 32-63); the totals land in lanes 31 and 63.
-template <int CTRL, int ROWS = 0xF>
-__device__ __forceinline__ float dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false));
-}
-__device__ __forceinline__ float half_wave_sum(float v) {
-    v += dpp<0xB1>(v);            // quad_perm [1,0,3,2]
-    v += dpp<0x4E>(v);            // quad_perm [2,3,0,1]
-    v += dpp<0x141>(v);           // row_half_mirror: 8-lane sums
-    v += dpp<0x140>(v);           // row_mirror: 16-lane sums in every lane of a row
-    v += dpp<0x142, 0xA>(v);      // row_bcast15: rows 1 and 3 add lane 15 of rows 0 and 2
-    return v;
-}
-
-// LDS layout of the matvec input (f16): chunk c of 32 values at xh + 20 * c (80 bytes, so the
-// 16-byte reads of 8 consecutive lanes fall in distinct banks). Dword i of a chunk's codes holds
-// codes 8i..8i+7 (nibble j at bits 4j); its x slot (16 bytes) holds the f16 pairs
+// LDS layout of the matvec input (f16): chunk c of 32 values at xh + 20 * c (80 bytes), code dword i
+// of the chunk (codes 8i..8i+7, nibble j at bits 4j) matched by the 16-byte slot i holding
 //   (x0, x4), (x1 / 16, x5 / 16), (x2, x6), (x3 / 16, x7 / 16)      (x of codes 8i..8i+7)
-// after a power-of-two scaling of the whole vector, then the chunk's (Cs, Xs) at byte 64:
-// Cs = 1024 * (sum of the chunk's 32 stored halves), Xs = sum of the chunk's scaled x.
+// after a power-of-two scaling of the whole vector; then the chunk's (Cs, Xs) at byte 64. gsum[g]
+// holds (Cs, Xs) of quantization group g; zero16 is 16 bytes of zeros (the masked B operand).
 constexpr int XH_STRIDE = 20;          // floats per chunk
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
-
-// One 32-code unit, s * sum_j q_j x_j + b * sum_j x_j (in the scaled x units). A nibble masked into
-// the low mantissa bits of the f16 1024.0 is the half 1024 + q (bits 4..7: 1024 + 16 q, met by the
-// x / 16 slots), so one AND-OR builds two operands of v_dot2_f32_f16 and
-// sum (1024 + q) x = Cs + sum q x. Products of halves are exact in the f32 accumulation.
-// (a & m) | c in one instruction; m and c are passed in VGPRs (a VOP3 takes one constant at most).
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-    uint32_t r; asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c)); return r;
-}
-
-// Constants of unit_dot, held in VGPRs for the whole phase.
-struct DotConsts { uint32_t m_lo, m_hi, magic; };   // magic: two halves of 1024.0
-__device__ __forceinline__ DotConsts dot_consts() {
-    DotConsts k;
-    asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(k.m_lo));
-    asm volatile("v_mov_b32 %0, 0x00F000F0" : "=v"(k.m_hi));
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(k.magic));
-    return k;
-}
-
-// One chunk of x in registers.
-struct XChunk { uint4 q[4]; float2 cx; };
-__device__ __forceinline__ XChunk load_x(const float* xc) {
-    XChunk x;
-    const uint4* xq = reinterpret_cast<const uint4*>(xc);
-#pragma unroll
-    for (int i = 0; i < 4; i++) x.q[i] = xq[i];
-    x.cx = *reinterpret_cast<const float2*>(xc + 16);
-    return x;
-}
-
-__device__ __forceinline__ float unit_dot(const uint4 w, uint32_t s16, uint32_t b16, const XChunk& x, const DotConsts& k) {
-    float d0 = 0.0f, d1 = 0.0f;
-    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint4 xv = x.q[i];
-        const uint32_t a = ww[i], a8 = a >> 8;
-        d0 = __builtin_amdgcn_fdot2(as_h2(and_or(a, k.m_lo, k.magic)), as_h2(xv.x), d0, false);
-        d1 = __builtin_amdgcn_fdot2(as_h2(and_or(a, k.m_hi, k.magic)), as_h2(xv.y), d1, false);
-        d0 = __builtin_amdgcn_fdot2(as_h2(and_or(a8, k.m_lo, k.magic)), as_h2(xv.z), d0, false);
-        d1 = __builtin_amdgcn_fdot2(as_h2(and_or(a8, k.m_hi, k.magic)), as_h2(xv.w), d1, false);
-    }
-    const float sc = __uint_as_float(s16 << 16), bi = __uint_as_float(b16 << 16);
-    return sc * ((d0 + d1) - x.cx.x) + bi * x.cx.y;
-}
 
 // Packs xf[0..K) (f32, contiguous; every thread's share already written, max |x| reduced by the
-// caller into gmax) into the f16 layout above. Scale 2^e maps max |x| below 2^14, so every stored
-// half is finite and (for all but values 2^28 below the maximum) normal. Returns 2^-e.
-__device__ __forceinline__ float pack_x16(const float* xf, int K, float gmax, float* xh) {
+// caller into gmax) into the f16 layout above and the group sums for group size 2^gsh. Scale 2^e
+// maps max |x| below 2^14, so every stored half is finite and (for all but values 2^28 below the
+// maximum) normal. Returns 2^-e.
+// LDS of a matvec phase (the attention phase reuses the same memory, so every phase rebuilds it).
+struct MvLds { float* xf; float* xh; float* gsum; float* zero16; float* hown; float* part; };
+
+__device__ __forceinline__ float pack_x16(const float* xf, int K, float gmax, const MvLds& L, int gsh) {
+    float* xh = L.xh; float* gsum = L.gsum;
+    if (threadIdx.x < 4) L.zero16[threadIdx.x] = 0.0f;
     int ex = 0;
     if (gmax > 0.0f && gmax <= 3.0e38f) frexpf(gmax, &ex);
     const int e = min(max(14 - ex, -100), 100);
@@ -312,125 +239,164 @@ __device__ __forceinline__ float pack_x16(const float* xf, int K, float gmax, fl
         if ((t & 3) == 0) *reinterpret_cast<float2*>(xh + c * XH_STRIDE + 16) = float2{1024.0f * cs, xsum};
     }
     __syncthreads();
+    const int cpg = 1 << (gsh - 5);   // chunks per group
+    for (int g = threadIdx.x; g < (K >> gsh); g += MK_THREADS) {
+        float2 s = {0.0f, 0.0f};
+        for (int c = g * cpg; c < (g + 1) * cpg; c++) {
+            const float2 v = *reinterpret_cast<const float2*>(xh + c * XH_STRIDE + 16);
+            s.x += v.x; s.y += v.y;
+        }
+        *reinterpret_cast<float2*>(gsum + 2 * g) = s;
+    }
+    __syncthreads();
     return 1.0f / up;
 }
 
-// Rows [r0, r1) of the phase assigned to this workgroup.
-__device__ __forceinline__ void wg_rows(int rows, int wg, int nwg, int& r0, int& r1) {
-    r0 = (int)((int64_t)rows * wg / nwg); r1 = (int)((int64_t)rows * (wg + 1) / nwg);
+// Sum over each row of 16 lanes (every lane of the row gets it).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<0xB1>(v);            // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);            // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);           // row_half_mirror: 8-lane sums
+    v += dpp<0x140>(v);           // row_mirror: 16-lane sums
+    return v;
 }
 
-// Rows [r0, r1) of the phase assigned to this wave.
-__device__ __forceinline__ void wave_rows(int rows, int wg, int nwg, int wave, bool pairs, int& r0, int& r1) {
-    const int unit = pairs ? 2 : 1;
-    const int n = rows / unit;
-    const int a = (int)((int64_t)n * wg / nwg), b = (int)((int64_t)n * (wg + 1) / nwg);
-    const int m = b - a;
-    const int wa = a + m * wave / MK_WAVES, wb = a + m * (wave + 1) / MK_WAVES;
-    r0 = wa * unit; r1 = wb * unit;
-}
-
-__device__ __forceinline__ int gshift(int gs) { return gs == 32 ? 5 : gs == 64 ? 6 : gs == 128 ? 7 : 8; }
-
-// The phase descriptor is taken by value: held in registers, a row change reads no memory (a load
-// there would make the ring's next memory-counter wait drain every unit in flight).
-__device__ __forceinline__ int pair_units(const MvPhase& p) { return ((p.K >> 5) + 31) >> 5; }
-
-template <bool FULL>
-__device__ __forceinline__ void mv_prefetch_t(const MvPhase& p, int r0, int r1, int lane, Ring& ring) {
-    const int nci = pair_units(p), nch = p.K >> 5, gsh = gshift(p.gs);
-    const int n = ((r1 - r0 + 1) >> 1) * nci;
-    if (n <= 0) return;
-    Cursor c; cursor_pair(p, r0, r1, lane, gsh, c);
+// Streams the wave's scale groups (the first already in the ring), leaving per-tile partial row
+// sums in part[(tile * MK_WAVES + wave) * 16 + row] (LDS) for mv_finish.
+template <int FB>
+__device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const float* gsum, const float* zero16, int wg, int nwg,
+                                       int wave, int lane, Ring<FB>& ring, float* part) {
+    constexpr int GSH = FB == 4 ? 5 : 6;          // log2 of the group size
+    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, wave);
+    const int nfb = g.f1 - g.f0;
+    if (nfb <= 0) return;
+    const int gpr = p.K >> GSH;                   // groups per row
+    const gptr8 base = mv_base<FB>(p, g, lane);
+    const DotConsts kc = dot_consts(__float_as_int(zero16[lane & 3]));   // a zero the compiler cannot fold
+    const int col = lane & 15;
+    f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f};
+    int tile = g.f0 / g.NF, f = g.f0 - tile * g.NF;   // scale group within the tile
+    for (int i = 0; i < nfb; i++) {
+        const gptr8 nxt = base + (int64_t)min(i + 1, nfb - 1) * ((FB + 1) * 1024);   // the last reloads itself
+        const uint4 sbr = ring.u[0];
+        ring.u[0] = ld_stream16(nxt);
+        const float* xb = xh + (lane >> 4) * 4 + f * (4 * FB) * XH_STRIDE;   // this lane's slot of the group's first chunk
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int d = 0; d < MK_DEPTH; d++) {
-        cursor_load<FULL>(c, lane, nch, gsh, ring.code[d], ring.s[d], ring.b[d]);
-        cursor_next<FULL>(p, r1, lane, gsh, nci, d + 1 >= n, c);
+        for (int k = 0; k < FB; k++) {
+            const uint4 unit = ring.u[k + 1];
+            const uint32_t wd[4] = {unit.x, unit.y, unit.z, unit.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                constexpr int CPG = 1 << (GSH - 5);                       // chunks per group
+                const int gcol = (4 * k + j) / CPG;                        // the chunk's group column
+                const float* bp = col == gcol ? xb + (4 * k + j) * XH_STRIDE : zero16;
+                const f16x8_t b = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(bp));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b, acc, 0, 0, 0);
+            }
+            ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
+        }
+        // scales of the 16 groups (groups past the row's last are zero-scaled; their sums may be junk)
+        const int gi = 16 * f + col;
+        const bool real = gi < gpr;
+        const float2 gs2 = *reinterpret_cast<const float2*>(gsum + 2 * (real ? gi : 0));
+        const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float sc = __uint_as_float(sv[r] << 16), bb = __uint_as_float(sv[r] & 0xffff0000u);
+            const float t = sc * (acc[r] - gs2.x) + bb * gs2.y;
+            run[r] += real ? t : 0.0f;
+        }
+        if (f == g.NF - 1 || i == nfb - 1) {     // tile done (or the wave's range): row sums to LDS
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float v = row16_sum(run[r]);
+                if (col == 0) part[(tile * MK_WAVES + wave) * 16 + 4 * (lane >> 4) + r] = v;
+            }
+            run = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (++f == g.NF) { f = 0; tile++; }
     }
-}
-__device__ __forceinline__ bool mv_full(const MvPhase& p) { return ((p.K >> 5) & 31) == 0; }
-__device__ __forceinline__ void mv_prefetch(const MvPhase p, int r0, int r1, int lane, Ring& ring) {
-    if (mv_full(p)) mv_prefetch_t<true>(p, r0, r1, lane, ring);
-    else mv_prefetch_t<false>(p, r0, r1, lane, ring);
 }
 
 enum MvOut { OUT_STORE = 0, OUT_ADD = 1, OUT_GATED = 2, OUT_ARGMAX = 3 };
 
-struct MvResult { float best; int best_idx; };   // wave-uniform
+struct MvResult { float best; int best_idx; };
 
+// Branch-free (part, row) of a concatenated row (bias lookup).
+__device__ __forceinline__ void mv_locate(const MvPhase& p, int vr, int& part, int& row) {
+    const int a = vr >= p.o1 ? 1 : 0, b = vr >= p.o1 + p.o2 ? 1 : 0;
+    part = a + b; row = vr - (a ? p.o1 : 0) - (b ? p.o2 : 0);
+}
 __device__ __forceinline__ float row_bias(const MvPhase& p, int vr) {
+    if (!p.bias[0]) return 0.0f;
     int part, row; mv_locate(p, vr, part, row);
-    return bf16_to_f32(pick3(p.bias, part)[row]);
+    const uint16_t* b = part == 0 ? p.bias[0] : part == 1 ? p.bias[1] : p.bias[2];
+    return bf16_to_f32(b[row]);
 }
 
-// Consumes the wave's units (the first DEPTH already in the ring) and writes row results.
-// Gated phases have even r0 and r1, so a pair is (gate row, up row) of one output.
-// Row results are collected in this wave's LDS slice `ybuf` and written to `out` once, after the
-// last unit: a store between ring loads would hold back every later load's completion (vector
-// memory operations count down in issue order, and an agent-scope store completes only at memory).
-template <int MODE, bool FULL>
-__device__ __forceinline__ MvResult mv_run_t(const MvPhase& p, const float* xh, float unscale, int r0, int r1, int lane, Ring& ring,
-                                             float* out, const float* hown, int hrow0, float* ybuf) {
-    const int nci = pair_units(p), nch = p.K >> 5, gsh = gshift(p.gs);
-    const int n = ((r1 - r0 + 1) >> 1) * nci;
+// Row r of tile tl of this workgroup: the partial sums of the waves whose ranges meet the tile, in
+// wave order.
+__device__ __forceinline__ float tile_row(const float* part, int tl, int r, int nfw, int NF) {
+    float s = 0.0f;
+    for (int w = 0; w < MK_WAVES; w++) {
+        const int a = nfw * w / MK_WAVES, b = nfw * (w + 1) / MK_WAVES;
+        if (a < b && a < (tl + 1) * NF && b > tl * NF) s += part[(tl * MK_WAVES + w) * 16 + r];   // non-empty, meets the tile
+    }
+    return s;
+}
+
+// After every wave's mv_run: combines the partials and writes the phase's outputs (coherent stores
+// for data other workgroups read). ARGMAX returns the workgroup's largest row (lowest index among
+// equals; NaN rows never win) to every thread.
+template <int MODE, int FB>
+__device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, int wg, int nwg, const float* part, float* out,
+                                              const float* hown, float* red, int* redi) {
+    __syncthreads();
+    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
+    const int nfw = g.nt * g.NF;
     MvResult res{-INFINITY, 0x7fffffff};
-    int cpr = r0, cci = 0;                 // consume pointer
-    // load cursor: unit DEPTH, clamped to the last unit n - 1
-    Cursor lc; cursor_pair(p, r0, r1, lane, gsh, lc);
-    for (int k = 0; k < MK_DEPTH && k + 1 < n; k++) cursor_next<FULL>(p, r1, lane, gsh, nci, false, lc);
-    float acc = 0.0f;
-    const DotConsts kc = dot_consts();
-    const bool has_bias = p.bias[0] != nullptr;
-    const float* xl = xh + (lane & 31) * XH_STRIDE;       // this lane's chunk of unit 0 of a pair
-    for (int u = 0; u < n; u += MK_DEPTH) {
-#pragma unroll
-        for (int d = 0; d < MK_DEPTH; d++) {
-            const bool valid = u + d < n;                       // wave-uniform
-            const int ch = (lane & 31) + 32 * cci;
-            float contrib = 0.0f;
-            if (valid) contrib = unit_dot(ring.code[d], ring.s[d], ring.b[d], load_x(FULL ? xl + cci * 32 * XH_STRIDE
-                                          : xh + min(ch, nch - 1) * XH_STRIDE), kc);
-            const bool lane_ok = FULL || ch < nch;     // a missing second row is dropped at the pair's end
-            // next unit for this slot (clamped to the last one: harmless reload, never consumed)
-            cursor_load<FULL>(lc, lane, nch, gsh, ring.code[d], ring.s[d], ring.b[d]);
-            cursor_next<FULL>(p, r1, lane, gsh, nci, u + d + MK_DEPTH + 1 >= n, lc);
-            if (valid) {
-                acc += FULL ? contrib : (lane_ok ? contrib : 0.0f);
-                if (++cci == nci) {
-                    const float t = half_wave_sum(acc);
-                    acc = 0.0f;
-                    const bool two = cpr + 1 < r1;
-                    float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 31)) * unscale;
-                    float v1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 63)) * unscale;
-                    if (has_bias) { v0 += row_bias(p, cpr); if (two) v1 += row_bias(p, cpr + 1); }
-                    if (MODE == OUT_GATED) {
-                        if (lane == 0) ybuf[(cpr - r0) >> 1] = (v0 / (1.0f + expf(-v0))) * v1;
-                    } else {
-                        if (lane < 2 && (lane == 0 || two)) ybuf[cpr - r0 + lane] = lane ? v1 : v0;
-                        if (MODE == OUT_ARGMAX) {
-                            if (v0 > res.best) { res.best = v0; res.best_idx = cpr; }
-                            if (two && v1 > res.best) { res.best = v1; res.best_idx = cpr + 1; }
-                        }
-                    }
-                    cci = 0; cpr += 2;
-                }
+    if (MODE == OUT_GATED) {
+        for (int i = threadIdx.x; i < g.nt * 8; i += MK_THREADS) {
+            const int tl = i >> 3, j = i & 7, o = 8 * (g.t0 + tl) + j;
+            if (o < p.o1) {
+                const float gv = tile_row(part, tl, j, nfw, g.NF) * unscale;
+                const float uv = tile_row(part, tl, j + 8, nfw, g.NF) * unscale;
+                st_ag(out + o, (gv / (1.0f + expf(-gv))) * uv);
             }
         }
+        return res;
     }
-    __builtin_amdgcn_wave_barrier();
-    const int o0 = MODE == OUT_GATED ? r0 >> 1 : r0, no = MODE == OUT_GATED ? (r1 - r0) >> 1 : r1 - r0;
-    for (int i = lane; i < no; i += 64) {
-        const float v = ybuf[i];
-        if (MODE == OUT_ARGMAX) out[o0 + i] = v;   // logits: read by the host after the launch
-        else st_ag(out + o0 + i, MODE == OUT_ADD ? hown[o0 + i - hrow0] + v : v);
+    for (int i = threadIdx.x; i < g.nt * 16; i += MK_THREADS) {
+        const int row = 16 * g.t0 + i;
+        if (row >= p.rows) break;
+        const float v = tile_row(part, i >> 4, i & 15, nfw, g.NF) * unscale + row_bias(p, row);
+        if (MODE == OUT_STORE) st_ag(out + row, v);
+        else if (MODE == OUT_ADD) st_ag(out + row, hown[i] + v);
+        else {
+            out[row] = v;   // logits: read by the host after the launch
+            if (v > res.best) { res.best = v; res.best_idx = row; }
+        }
+    }
+    if (MODE == OUT_ARGMAX) {
+        // workgroup reduction: larger value, then lower index
+        float m = res.best; int idx = res.best_idx;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float m2 = __shfl_xor(m, o, 64); const int i2 = __shfl_xor(idx, o, 64);
+            if (m2 > m || (m2 == m && i2 < idx)) { m = m2; idx = i2; }
+        }
+        if ((threadIdx.x & 63) == 0) { red[threadIdx.x >> 6] = m; redi[threadIdx.x >> 6] = idx; }
+        __syncthreads();
+        res.best = -INFINITY; res.best_idx = 0x7fffffff;
+        for (int w = 0; w < MK_WAVES; w++)
+            if (red[w] > res.best || (red[w] == res.best && redi[w] < res.best_idx)) { res.best = red[w]; res.best_idx = redi[w]; }
     }
     return res;
-}
-template <int MODE>
-__device__ __forceinline__ MvResult mv_run(const MvPhase p, const float* xh, float unscale, int r0, int r1, int lane, Ring& ring,
-                                           float* ybuf, float* out, const float* hown = nullptr, int hrow0 = 0) {
-    if (mv_full(p)) return mv_run_t<MODE, true>(p, xh, unscale, r0, r1, lane, ring, out, hown, hrow0, ybuf);
-    return mv_run_t<MODE, false>(p, xh, unscale, r0, r1, lane, ring, out, hown, hrow0, ybuf);
 }
 
 // Loads src[0..K) (written by other workgroups) into xf (f32, contiguous): 8 coherent 16-byte loads
@@ -469,10 +435,11 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     return m;
 }
 
+
 // x := RMSNorm(src) * w, packed to the f16 matvec layout (every workgroup computes the same
 // values). Returns the unscale factor of the packing.
-__device__ __forceinline__ float norm_to_lds(const float* src, const float* w, int K, float eps, float* xf, float* xh, float* red) {
-    const float ss = wave_sum(fetch_to_lds(src, K, xf).x);
+__device__ __forceinline__ float norm_to_lds(const float* src, const float* w, int K, float eps, const MvLds& L, int gsh, float* red) {
+    const float ss = wave_sum(fetch_to_lds(src, K, L.xf).x);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
@@ -480,25 +447,25 @@ __device__ __forceinline__ float norm_to_lds(const float* src, const float* w, i
     const float inv = 1.0f / sqrtf(tot / (float)K + eps);
     float mx = 0.0f;
     for (int i = threadIdx.x * 4; i < K; i += MK_THREADS * 4) {
-        float4 v = *reinterpret_cast<float4*>(xf + i);
+        float4 v = *reinterpret_cast<float4*>(L.xf + i);
         const float4 ww = *reinterpret_cast<const float4*>(w + i);
         v.x = v.x * inv * ww.x; v.y = v.y * inv * ww.y; v.z = v.z * inv * ww.z; v.w = v.w * inv * ww.w;
-        *reinterpret_cast<float4*>(xf + i) = v;
+        *reinterpret_cast<float4*>(L.xf + i) = v;
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
-    return pack_x16(xf, K, block_max(mx, red), xh);
+    return pack_x16(L.xf, K, block_max(mx, red), L, gsh);
 }
 
 // x := src packed to the f16 matvec layout, plus this workgroup's residual rows h[row0 .. row1)
 // into hown (for the accumulate epilogue, so no row needs its own round trip).
-__device__ __forceinline__ float copy_to_lds(const float* src, int K, float* xf, float* xh, const float* h, int H, int row0,
-                                             int row1, float* hown, float* red) {
+__device__ __forceinline__ float copy_to_lds(const float* src, int K, const MvLds& L, int gsh, const float* h, int H, int row0,
+                                             int row1, float* red) {
     const int n = row1 - row0;
     float hv = 0.0f;
     if ((int)threadIdx.x < n) hv = ld_coh1(h, row0 + threadIdx.x, H);
-    const float mx = fetch_to_lds(src, K, xf).y;
-    if ((int)threadIdx.x < n) hown[threadIdx.x] = hv;
-    return pack_x16(xf, K, block_max(mx, red), xh);
+    const float mx = fetch_to_lds(src, K, L.xf).y;
+    if ((int)threadIdx.x < n) L.hown[threadIdx.x] = hv;
+    return pack_x16(L.xf, K, block_max(mx, red), L, gsh);
 }
 
 // ------------------------------------------------------------------------------- attention phase
@@ -569,7 +536,8 @@ __device__ __forceinline__ float head_norm_rope(float v, int i, const float* nw,
 
 // ------------------------------------------------------------------------------- the kernel
 // MAXG: the largest query-head group the attention phase's registers hold (4 or 8).
-template <int MAXG>
+// FB: code blocks per scale group (4: group size 32, 8: group size 64).
+template <int MAXG, int FB>
 __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     __shared__ float red[64];
@@ -579,11 +547,15 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
     const int pos = *a.dpos, L = pos + 1;
     const int H = a.H, D = 128, nH = a.nH, nKV = a.nKV, G = nH / nKV;
     const int Kmax = std::max(H, std::max(a.I, nH * D));
-    float* xf = lds;                              // matvec input, f32 staging (Kmax floats)
-    float* xh = lds + Kmax;                       // matvec input, f16 layout (Kmax / 32 chunks)
-    float* hown = xh + (Kmax >> 5) * XH_STRIDE;   // this workgroup's residual rows (up to MK_HOWN)
-    float* ybuf = hown + MK_HOWN + wave * MK_YCAP; // this wave's row results
-    Ring ring;
+    MvLds ml;
+    ml.xf = lds;                                  // matvec input, f32 staging (Kmax floats)
+    ml.xh = ml.xf + Kmax;                         // matvec input, f16 layout (Kmax / 32 chunks)
+    ml.gsum = ml.xh + (Kmax >> 5) * XH_STRIDE;    // per-group sums (Kmax / 32 float2 at most)
+    ml.zero16 = ml.gsum + (Kmax >> 5) * 2;        // 16 bytes of zeros
+    ml.hown = ml.zero16 + 4;                      // this workgroup's residual rows (up to MK_HOWN)
+    ml.part = ml.hown + MK_HOWN;                  // per-tile partial row sums [MK_TPW][waves][16]
+    __shared__ int redi[MK_WAVES];
+    Ring<FB> ring;
     KVPrefetch kvpf;
 
     // embedding row of hist[pos] -> h (each workgroup writes a slice), and the first prefetch
@@ -600,10 +572,8 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
     }
     unsigned epoch = 0;
     prof_mark(a.prof, 0);
-    int r0, r1;
     prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
-    wave_rows(a.layers[0].qkv.rows, wg, nwg, wave, false, r0, r1);
-    mv_prefetch(a.layers[0].qkv, r0, r1, lane, ring);
+    mv_prefetch<FB>(a.layers[0].qkv, wg, nwg, wave, lane, ring);
     grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
 
     const int nsplit = nwg / nKV;
@@ -611,10 +581,10 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         const LayerDev& ly = a.layers[li];
         // ---- A: q|k|v
         {
-            const float us = norm_to_lds(a.h, ly.in_norm, H, a.eps, xf, xh, red);
+            const float us = norm_to_lds(a.h, ly.in_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 0);
-            wave_rows(ly.qkv.rows, wg, nwg, wave, false, r0, r1);
-            mv_run<OUT_STORE>(ly.qkv, xh, us, r0, r1, lane, ring, ybuf, a.qkv);
+            mv_run<FB>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkv, nullptr, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
         // prefetch this workgroup's K/V rows (positions < pos are final)
@@ -797,64 +767,55 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             }
         }
         prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
-        wave_rows(ly.o.rows, wg, nwg, wave, false, r0, r1);
-        mv_prefetch(ly.o, r0, r1, lane, ring);
+        mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
         grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- C: o_proj, h += W_o attn
         {
-            int g0, g1; wg_rows(ly.o.rows, wg, nwg, g0, g1);
-            const float us = copy_to_lds(a.attn, nH * D, xf, xh, a.h, H, g0, g1, hown, red);
+            const MvGeom<FB> gg = mv_geom<FB>(ly.o, wg, nwg, 0);
+            const float us = copy_to_lds(a.attn, nH * D, ml, FB == 4 ? 5 : 6, a.h, H, 16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 4);
-            mv_run<OUT_ADD>(ly.o, xh, us, r0, r1, lane, ring, ybuf, a.h, hown, g0);
+            mv_run<FB>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.h, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
-        wave_rows(ly.gu.rows, wg, nwg, wave, true, r0, r1);
-        mv_prefetch(ly.gu, r0, r1, lane, ring);
+        mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
         grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- D: gate|up with SiLU
         {
-            const float us = norm_to_lds(a.h, ly.post_norm, H, a.eps, xf, xh, red);
+            const float us = norm_to_lds(a.h, ly.post_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 5);
-            mv_run<OUT_GATED>(ly.gu, xh, us, r0, r1, lane, ring, ybuf, a.mlp);
+            mv_run<FB>(ly.gu, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_finish<OUT_GATED, FB>(ly.gu, us, wg, nwg, ml.part, a.mlp, nullptr, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
-        wave_rows(ly.down.rows, wg, nwg, wave, false, r0, r1);
-        mv_prefetch(ly.down, r0, r1, lane, ring);
+        mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
         grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- E: down, h += W_d mlp
         {
-            int g0, g1; wg_rows(ly.down.rows, wg, nwg, g0, g1);
-            const float us = copy_to_lds(a.mlp, a.I, xf, xh, a.h, H, g0, g1, hown, red);
+            const MvGeom<FB> gg = mv_geom<FB>(ly.down, wg, nwg, 0);
+            const float us = copy_to_lds(a.mlp, a.I, ml, FB == 4 ? 5 : 6, a.h, H, 16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 6);
-            mv_run<OUT_ADD>(ly.down, xh, us, r0, r1, lane, ring, ybuf, a.h, hown, g0);
+            mv_run<FB>(ly.down, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.h, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
-        if (li + 1 < a.L) {
-            wave_rows(a.layers[li + 1].qkv.rows, wg, nwg, wave, false, r0, r1);
-            mv_prefetch(a.layers[li + 1].qkv, r0, r1, lane, ring);
-        } else {
-            wave_rows(a.head.rows, wg, nwg, wave, false, r0, r1);
-            mv_prefetch(a.head, r0, r1, lane, ring);
-        }
+        if (li + 1 < a.L) mv_prefetch<FB>(a.layers[li + 1].qkv, wg, nwg, wave, lane, ring);
+        else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
         grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
     }
 
     // ---- lm_head with the final norm, logits and the greedy token
-    const float us = norm_to_lds(a.h, a.final_norm, H, a.eps, xf, xh, red);
-    const MvResult best = mv_run<OUT_ARGMAX>(a.head, xh, us, r0, r1, lane, ring, ybuf, a.logits);
+    const float us = norm_to_lds(a.h, a.final_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
+    mv_run<FB>(a.head, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+    const MvResult best = mv_finish<OUT_ARGMAX, FB>(a.head, us, wg, nwg, ml.part, a.logits, nullptr, red, redi);
     prof_mark(a.prof, 2 * epoch);
     __shared__ float bv[MK_WAVES];
     __shared__ int bi[MK_WAVES];
-    if (lane == 0) { bv[wave] = best.best; bi[wave] = best.best_idx; }
-    __syncthreads();
     if (tid == 0) {
-        float m = -INFINITY; int idx = 0x7fffffff;
-        for (int w = 0; w < MK_WAVES; w++)   // waves hold ascending row ranges
-            if (bv[w] > m) { m = bv[w]; idx = bi[w]; }
-        st_ag(a.wg_best + wg, m); st_ag(a.wg_idx + wg, idx);
+        st_ag(a.wg_best + wg, best.best); st_ag(a.wg_idx + wg, best.best_idx);
         __builtin_amdgcn_s_waitcnt(0);
         const unsigned done = add_ag(a.head_done, 1u);
         flag = done == (unsigned)nwg - 1;
@@ -888,29 +849,92 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
     *a.dpos = pos + 1;
 }
 
+// ------------------------------------------------------------------------------- repack (load time)
+// Virtual row vr of tile t, row r16 (0..15) -> (part, row), or part -1 past the matrix.
+__device__ __forceinline__ void dpack_row(const DPackSrc& s, int t, int r16, int& part, int& row) {
+    if (s.gated) {
+        part = r16 < 8 ? 0 : 1; row = 8 * t + (r16 & 7);
+        if (row >= s.o1) part = -1;
+        return;
+    }
+    const int vr = 16 * t + r16;
+    if (vr >= s.rows) { part = -1; row = 0; return; }
+    const int a = vr >= s.o1 ? 1 : 0, b = vr >= s.o1 + s.o2 ? 1 : 0;
+    part = a + b; row = vr - (a ? s.o1 : 0) - (b ? s.o2 : 0);
+}
+
+// One thread per output dword of the interleaved stream.
+__global__ void dpack_kernel(DPackSrc s, uint32_t* out, int tiles) {
+    const int KBT = s.K >> 7, gpr = s.K / s.gs, FB = s.gs >> 3, NF = (KBT + FB - 1) / FB, dpr = s.K >> 3;
+    const int64_t n = (int64_t)tiles * NF * (FB + 1) * 256;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int dw = (int)(i & 3), l = (int)((i >> 2) & 63);
+        const int64_t blk = i >> 8;
+        const int pos = (int)(blk % (FB + 1));
+        const int64_t tf = blk / (FB + 1);
+        const int t = (int)(tf / NF), f = (int)(tf % NF);
+        uint32_t v = 0;
+        if (pos == 0) {                       // scales of rows 4 (l >> 4) + dw, group 16 f + (l & 15)
+            const int g = 16 * f + (l & 15);
+            int part, row; dpack_row(s, t, 4 * (l >> 4) + dw, part, row);
+            if (part >= 0 && g < gpr) {
+                const uint16_t* sc = part == 0 ? s.s[0] : part == 1 ? s.s[1] : s.s[2];
+                const uint16_t* bi = part == 0 ? s.b[0] : part == 1 ? s.b[1] : s.b[2];
+                v = (uint32_t)sc[(int64_t)row * gpr + g] | ((uint32_t)bi[(int64_t)row * gpr + g] << 16);
+            }
+        } else {                              // code block kb: row l & 15, dword 16 kb + 4 dw + (l >> 4)
+            const int kb = f * FB + pos - 1;
+            int part, row; dpack_row(s, t, l & 15, part, row);
+            if (part >= 0 && kb < KBT) {
+                const uint32_t* src = reinterpret_cast<const uint32_t*>(part == 0 ? s.w[0] : part == 1 ? s.w[1] : s.w[2]);
+                v = src[(int64_t)row * dpr + 16 * kb + 4 * dw + (l >> 4)];
+            }
+        }
+        out[i] = v;
+    }
+}
+
+int dpack_tiles(const DPackSrc& s) { return s.gated ? (s.o1 + 7) / 8 : (s.rows + 15) / 16; }
+size_t dpack_bytes(const DPackSrc& s) {
+    const int FB = s.gs >> 3, NF = ((s.K >> 7) + FB - 1) / FB;
+    return (size_t)dpack_tiles(s) * NF * (FB + 1) * 1024;
+}
+hipError_t launch_dpack(const DPackSrc& s, uint8_t* out, hipStream_t st) {
+    hipLaunchKernelGGL(dpack_kernel, dim3(2048), dim3(256), 0, st, s, reinterpret_cast<uint32_t*>(out), dpack_tiles(s));
+    return hipGetLastError();
+}
+
 size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split) {
     const int G = a.nH / a.nKV;
     const size_t kmax = (size_t)std::max(a.H, std::max(a.I, a.nH * 128));
-    size_t mv = (kmax + kmax / 32 * XH_STRIDE + MK_HOWN + MK_WAVES * MK_YCAP) * 4;
+    size_t mv = (kmax + kmax / 32 * (XH_STRIDE + 2) + 4 + MK_HOWN + MK_TPW * MK_WAVES * 16) * 4;
     size_t att = (size_t)(MK_MAXG * 128 + 256 + 512) * 4 + (size_t)G * max_keys_per_split * 4 + 2 * MK_MAXG * 4 +
                  (size_t)std::max(MK_WAVES * G * 128, 2 * MK_MAXG * 64) * 4;
     return std::max(mv, att);
 }
 
+// Every layer's matrices share the group size (checked at setup); a.head.gs selects the variant.
 hipError_t launch_decode_step(const MegaArgs& a, int nwg, size_t lds, hipStream_t s) {
-    if (a.nH / a.nKV <= 4) hipLaunchKernelGGL(decode_step_kernel<4>, dim3(nwg), dim3(MK_THREADS), lds, s, a);
-    else hipLaunchKernelGGL(decode_step_kernel<8>, dim3(nwg), dim3(MK_THREADS), lds, s, a);
+    const bool g4 = a.nH / a.nKV <= 4, fb4 = a.head.gs == 32;
+    if (g4 && fb4) hipLaunchKernelGGL((decode_step_kernel<4, 4>), dim3(nwg), dim3(MK_THREADS), lds, s, a);
+    else if (g4) hipLaunchKernelGGL((decode_step_kernel<4, 8>), dim3(nwg), dim3(MK_THREADS), lds, s, a);
+    else if (fb4) hipLaunchKernelGGL((decode_step_kernel<8, 4>), dim3(nwg), dim3(MK_THREADS), lds, s, a);
+    else hipLaunchKernelGGL((decode_step_kernel<8, 8>), dim3(nwg), dim3(MK_THREADS), lds, s, a);
     return hipGetLastError();
 }
 
 hipError_t mega_set_lds_limit(size_t lds) {
-    hipError_t e = hipFuncSetAttribute((const void*)decode_step_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void*)decode_step_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const void* k[4] = {(const void*)decode_step_kernel<4, 4>, (const void*)decode_step_kernel<4, 8>,
+                        (const void*)decode_step_kernel<8, 4>, (const void*)decode_step_kernel<8, 8>};
+    for (const void* f : k) {
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 int mega_threads() { return MK_THREADS; }
-int mega_wave_row_cap() { return MK_YCAP; }
+int mega_tiles_per_wg_cap() { return MK_TPW; }
 int mega_wg_row_cap() { return MK_HOWN; }
 
 }  // namespace mlxr

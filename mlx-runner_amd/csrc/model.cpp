@@ -327,7 +327,7 @@ void sparse_clamp(mlxr_sparse_cfg& c) {   // SparseAttention.init (SparseAttenti
 static int mega_setup(Model* m) {
     const Config& c = m->cfg;
     auto no = [&](const std::string& why) { m->mega_ok = false; m->mega_reason = why; return MLXR_OK; };
-    auto four_bf16 = [](const Lin& l) { return l.bits == 4 && l.st == 0 && l.K % 32 == 0; };
+    auto four_bf16 = [&](const Lin& l) { return l.bits == 4 && l.st == 0 && l.K % 128 == 0 && (l.gs == 32 || l.gs == 64) && l.gs == m->head.gs; };
     if (!four_bf16(m->embed) || !four_bf16(m->head)) return no("embedding / lm_head not 4-bit bf16");
     for (auto& ly : m->layers)
         for (const Lin* l : {&ly.q, &ly.k, &ly.v, &ly.o, &ly.gate, &ly.up, &ly.down})
@@ -341,25 +341,35 @@ static int mega_setup(Model* m) {
     const int nsplit = nwg / c.nKV;
     const int max_keys = (m->max_seq + nsplit - 1) / nsplit;
     {
-        const int waves = nwg * (mega_threads() / 64);
-        const int rmax = std::max({c.V, (c.nH + 2 * c.nKV) * c.D, 2 * c.I, c.H});
-        if ((rmax + waves - 1) / waves + 2 > mega_wave_row_cap()) return no("too many rows per wave");
-        if ((c.H + nwg - 1) / nwg + 1 > mega_wg_row_cap()) return no("too many residual rows per workgroup");
+        const int tmax = std::max({(c.V + 15) / 16, ((c.nH + 2 * c.nKV) * c.D + 15) / 16, (c.I + 7) / 8, (c.H + 15) / 16});
+        if ((tmax + nwg - 1) / nwg > mega_tiles_per_wg_cap()) return no("too many row tiles per workgroup");
+        if (16 * ((c.H + 15) / 16 + nwg - 1) / nwg > mega_wg_row_cap()) return no("too many residual rows per workgroup");
+        for (auto& ly : m->layers)
+            if (ly.q.gs != ly.k.gs || ly.q.gs != ly.v.gs || ly.gate.gs != ly.up.gs) return no("mixed group sizes in a fused phase");
     }
     MegaArgs& a = m->mega;
     a.H = c.H; a.nH = c.nH; a.nKV = c.nKV; a.I = c.I; a.rot_dim = c.rot_dim; a.traditional = c.traditional;
     const size_t lds = mega_lds_bytes(a, max_keys);
     if (lds > 150 * 1024) return no("LDS need " + std::to_string(lds >> 10) + " KiB");
     if (mega_set_lds_limit(lds) != hipSuccess) return no("LDS attribute");
-    auto desc = [](const Lin* parts, int n, bool gated) {
+    // each phase's matrices, repacked once into the decode tile layout (a second copy of the weights)
+    int rc = MLXR_OK;
+    auto desc = [&](const Lin* parts, int n, bool gated) {
         MvPhaseDesc d{};
+        DPackSrc src{};
         for (int i = 0; i < 3; i++) {
             const Lin& l = parts[i < n ? i : n - 1];
-            d.w[i] = l.m.w; d.s[i] = l.m.s; d.b[i] = l.m.b; d.bias[i] = l.m.bias;
+            src.w[i] = reinterpret_cast<const uint8_t*>(l.m.w); src.s[i] = l.m.s; src.b[i] = l.m.b;
+            d.bias[i] = l.m.bias;
         }
-        d.o1 = parts[0].O; d.o2 = n > 1 ? parts[1].O : 0;
+        d.o1 = src.o1 = parts[0].O; d.o2 = src.o2 = n > 1 ? parts[1].O : 0;
         int rows = 0; for (int i = 0; i < n; i++) rows += parts[i].O;
-        d.rows = rows; d.K = parts[0].K; d.gs = parts[0].gs; d.gated = gated ? 1 : 0;
+        d.rows = src.rows = rows; d.K = src.K = parts[0].K; d.gs = src.gs = parts[0].gs; d.gated = src.gated = gated ? 1 : 0;
+        d.tiles = dpack_tiles(src);
+        uint8_t* code = nullptr;
+        if (rc == MLXR_OK) rc = dalloc(m, &code, dpack_bytes(src));
+        if (rc == MLXR_OK && launch_dpack(src, code, m->stream) != hipSuccess) rc = set_error(MLXR_E_GPU, "repack launch");
+        d.code = code;
         return d;
     };
     std::vector<LayerDev> host(c.L);
@@ -368,14 +378,16 @@ static int mega_setup(Model* m) {
         const Lin qkv[3] = {ly.q, ly.k, ly.v}, gu[2] = {ly.gate, ly.up};
         LayerDev& d = host[i];
         d.qkv = desc(qkv, 3, false); d.o = desc(&ly.o, 1, false); d.gu = desc(gu, 2, true); d.down = desc(&ly.down, 1, false);
+        if (rc) return rc;
         d.in_norm = ly.in_norm; d.post_norm = ly.post_norm; d.q_norm = ly.q_norm; d.k_norm = ly.k_norm;
         d.kc = ly.kc; d.vc = ly.vc;
     }
-    int rc;
     if ((rc = dalloc(m, &m->mega_layers, c.L))) return rc;
     HIPCHECK(hipMemcpy(m->mega_layers, host.data(), sizeof(LayerDev) * c.L, hipMemcpyHostToDevice));
     a.layers = m->mega_layers; a.L = c.L;
     a.head = desc(&m->head, 1, false);
+    if (rc) return rc;
+    HIPCHECK(hipStreamSynchronize(m->stream));
     a.embed_w = m->embed.m.w; a.embed_s = m->embed.m.s; a.embed_b = m->embed.m.b; a.embed_gs = m->embed.gs;
     a.final_norm = m->final_norm; a.inv_freq = m->inv_freq;
     a.eps = c.eps; a.scale = c.query_scale * c.rope_attention_factor * c.rope_attention_factor;
