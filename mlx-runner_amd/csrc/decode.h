@@ -28,15 +28,15 @@ struct LayerDev {
     uint16_t* kc; uint16_t* vc;
 };
 
-// Grid-barrier state: per-XCD arrival counters (one 128-byte line each), the count of XCDs done,
-// and the release epoch every workgroup polls. Monotonic within a launch; reset by the last
-// workgroup to leave the kernel.
+// Grid-barrier state: every workgroup's arrival number in its own slot, and the launch count that
+// makes arrival numbers unique across launches (launch n uses n * 1024 + phase), so no slot is ever
+// reset. Compared with wrap-safe signed differences.
+constexpr int MEGA_MAX_WG = 1024;
 struct MegaSync {
-    unsigned count;      // XCD groups arrived
-    unsigned abort;      // set when a barrier wait expires
-    unsigned gen;        // released epoch
-    unsigned pad0[29];
-    unsigned xcd[8][32]; // arrivals per XCD group (blockIdx % 8)
+    unsigned launch;      // launches completed
+    unsigned abort;       // set when a barrier wait expires
+    unsigned pad0[30];
+    unsigned flag[MEGA_MAX_WG];
 };
 
 struct MegaArgs {
@@ -52,6 +52,7 @@ struct MegaArgs {
     float* wg_best; int* wg_idx;
     unsigned* kv_done; unsigned* head_done;
     MegaSync* sync;
+    int* abort_host;                  // host-mapped copy of sync->abort (read by the host after a step)
     int select;                       // 1: greedy token selection fused (writes hist / ring, advances *dpos)
     int* ring_tok; int* ring_status; int ring_mask;
     unsigned long long* prof;         // optional: per workgroup, wall-clock at every phase start / end

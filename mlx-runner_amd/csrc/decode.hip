@@ -31,7 +31,6 @@ namespace mlxr {
 
 constexpr int MK_THREADS = 512;
 constexpr int MK_WAVES = MK_THREADS / 64;
-constexpr int MK_KV_PF = 4;          // attention: K/V rounds (32 keys each) prefetched per thread
 constexpr int MK_MAXG = 8;
 constexpr int MK_HOWN = 1024;        // residual rows of one workgroup in an accumulate phase (max)
 constexpr int MK_TPW = 64;           // 16-row tiles of one workgroup in a matvec phase (max)
@@ -69,34 +68,35 @@ __device__ __forceinline__ unsigned add_ag(unsigned* p, unsigned v) {
 }
 
 // ------------------------------------------------------------------------------- grid barrier
-// Split barrier. `arrive`: every wave waits for its own stores to complete, then one thread counts
-// the workgroup into its XCD group's counter; the last of a group counts the group, and the last
-// group publishes the epoch. The caller then issues its next-phase loads, and `wait` polls the
-// epoch. (1.9 us measured for 256 workgroups, against ~14 us with agent-scope fences.)
-// An expired wait sets `abort`, which every later wait honours, so every wave reaches the end.
+// Split barrier. `arrive`: every wave waits for its own stores to complete, then one thread stores
+// the workgroup's arrival number e into its slot (no read-modify-write round trip). The caller then
+// issues its next-phase loads, and `wait` has one wave read every slot (4 per lane, coherent) until
+// all hold e or later. An expired wait sets `abort` (device and host copies), which every later
+// wait honours, so every wave reaches the end of the kernel.
 __device__ __forceinline__ void prof_mark(unsigned long long* prof, int ev) {
     if (prof && threadIdx.x == 0 && ev < MEGA_PROF_EVENTS) prof[(size_t)blockIdx.x * MEGA_PROF_EVENTS + ev] = wall_clock64();
 }
 
-__device__ __forceinline__ void grid_arrive(MegaSync* sync, unsigned epoch) {
+__device__ __forceinline__ void grid_arrive(MegaSync* sync, unsigned e) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const int x = blockIdx.x & 7, nwg = gridDim.x;
-        const unsigned per = (unsigned)((nwg - x + 7) / 8), groups = nwg < 8 ? (unsigned)nwg : 8u;
-        if (add_ag(&sync->xcd[x][0], 1u) + 1 == epoch * per)
-            if (add_ag(&sync->count, 1u) + 1 == epoch * groups)
-                __hip_atomic_store(&sync->gen, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (threadIdx.x == 0) __hip_atomic_store(&sync->flag[blockIdx.x], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void grid_wait(MegaSync* sync, unsigned epoch) {
-    if (threadIdx.x == 0) {
+__device__ __forceinline__ void grid_wait(MegaSync* sync, unsigned e, int* abort_host) {
+    if (threadIdx.x < 64) {
+        const int nwg = gridDim.x, lane = threadIdx.x;
         unsigned spins = 0;
-        while (ld_ag(&sync->gen) < epoch) {
+        for (;;) {
+            bool ok = true;
+            for (int w = lane; w < nwg; w += 64) ok = ok && (int)(ld_ag(&sync->flag[w]) - e) >= 0;
+            if (__all(ok)) break;
             if (ld_ag(&sync->abort)) break;
             __builtin_amdgcn_s_sleep(1);
-            if (++spins > (1u << 21)) {   // far beyond any phase: let every wave run to the end instead
-                __hip_atomic_store(&sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (++spins > (1u << 20)) {   // far beyond any phase: let every wave run to the end instead
+                if (lane == 0) {
+                    __hip_atomic_store(&sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(abort_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
                 break;
             }
         }
@@ -172,7 +172,11 @@ __device__ __forceinline__ gptr8 mv_base(const MvPhase& p, const MvGeom<FB>& g, 
 template <int FB>
 __device__ __forceinline__ void mv_prefetch(const MvPhase p, int wg, int nwg, int wave, int lane, Ring<FB>& ring) {
     const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, wave);
-    if (g.f1 <= g.f0) return;
+    if (g.f1 <= g.f0) {   // every path defines the ring, so no earlier value stays live across phases
+#pragma unroll
+        for (int d = 0; d <= FB; d++) ring.u[d] = uint4{0u, 0u, 0u, 0u};
+        return;
+    }
     const gptr8 b = mv_base<FB>(p, g, lane);
 #pragma unroll
     for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
@@ -401,7 +405,7 @@ __device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, i
 
 // Loads src[0..K) (written by other workgroups) into xf (f32, contiguous): 8 coherent 16-byte loads
 // per thread in flight per batch; returns this thread's sum of squares and max |x|.
-constexpr int MK_LDB = 8;
+constexpr int MK_LDB = 4;
 __device__ __forceinline__ float2 fetch_to_lds(const float* src, int K, float* xf) {
     float ss = 0.0f, mx = 0.0f;
     const int K4 = K >> 2;
@@ -469,7 +473,10 @@ __device__ __forceinline__ float copy_to_lds(const float* src, int K, const MvLd
 }
 
 // ------------------------------------------------------------------------------- attention phase
-struct KVPrefetch { uint4 k[MK_KV_PF]; uint4 v[MK_KV_PF]; };
+// K and V of one chunk of 128 keys held in registers: k[db] is the lane's A-operand slice of the
+// wave's 16 keys (dims 32 db + 8 (lane >> 4) .. +8 of key 16 wave + (lane & 15)); v[r] is the
+// thread's P.V slice (dims 4 (tid & 31) .. +4 of key 8 (tid >> 5) + r).
+struct KVPrefetch { uint4 k[4]; uint2 v[8]; };
 
 // Key range of attention item (kvh, split): [n0, n1) of the L = pos + 1 keys.
 __device__ __forceinline__ void att_range(int L, int nsplit, int split, int& n0, int& n1) {
@@ -477,25 +484,47 @@ __device__ __forceinline__ void att_range(int L, int nsplit, int split, int& n0,
     n0 = min(L, split * c); n1 = min(L, n0 + c);
 }
 
-__device__ __forceinline__ void att_prefetch(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int n1, KVPrefetch& pf) {
-    const int t = threadIdx.x, slot = t >> 4, part = t & 15;   // 16 lanes per key row, 32 keys per round
+// Loads chunk c of keys [n0, nf) (nf: the first key not yet final in the cache; keys past it are
+// clamped to a final row and replaced or masked by the caller).
+// Every path defines the registers, so no earlier value stays live across phases.
+__device__ __forceinline__ void att_prefetch_k(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int nf, int c, KVPrefetch& pf) {
+    if (nf <= n0) {
 #pragma unroll
-    for (int r = 0; r < MK_KV_PF; r++) {
-        const int j = n0 + r * 32 + slot;
-        if (j < n1) {
-            const int64_t row = kv_row(a.pt, a.nKV, kvh, j) * 128 + part * 8;
-            pf.k[r] = ld_stream16((gptr8)(ly.kc + row));
-            pf.v[r] = ld_stream16((gptr8)(ly.vc + row));
-        }
+        for (int db = 0; db < 4; db++) pf.k[db] = uint4{0u, 0u, 0u, 0u};
+        return;
+    }
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int kb = n0 + 128 * c + 16 * wave;            // the wave's 16 keys span at most two pages
+    const int jf = min(kb, nf - 1), jl = min(kb + 15, nf - 1);
+    const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = a.pt[pg0], e1 = a.pt[jl >> MLXR_PAGE_SHIFT];
+    const int jk = min(kb + (lane & 15), nf - 1);
+    const int64_t rk = ((int64_t)(((jk >> MLXR_PAGE_SHIFT) == pg0 ? e0 : e1) * a.nKV + kvh) * MLXR_PAGE + (jk & (MLXR_PAGE - 1))) * 128 +
+                       8 * (lane >> 4);
+#pragma unroll
+    for (int db = 0; db < 4; db++) pf.k[db] = ld_stream16((gptr8)(ly.kc + rk + 32 * db));
+}
+__device__ __forceinline__ void att_prefetch_v(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int nf, int c, KVPrefetch& pf) {
+    if (nf <= n0) {
+#pragma unroll
+        for (int r = 0; r < 8; r++) pf.v[r] = uint2{0u, 0u};
+        return;
+    }
+    const int t = threadIdx.x;
+    const int kb = n0 + 128 * c + 8 * (t >> 5);          // the thread's 8 keys span at most two pages
+    const int jf = min(kb, nf - 1), jl = min(kb + 7, nf - 1);
+    const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = a.pt[pg0], e1 = a.pt[jl >> MLXR_PAGE_SHIFT];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const int jv = min(kb + r, nf - 1);
+        const int64_t rv = ((int64_t)(((jv >> MLXR_PAGE_SHIFT) == pg0 ? e0 : e1) * a.nKV + kvh) * MLXR_PAGE + (jv & (MLXR_PAGE - 1))) * 128;
+        typedef const __attribute__((address_space(1))) unsigned long long* gptr64;
+        const unsigned long long v = *(gptr64)(ly.vc + rv + 4 * (t & 31));
+        pf.v[r] = uint2{(uint32_t)v, (uint32_t)(v >> 32)};
     }
 }
-
-// Register array element r (r < MK_KV_PF) without dynamic indexing (a select chain).
-__device__ __forceinline__ uint4 pick_pf(const uint4 (&a)[MK_KV_PF], int r) {
-    uint4 v = a[0];
-#pragma unroll
-    for (int i = 1; i < MK_KV_PF; i++) if (r == i) v = a[i];
-    return v;
+__device__ __forceinline__ void att_prefetch(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int nf, int c, KVPrefetch& pf) {
+    att_prefetch_k(a, ly, kvh, n0, nf, c, pf);
+    att_prefetch_v(a, ly, kvh, n0, nf, c, pf);
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4 v, float* o) {
@@ -570,11 +599,12 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             for (int j = 0; j < 8; j++) st_ag(a.h + c * 8 + j, (float)((w >> (4 * j)) & 15u) * s + b);
         }
     }
-    unsigned epoch = 0;
+    unsigned epoch = 0;                                   // barrier phases of this launch
+    const unsigned base = ld_ag(&a.sync->launch) << 10;   // unique arrival numbers across launches
     prof_mark(a.prof, 0);
-    prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+    prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
     mv_prefetch<FB>(a.layers[0].qkv, wg, nwg, wave, lane, ring);
-    grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
+    grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
     const int nsplit = nwg / nKV;
     for (int li = 0; li < a.L; li++) {
@@ -586,22 +616,31 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_run<FB>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkv, nullptr, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
         // prefetch this workgroup's K/V rows (positions < pos are final)
         const int item = wg;                       // nwg == nKV * nsplit
         const int kvh = item / nsplit, split = item % nsplit;
         int n0, n1; att_range(L, nsplit, split, n0, n1);
-        att_prefetch(a, ly, kvh, n0, min(n1, pos), kvpf);
-        grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
+        att_prefetch(a, ly, kvh, n0, min(n1, pos), 0, kvpf);
+        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
-        // ---- B: attention for (kvh, split)
+        // ---- B: attention for (kvh, split): scores on the matrix cores (K rows from the bf16 cache as
+        // the A operand, q as bf16 hi + lo parts in B), softmax over chunks of 128 keys with running
+        // max / sum, P.V on the vector units.
+        typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+        const int nk = n1 - n0;
+        const int prow = (kvh * G) * nsplit;             // partial rows: (head, split)
+        float* pm = a.part; float* pl = a.part + nH * nsplit; float* pa = a.part + 2 * nH * nsplit;
+        uint16_t* qb = reinterpret_cast<uint16_t*>(lds); // [2][16][128] bf16: q hi / lo
+        uint16_t* kn16 = qb + 2 * 16 * 128;              // new key, bf16 [128]
+        uint16_t* vn16 = kn16 + 128;                     // new value, bf16 [128]
+        float* buf = reinterpret_cast<float*>(vn16 + 128);   // 4 x 128 rope scratch
+        float* wred = buf + 4 * 128;                     // [2][waves][16] per-wave max, sum
+        float* mls = wred + 2 * MK_WAVES * 16;           // [2][16] running max, sum per head
+        float* pp = mls + 32;                            // [MAXG][128] chunk probabilities
+        float* wacc = pp + MAXG * 128;                   // [waves][MAXG][128] P.V partials; merge scratch
+        float* mrow = wacc + MK_WAVES * MAXG * 128;      // [MAXG] merge scale
         {
-            float* qs = lds;                        // [G][128] scaled queries
-            float* kn = qs + MK_MAXG * 128;         // new key (bf16-rounded) [128]
-            float* vn = kn + 128;                   // new value [128]
-            float* buf = vn + 128;                  // 4 x 128 rope scratch
-            float* sc = buf + 4 * 128;              // scores [G][nk]
-            const int nk = n1 - n0;
             const bool owns_new = pos >= n0 && pos < n1;
             // q heads (4 per pass of 512 threads), then the new k and v if this range holds pos
             const int grp = tid >> 7, i = tid & 127;
@@ -615,108 +654,144 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 const int g = base + grp;
                 const float v = g < G ? (base == 0 ? qv0 : qv1) : 0.0f;
                 const float o = head_norm_rope(v, i, ly.q_norm, a.eps, a.inv_freq, pos, a.rot_dim, a.traditional, buf + grp * 128, red, grp);
-                if (g < G) qs[g * 128 + i] = o * a.scale;
+                if (g < G) {
+                    const float q = o * a.scale;
+                    const uint16_t hi = f32_to_bf16(q);
+                    qb[g * 128 + i] = hi;
+                    qb[2048 + g * 128 + i] = f32_to_bf16(q - bf16_to_f32(hi));
+                }
             }
+            for (int e = tid; e < 2 * (16 - G) * 128; e += MK_THREADS) {   // unused head columns: zero
+                const int hl = e / ((16 - G) * 128), r = e - hl * (16 - G) * 128;
+                qb[hl * 2048 + G * 128 + r] = 0;
+            }
+            if (tid < 32) mls[tid] = tid < 16 ? -1e30f : 0.0f;
             if (owns_new) {
                 const float ko = head_norm_rope(tid < 128 ? kraw : 0.0f, i, ly.k_norm, a.eps, a.inv_freq, pos, a.rot_dim, a.traditional, buf + grp * 128, red, grp);
                 if (tid < 128) {
                     const uint16_t kb = f32_to_bf16(ko), vb = f32_to_bf16(vraw);
-                    kn[i] = bf16_to_f32(kb); vn[i] = bf16_to_f32(vb);
+                    kn16[i] = kb; vn16[i] = vb;
                     const int64_t row = kv_row(a.pt, nKV, kvh, pos) * 128 + i;
                     ly.kc[row] = kb; ly.vc[row] = vb;
                 }
             }
             __syncthreads();
-            // scores: 16 lanes per key (8 dims each), 32 keys per round
-            const int slot = tid >> 4, part = tid & 15;
-            const int rounds = (nk + 31) / 32;
-            for (int r = 0; r < rounds; r++) {
-                const int jj = r * 32 + slot, j = n0 + jj;
-                float kf[8];
-                if (j == pos) {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) kf[e] = kn[part * 8 + e];
-                } else if (jj < nk) {
-                    uint4 kv = pick_pf(kvpf.k, r);
-                    if (r >= MK_KV_PF) kv = *reinterpret_cast<const uint4*>(ly.kc + kv_row(a.pt, nKV, kvh, j) * 128 + part * 8);
-                    unpack_bf16x8(kv, kf);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) kf[e] = 0.0f;
-                }
-                for (int g = 0; g < G; g++) {
-                    float s = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) s = fmaf(qs[g * 128 + part * 8 + e], kf[e], s);
-                    s += __shfl_xor(s, 1, 64); s += __shfl_xor(s, 2, 64); s += __shfl_xor(s, 4, 64); s += __shfl_xor(s, 8, 64);
-                    if (part == 0 && jj < nk) sc[g * nk + jj] = s;
-                }
-            }
-            __syncthreads();
-            prof_mark(a.prof, 512 + 8 * li + 1);
-            // softmax partial per head (waves take heads)
-            float* mrow = sc + G * (nk > 0 ? nk : 1);        // [G] max, [G] sum
-            for (int g = wave; g < G; g += MK_WAVES) {
-                float m = -1e30f;
-                for (int k = lane; k < nk; k += 64) m = fmaxf(m, sc[g * nk + k]);
-                m = wave_max(m);
-                float l = 0.0f;
-                for (int k = lane; k < nk; k += 64) { const float p = expf(sc[g * nk + k] - m); sc[g * nk + k] = p; l += p; }
-                l = wave_sum(l);
-                if (lane == 0) { mrow[g] = m; mrow[MK_MAXG + g] = l; }
-            }
-            __syncthreads();
-            // P.V: thread owns 8 dims (part) of keys slot, slot+32, ...
-            float acc[MAXG][8];
+            prof_mark(a.prof, 512 + 8 * li + 7);
+
+            float acc[MAXG][4];
 #pragma unroll
             for (int g = 0; g < MAXG; g++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
-            for (int r = 0; r < rounds; r++) {
-                const int jj = r * 32 + slot, j = n0 + jj;
-                if (jj >= nk) continue;
-                float vf[8];
-                if (j == pos) {
+                for (int e = 0; e < 4; e++) acc[g][e] = 0.0f;
+            const int hh = lane & 15, d4 = tid & 31, slice = tid >> 5;
+            const int nchunks = (nk + 127) >> 7;
+            const int nf = min(n1, pos);
+            for (int c = 0; c < nchunks; c++) {
+                asm volatile("" ::: "memory");   // keeps the q reads in the loop (no registers held across chunks)
+                // scores S[key][head] of the wave's 16 keys
+                const int kbase = n0 + 128 * c + 16 * wave;
+                uint4* kq = kvpf.k;
+                if (owns_new && kbase + (lane & 15) == pos) {   // only the owner wrote kn16 / vn16
 #pragma unroll
-                    for (int e = 0; e < 8; e++) vf[e] = vn[part * 8 + e];
-                } else {
-                    uint4 vv = pick_pf(kvpf.v, r);
-                    if (r >= MK_KV_PF) vv = *reinterpret_cast<const uint4*>(ly.vc + kv_row(a.pt, nKV, kvh, j) * 128 + part * 8);
-                    unpack_bf16x8(vv, vf);
+                    for (int db = 0; db < 4; db++) kq[db] = *reinterpret_cast<const uint4*>(kn16 + 32 * db + 8 * (lane >> 4));
                 }
+                f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+#pragma unroll
+                    for (int hl = 0; hl < 2; hl++) {
+                        const uint4 bq = *reinterpret_cast<const uint4*>(qb + hl * 2048 + hh * 128 + 32 * db + 8 * (lane >> 4));
+                        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kq[db]), __builtin_bit_cast(bf16x8_t, bq), sacc, 0, 0, 0);
+                    }
+                float sv[4], mloc = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const bool ok = kbase + 4 * (lane >> 4) + r < n1;
+                    sv[r] = ok ? sacc[r] : -INFINITY;
+                    mloc = fmaxf(mloc, sv[r]);
+                }
+                mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64)); mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+                if (lane < 16) wred[lane * MK_WAVES + wave] = mloc;
+                __syncthreads();
+                // new running max per head; probabilities of this lane's keys
+                const float4 wa = *reinterpret_cast<const float4*>(wred + hh * MK_WAVES);
+                const float4 wb = *reinterpret_cast<const float4*>(wred + hh * MK_WAVES + 4);
+                const float mnew_h = fmaxf(mls[hh], fmaxf(fmaxf(fmaxf(wa.x, wa.y), fmaxf(wa.z, wa.w)), fmaxf(fmaxf(wb.x, wb.y), fmaxf(wb.z, wb.w))));
+                float lsum = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float p = expf(sv[r] - mnew_h);
+                    lsum += p;
+                    if (hh < MAXG) pp[hh * 128 + 16 * wave + 4 * (lane >> 4) + r] = hh < G ? p : 0.0f;
+                }
+                lsum += __shfl_xor(lsum, 16, 64); lsum += __shfl_xor(lsum, 32, 64);
+                if (lane < 16) wred[MK_WAVES * 16 + lane * MK_WAVES + wave] = lsum;
+                float alpha[MAXG];
 #pragma unroll
                 for (int g = 0; g < MAXG; g++) {
-                    if (g < G) {
-                        const float p = sc[g * nk + jj];
+                    const float4 ga = *reinterpret_cast<const float4*>(wred + g * MK_WAVES);
+                    const float4 gb = *reinterpret_cast<const float4*>(wred + g * MK_WAVES + 4);
+                    const float mn = fmaxf(mls[g], fmaxf(fmaxf(fmaxf(ga.x, ga.y), fmaxf(ga.z, ga.w)), fmaxf(fmaxf(gb.x, gb.y), fmaxf(gb.z, gb.w))));
+                    alpha[g] = expf(mls[g] - mn);
+                }
+                if (c + 1 < nchunks) att_prefetch_k(a, ly, kvh, n0, nf, c + 1, kvpf);   // while softmax and P.V run
+                __syncthreads();
+                // running sums (one thread per head), then P.V with the rescaled accumulators
+                if (tid < G) {
+                    float mn = mls[tid], ls = 0.0f;
+                    for (int w = 0; w < MK_WAVES; w++) { mn = fmaxf(mn, wred[tid * MK_WAVES + w]); ls += wred[MK_WAVES * 16 + tid * MK_WAVES + w]; }
+                    mls[16 + tid] = mls[16 + tid] * alpha[tid] + ls;
+                    mls[tid] = mn;
+                }
 #pragma unroll
-                        for (int e = 0; e < 8; e++) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+                for (int g = 0; g < MAXG; g++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[g][e] *= alpha[g];
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    // keys 8 slice + 4 half .. +4 of the chunk (probabilities of masked keys are 0)
+                    float4 pr[MAXG];
+#pragma unroll
+                    for (int g = 0; g < MAXG; g++) pr[g] = *reinterpret_cast<const float4*>(pp + g * 128 + 8 * slice + 4 * half);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int r = 4 * half + q, j = n0 + 128 * c + 8 * slice + r;
+                        uint2 vv = kvpf.v[r];
+                        if (owns_new && j == pos) vv = *reinterpret_cast<const uint2*>(vn16 + 4 * d4);
+                        const float vf[4] = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
+                                             __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
+#pragma unroll
+                        for (int g = 0; g < MAXG; g++) {
+                            const float pg = q == 0 ? pr[g].x : q == 1 ? pr[g].y : q == 2 ? pr[g].z : pr[g].w;
+#pragma unroll
+                            for (int e = 0; e < 4; e++) acc[g][e] = fmaf(pg, vf[e], acc[g][e]);
+                        }
                     }
                 }
+                if (c + 1 < nchunks) att_prefetch_v(a, ly, kvh, n0, nf, c + 1, kvpf);
             }
+            prof_mark(a.prof, 512 + 8 * li + 1);
             prof_mark(a.prof, 512 + 8 * li + 2);
-            // reduce over the 4 slots of a wave (lanes l, l+16, l+32, l+48), then over waves via LDS
-            float* wsum = mrow + 2 * MK_MAXG;                 // [waves][G][128]
+            // reduce over the 2 slices of a wave (lanes l, l^32), then over waves via LDS
 #pragma unroll
             for (int g = 0; g < MAXG; g++) {
                 if (g < G) {
 #pragma unroll
-                    for (int e = 0; e < 8; e++) {
+                    for (int e = 0; e < 4; e++) {
                         float v = acc[g][e];
-                        v += __shfl_xor(v, 16, 64); v += __shfl_xor(v, 32, 64);
-                        if (lane < 16) wsum[(wave * G + g) * 128 + lane * 8 + e] = v;
+                        v += __shfl_xor(v, 32, 64);
+                        if (lane < 32) wacc[(wave * MAXG + g) * 128 + lane * 4 + e] = v;
                     }
                 }
             }
             __syncthreads();
-            const int prow = (kvh * G) * nsplit;             // partial rows: (head, split)
-            float* pm = a.part; float* pl = a.part + nH * nsplit; float* pa = a.part + 2 * nH * nsplit;
             for (int idx = tid; idx < G * 128; idx += MK_THREADS) {
                 const int g = idx >> 7, d = idx & 127;
                 float v = 0.0f;
-                for (int w = 0; w < MK_WAVES; w++) v += wsum[(w * G + g) * 128 + d];
+                for (int w = 0; w < MK_WAVES; w++) v += wacc[(w * MAXG + g) * 128 + d];
                 const int r = prow + g * nsplit + split;
                 st_ag(pa + (int64_t)r * 128 + d, nk > 0 ? v : 0.0f);
-                if (d == 0) { st_ag(pm + r, nk > 0 ? mrow[g] : -1e30f); st_ag(pl + r, nk > 0 ? mrow[MK_MAXG + g] : 0.0f); }
+                if (d == 0) { st_ag(pm + r, nk > 0 ? mls[g] : -1e30f); st_ag(pl + r, nk > 0 ? mls[16 + g] : 0.0f); }
             }
             prof_mark(a.prof, 512 + 8 * li + 3);
             // the last range of this KV head to finish merges the partials in range order
@@ -732,8 +807,8 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 // merge: weights f_s = exp(m_s - M) and 1 / sum_s l_s f_s per head (m, l staged in LDS),
                 // then every (head, dim) sums its nsplit partials, loaded 32 at a time
                 const int P = nH * nsplit;
-                float* wts = wsum;                                  // [G][nsplit] weights
-                float* lsv = wsum + MK_MAXG * 64;                   // [G][nsplit] sums
+                float* wts = wacc;                                  // [G][nsplit] weights
+                float* lsv = wacc + MK_MAXG * 64;                   // [G][nsplit] sums
                 for (int idx = tid; idx < G * nsplit; idx += MK_THREADS) {
                     wts[idx] = ld_coh1(pm, prow + idx, P);
                     lsv[idx] = ld_coh1(pl, prow + idx, P);
@@ -766,9 +841,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 }
             }
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
         mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
+        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- C: o_proj, h += W_o attn
         {
@@ -778,9 +853,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_run<FB>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.h, ml.hown, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
         mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
+        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- D: gate|up with SiLU
         {
@@ -789,9 +864,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_run<FB>(ly.gu, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_GATED, FB>(ly.gu, us, wg, nwg, ml.part, a.mlp, nullptr, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
         mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
+        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- E: down, h += W_d mlp
         {
@@ -801,10 +876,10 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_run<FB>(ly.down, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.h, ml.hown, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
         if (li + 1 < a.L) mv_prefetch<FB>(a.layers[li + 1].qkv, wg, nwg, wave, lane, ring);
         else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, epoch); prof_mark(a.prof, 2 * epoch - 1);
+        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
     }
 
     // ---- lm_head with the final norm, logits and the greedy token
@@ -819,11 +894,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         __builtin_amdgcn_s_waitcnt(0);
         const unsigned done = add_ag(a.head_done, 1u);
         flag = done == (unsigned)nwg - 1;
-        if (flag) {   // every workgroup is past its last barrier: reset the counters for the next launch
+        if (flag) {   // every workgroup is past its last barrier: reset the counter, count the launch
             __hip_atomic_store(a.head_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&a.sync->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&a.sync->gen, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            for (int x = 0; x < 8; x++) __hip_atomic_store(&a.sync->xcd[x][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&a.sync->launch, (base >> 10) + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();
@@ -908,8 +981,10 @@ size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split) {
     const int G = a.nH / a.nKV;
     const size_t kmax = (size_t)std::max(a.H, std::max(a.I, a.nH * 128));
     size_t mv = (kmax + kmax / 32 * (XH_STRIDE + 2) + 4 + MK_HOWN + MK_TPW * MK_WAVES * 16) * 4;
-    size_t att = (size_t)(MK_MAXG * 128 + 256 + 512) * 4 + (size_t)G * max_keys_per_split * 4 + 2 * MK_MAXG * 4 +
-                 (size_t)std::max(MK_WAVES * G * 128, 2 * MK_MAXG * 64) * 4;
+    // attention: q hi/lo image, new k/v, rope scratch, exchanges, probabilities, P.V partials, merge scale
+    size_t att = 2 * 16 * 128 * 2 + 2 * 128 * 2 + (size_t)(4 * 128 + 2 * MK_WAVES * 16 + 32 + MK_MAXG * 128 +
+                 MK_WAVES * MK_MAXG * 128 + MK_MAXG) * 4;
+    (void)max_keys_per_split; (void)G;
     return std::max(mv, att);
 }
 

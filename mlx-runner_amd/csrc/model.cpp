@@ -216,6 +216,7 @@ Model::~Model() {
     if (h_logits) hipHostFree(h_logits);
     if (ring_tok) hipHostFree(ring_tok);
     if (ring_status) hipHostFree(ring_status);
+    if (abort_host) hipHostFree(abort_host);
     if (stream) hipStreamDestroy(stream);
 }
 
@@ -340,6 +341,7 @@ static int mega_setup(Model* m) {
     if (nwg < c.nKV) return no("too few compute units");
     const int nsplit = nwg / c.nKV;
     const int max_keys = (m->max_seq + nsplit - 1) / nsplit;
+    if ((c.nH / c.nKV) * nsplit > 512) return no("too many attention partials per KV head");
     {
         const int tmax = std::max({(c.V + 15) / 16, ((c.nH + 2 * c.nKV) * c.D + 15) / 16, (c.I + 7) / 8, (c.H + 15) / 16});
         if ((tmax + nwg - 1) / nwg > mega_tiles_per_wg_cap()) return no("too many row tiles per workgroup");
@@ -352,6 +354,7 @@ static int mega_setup(Model* m) {
     const size_t lds = mega_lds_bytes(a, max_keys);
     if (lds > 150 * 1024) return no("LDS need " + std::to_string(lds >> 10) + " KiB");
     if (mega_set_lds_limit(lds) != hipSuccess) return no("LDS attribute");
+    if (nwg > MEGA_MAX_WG) return no("too many workgroups");
     // each phase's matrices, repacked once into the decode tile layout (a second copy of the weights)
     int rc = MLXR_OK;
     auto desc = [&](const Lin* parts, int n, bool gated) {
@@ -401,6 +404,8 @@ static int mega_setup(Model* m) {
     HIPCHECK(hipMemset(a.head_done, 0, 64 * 4));
     HIPCHECK(hipMemset(a.sync, 0, sizeof(MegaSync)));
     a.ring_tok = m->ring_tok_dev; a.ring_status = m->ring_status_dev; a.ring_mask = Model::RING - 1;
+    *m->abort_host = 0;
+    a.abort_host = m->abort_host_dev;
     m->mega_nwg = nwg; m->mega_lds = lds; m->mega_ok = true;
     return MLXR_OK;
 }
@@ -535,6 +540,9 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
     HIPCHECK(hipHostMalloc((void**)&m->ring_status, Model::RING * 4, hipHostMallocMapped));
     HIPCHECK(hipHostGetDevicePointer((void**)&m->ring_tok_dev, m->ring_tok, 0));
     HIPCHECK(hipHostGetDevicePointer((void**)&m->ring_status_dev, m->ring_status, 0));
+    HIPCHECK(hipHostMalloc((void**)&m->abort_host, 64, hipHostMallocMapped));
+    HIPCHECK(hipHostGetDevicePointer((void**)&m->abort_host_dev, m->abort_host, 0));
+    *m->abort_host = 0;
     for (auto& s : m->slots) { HIPCHECK(hipEventCreate(&s.start)); HIPCHECK(hipEventCreate(&s.stop)); }
     if ((rc = model_seed(m, 0))) return fail(rc);
     if ((rc = mega_setup(m))) return fail(rc);
@@ -857,14 +865,11 @@ int model_finish(Model* m, const mlxr_step* st, int32_t* tok) {
     slot.busy = false;
     if (e != hipSuccess) return set_error(MLXR_E_GPU, std::string("GPU error: ") + hipGetErrorString(e));
     record_gpu_time(m, slot);
-    if (m->mega_ok) {
-        MegaSync ms;
-        HIPCHECK(hipMemcpy(&ms, m->mega.sync, sizeof(MegaSync), hipMemcpyDeviceToHost));
-        if (ms.abort) {
-            m->mega_ok = false;   // fall back to the kernel-per-op step from now on
-            HIPCHECK(hipMemset(m->mega.sync, 0, sizeof(MegaSync)));
-            return set_error(MLXR_E_GPU, "persistent decode step: a grid barrier expired (step result discarded)");
-        }
+    if (m->mega_ok && *(volatile int*)m->abort_host) {
+        m->mega_ok = false;   // fall back to the kernel-per-op step from now on
+        *m->abort_host = 0;
+        HIPCHECK(hipMemset(m->mega.sync, 0, sizeof(MegaSync)));
+        return set_error(MLXR_E_GPU, "persistent decode step: a grid barrier expired (step result discarded)");
     }
     return read_ring(m, st->offset + 1, tok);
 }

@@ -75,6 +75,7 @@ struct Model {
     float* h_logits = nullptr;           // pinned [8][V]
     int* ring_tok = nullptr; int* ring_status = nullptr;   // host-mapped token ring
     int* ring_tok_dev = nullptr; int* ring_status_dev = nullptr;
+    int* abort_host = nullptr; int* abort_host_dev = nullptr;   // host-mapped barrier-expiry flag
     static constexpr int RING = 64;
 
     hipStream_t stream = nullptr;
