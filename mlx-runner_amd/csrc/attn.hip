@@ -304,6 +304,4 @@ hipError_t launch_sparse_select_plan(const float* scores, int* lists, int list_s
     return hipGetLastError();
 }
 
-hipError_t launch_flash_prefill(const FlashArgs&, hipStream_t) { return hipErrorNotSupported; }
-
 }  // namespace mlxr

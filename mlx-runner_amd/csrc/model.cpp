@@ -505,8 +505,7 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
     const int B = m->max_batch, H = c.H, I = c.I, V = c.V;
     m->qkv_cols = (c.nH + 2 * c.nKV) * c.D;
     m->nsplit_dec = std::max((seq + 511) / 512, std::min(64, (512 + c.nKV - 1) / c.nKV));
-    m->nsplit_pre = std::max(1, (seq + 511) / 512);
-    const size_t partFloats = std::max((size_t)B * c.nH * m->nsplit_pre, (size_t)8 * c.nH * m->nsplit_dec) * (c.D + 2);
+    const size_t partFloats = (size_t)8 * c.nH * m->nsplit_dec * (c.D + 2);   // split-attention partials (T <= 8)
     int Kmax = std::max(c.I, std::max(c.H, c.nH * c.D));
     int rc;
     if ((rc = dalloc(m, &m->hist, seq + 1)) || (rc = dalloc(m, &m->status, seq + 1)) || (rc = dalloc(m, &m->rng, 2)) ||
@@ -672,10 +671,15 @@ int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
         HIPCHECK(launch_qkv_post(pa, s));
         if (m->sparse_alloc) HIPCHECK(launch_sparse_index(ly.kc, m->page_table, ly.idx, c.nKV, c.D, m->dpos, 0, T, s));
         const float scale = c.query_scale * c.rope_attention_factor * c.rope_attention_factor;
-        {
+        if (T > 8) {   // prefill chunk: flash attention on the matrix cores
+            FlashArgs fa; fa.q = m->qkv; fa.q_stride = m->qkv_cols; fa.kc = ly.kc; fa.vc = ly.vc; fa.pt = m->page_table;
+            fa.out = m->attn; fa.out_stride = c.nH * c.D; fa.D = c.D; fa.nH = c.nH; fa.nKV = c.nKV; fa.T = T;
+            fa.dpos = m->dpos; fa.scale = scale;
+            HIPCHECK(launch_flash_prefill(fa, s));
+        } else {       // verify batch: the decode attention per query
             AttnArgs aa; aa.q = m->qkv; aa.q_stride = m->qkv_cols; aa.kc = ly.kc; aa.vc = ly.vc; aa.pt = m->page_table;
             aa.out = m->attn; aa.out_stride = c.nH * c.D; aa.part = m->part; aa.D = c.D; aa.nH = c.nH; aa.nKV = c.nKV; aa.T = T;
-            aa.nsplit = T > 8 ? m->nsplit_pre : m->nsplit_dec; aa.dpos = m->dpos; aa.scale = scale;
+            aa.nsplit = m->nsplit_dec; aa.dpos = m->dpos; aa.scale = scale;
             HIPCHECK(launch_attn_decode(aa, s));
         }
         if (int rc = project(m, &ly.o, 1, m->attn, c.nH * c.D, m->tmp, H, T)) return rc;

@@ -79,8 +79,8 @@ struct Model {
     static constexpr int RING = 64;
 
     hipStream_t stream = nullptr;
-    int qkv_cols = 0, nsplit_dec = 32, nsplit_pre = 1;
-    int max_batch = 512;
+    int qkv_cols = 0, nsplit_dec = 32;
+    int max_batch = 2048;                // prefill chunk (tokens per batched pass)
     int dev_pos_known = -1;              // value *dpos will hold once queued work completes
     int written_high = 0;
     bool use_graphs = true;

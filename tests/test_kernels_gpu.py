@@ -258,6 +258,39 @@ def test_attention_decode_and_split(gpu, nH, nKV):
     del rng
 
 
+def run_flash(mlxr, q, kc, vc, nH, nKV, offset, T, scale):
+    D = q.shape[-1]
+    S = kc.shape[1]
+    dq = mlxr.DeviceArray.from_numpy(np.ascontiguousarray(q.reshape(T, nH * D)))
+    dk = mlxr.DeviceArray.from_numpy(bf16_round(to_paged(kc)))
+    dv = mlxr.DeviceArray.from_numpy(bf16_round(to_paged(vc)))
+    out = mlxr.DeviceArray.zeros((T, nH * D), np.float32)
+    mlxr.check(mlxr.lib.mlxr_k_flash_prefill(dq.ptr, nH * D, dk.ptr, dv.ptr, S, D, nH, nKV, offset, T, scale, out.ptr, nH * D))
+    mlxr.synchronize()
+    return out.numpy().reshape(T, nH, D)
+
+
+@pytest.mark.parametrize("nH,nKV,offset,T", [(4, 2, 0, 1), (4, 2, 0, 45), (32, 8, 37, 200), (40, 8, 64, 130), (16, 2, 5, 96)])
+def test_flash_prefill(gpu, nH, nKV, offset, T):
+    """flash_prefill (Kernels.swift:1839-2000): token t of the chunk (position offset + t) attends keys
+    0..offset + t; every token's output against the reference attention (oracle), and rows past the
+    chunk's last key filled with NaN to check they never reach the result. Tolerance 1e-4 relative:
+    q and p enter the bf16 matrix cores as hi + lo pairs (~2^-16), products accumulate in fp32."""
+    D, S = 128, 512
+    kc = bf16_to_f32(bf16_round(np.random.default_rng(nH + T).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
+    vc = bf16_to_f32(bf16_round(np.random.default_rng(nH + T + 1).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
+    kc[:, offset + T:] = np.nan
+    vc[:, offset + T:] = np.nan
+    q = np.random.default_rng(nH + T + 2).uniform(-1, 1, (T, nH, D)).astype(np.float32)
+    scale = 3 / np.sqrt(D)
+    got = run_flash(gpu, q, kc, vc, nH, nKV, offset, T, scale)
+    assert np.all(np.isfinite(got))
+    kref, vref = np.nan_to_num(kc), np.nan_to_num(vc)
+    for t in range(T):
+        ref = oracle.attention(q[t], kref, vref, nH, nKV, offset + t, scale)
+        assert max_rel_err(got[t], ref) < 1e-4, (t, max_rel_err(got[t], ref))
+
+
 @pytest.mark.parametrize("nH,nKV", [(4, 2), (8, 2), (10, 2)])
 def test_attention_over_lists(gpu, nH, nKV):
     """attentionOverTheList (SparseAttentionTests.swift:214-297): the full list is bit-identical to
