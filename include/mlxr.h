@@ -176,6 +176,12 @@ int mlxr_k_qmm(const mlxr_qmat* parts, int nparts, int K, int bits, int gs, int 
 /* Prefill GEMM on bf16 MFMA (`qgemm`, Kernels.swift:785-851), any T >= 1. */
 int mlxr_k_qgemm(const mlxr_qmat* mat, int K, int bits, int gs, int st, int T, const float* x, int x_stride,
                  float* y, int y_stride);
+/* The prefill GEMM over the repacked decode tiles that model prefill uses for 4-bit bf16-scale
+ * models (`qgemm`, Kernels.swift:785-851): parts [A|B|C] as in mlxr_k_qmv, bits 4, bf16 scales,
+ * gs 32/64, K % 128 == 0; gated (two parts of equal O): y[t][o] = silu(A x_t)[o] * (B x_t)[o]
+ * (the MLP's gate|up, silu_mul Kernels.swift:2004-2013). Repacks into a temporary buffer per call. */
+int mlxr_k_qgemm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int gated, int T, const float* x,
+                       int x_stride, float* y, int y_stride);
 /* Quantized embedding rows (`qembed`, Kernels.swift:1002-1023): ids device int32 [T]. */
 int mlxr_k_qembed(const mlxr_qmat* mat, int K, int bits, int gs, int st, const int32_t* ids, int T, float* out);
 /* RMSNorm rows (`rms_norm`, Kernels.swift:1037-1070), fp32 weights; add_rms_norm with r != NULL. */

@@ -21,6 +21,7 @@ int* g_pt = nullptr;           // identity page table
 int g_pt_pages = 0;
 float* g_part = nullptr; size_t g_part_floats = 0;
 uint16_t* g_xbf = nullptr; size_t g_xbf_elems = 0;
+float* g_xsc = nullptr; size_t g_xsc_elems = 0;
 float* g_bmax = nullptr; int* g_barg = nullptr; int g_blocks = 0;
 hipEvent_t g_t0 = nullptr, g_t1 = nullptr;
 
@@ -220,9 +221,46 @@ int mlxr_k_qgemm(const mlxr_qmat* mat, int K, int bits, int gs, int st, int T, c
     if (int rc = check_quant(K, bits, gs, st)) return rc;
     if (T < 1 || !x || !y || x_stride < K || y_stride < mat->O || x_stride % 4) return set_error(MLXR_E_INVALID_ARG, "T / strides");
     if (int rc = ensure_buf(g_xbf, g_xbf_elems, (size_t)T * K)) return rc;
+    if (int rc = ensure_buf(g_xsc, g_xsc_elems, (size_t)T)) return rc;
     QGemmArgs a; a.m = qmat(*mat); a.K = K; a.bits = bits; a.gs = gs; a.st = st; a.O = mat->O; a.T = T;
-    a.x = x; a.x_stride = x_stride; a.y = y; a.y_stride = y_stride; a.xbf = g_xbf;
+    a.x = x; a.x_stride = x_stride; a.y = y; a.y_stride = y_stride; a.xbf = g_xbf; a.xsc = g_xsc;
     return done(launch_qgemm(a, g_stream));
+}
+
+int mlxr_k_qgemm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int gated, int T, const float* x, int x_stride,
+                       float* y, int y_stride) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (int rc = ensure_stream()) return rc;
+    if (int rc = check_parts(parts, nparts)) return rc;
+    if ((gs != 32 && gs != 64) || K % 128) return set_error(MLXR_E_INVALID_ARG, "repacked tiles need gs 32/64 and K % 128 == 0");
+    if (gated && (nparts != 2 || parts[0].O != parts[1].O)) return set_error(MLXR_E_INVALID_ARG, "gated: two parts of equal O");
+    int rows = 0;
+    for (int i = 0; i < nparts; i++) rows += parts[i].O;
+    const int out_cols = gated ? parts[0].O : rows;
+    if (T < 1 || !x || !y || x_stride < K || y_stride < out_cols || x_stride % 4) return set_error(MLXR_E_INVALID_ARG, "T / strides");
+    DPackSrc src{};
+    MvPhaseDesc d{};
+    for (int i = 0; i < 3; i++) {
+        const mlxr_qmat& q = parts[i < nparts ? i : nparts - 1];
+        src.w[i] = static_cast<const uint8_t*>(q.w);
+        src.s[i] = static_cast<const uint16_t*>(q.scales); src.b[i] = static_cast<const uint16_t*>(q.biases);
+        d.bias[i] = i < nparts ? static_cast<const uint16_t*>(q.bias) : nullptr;
+    }
+    d.o1 = src.o1 = parts[0].O; d.o2 = src.o2 = nparts > 1 ? parts[1].O : 0;
+    d.rows = src.rows = rows; d.K = src.K = K; d.gs = src.gs = gs; d.gated = src.gated = gated ? 1 : 0;
+    d.tiles = dpack_tiles(src);
+    if (int rc = ensure_buf(g_xbf, g_xbf_elems, (size_t)T * K)) return rc;
+    if (int rc = ensure_buf(g_xsc, g_xsc_elems, (size_t)T)) return rc;
+    uint8_t* code = nullptr;
+    CK(hipMalloc(&code, dpack_bytes(src)));
+    d.code = code;
+    hipError_t e = launch_dpack(src, code, g_stream);
+    if (e == hipSuccess) e = launch_x_to_f16(x, x_stride, K, T, g_xbf, g_xsc, g_stream);
+    if (e == hipSuccess) e = launch_tile_gemm(d, g_xbf, g_xsc, T, y, y_stride, g_stream);
+    const hipError_t e2 = hipStreamSynchronize(g_stream);
+    hipFree(code);
+    if (e == hipSuccess) e = e2;
+    return done(e);
 }
 
 int mlxr_k_qembed(const mlxr_qmat* mat, int K, int bits, int gs, int st, const int32_t* ids, int T, float* out) {

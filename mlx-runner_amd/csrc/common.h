@@ -18,6 +18,7 @@ __device__ __host__ __forceinline__ uint16_t f32_to_bf16(float f) {
     b += 0x7fffu + ((b >> 16) & 1u);
     return (uint16_t)(b >> 16);
 }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 __device__ __forceinline__ float f16_to_f32(uint16_t u) {
     _Float16 h; __builtin_memcpy(&h, &u, 2); return (float)h;
 }

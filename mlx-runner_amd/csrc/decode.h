@@ -22,6 +22,12 @@ int dpack_tiles(const DPackSrc& s);
 size_t dpack_bytes(const DPackSrc& s);
 hipError_t launch_dpack(const DPackSrc& s, uint8_t* out, hipStream_t st);
 
+// Prefill GEMM over a repacked matrix (ptile.hip): y[T][rows] (gated: y[T][o1] = SiLU(gate) * up)
+// from x already converted by the 4-bit GEMM pre-pass (xh: f16 rows scaled by 1 / inv[t]).
+bool tile_gemm_supported(const MvPhaseDesc& p);
+hipError_t launch_tile_gemm(const MvPhaseDesc& p, const uint16_t* xh, const float* inv, int T, float* y, int ys,
+                            hipStream_t s);
+
 struct LayerDev {
     MvPhaseDesc qkv, o, gu, down;
     const float* in_norm; const float* post_norm; const float* q_norm; const float* k_norm;

@@ -47,9 +47,14 @@ struct QGemmArgs {
     int K = 0, bits = 4, gs = 64, st = 0, O = 0, T = 0;
     const float* x = nullptr; int x_stride = 0;
     float* y = nullptr; int y_stride = 0;
-    uint16_t* xbf = nullptr;              // scratch: T*K bf16 (x rounded once per call)
+    uint16_t* xbf = nullptr;              // scratch: T*K 16-bit (x rounded once per call)
+    float* xsc = nullptr;                 // scratch: T floats (per-row power-of-two scales); null = bf16 path
+    bool x_ready = false;                 // xbf / xsc already hold this x (same K): skip the pre-pass
 };
 hipError_t launch_qgemm(const QGemmArgs& a, hipStream_t s);
+// The 4-bit GEMM pre-pass: row t of x scaled by the power of two that puts max|x| in [2^13, 2^14),
+// rounded to f16 (each 8-group stored as 0,4,1,5,2,6,3,7), inv[t] = the inverse scale.
+hipError_t launch_x_to_f16(const float* x, int xs, int K, int T, uint16_t* out, float* inv, hipStream_t s);
 
 // Embedding: out[t][k] = dequant(row ids[t]) (ids read from hist + *dpos + t0).
 hipError_t launch_qembed(const QMat& m, int K, int bits, int gs, int st, const int* hist, const int* dpos, int T,

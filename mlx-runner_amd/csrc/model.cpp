@@ -387,6 +387,7 @@ static int mega_setup(Model* m) {
     }
     if ((rc = dalloc(m, &m->mega_layers, c.L))) return rc;
     HIPCHECK(hipMemcpy(m->mega_layers, host.data(), sizeof(LayerDev) * c.L, hipMemcpyHostToDevice));
+    m->tile_layers = host;
     a.layers = m->mega_layers; a.L = c.L;
     a.head = desc(&m->head, 1, false);
     if (rc) return rc;
@@ -514,7 +515,7 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
         (rc = dalloc(m, &m->attn, (size_t)B * c.nH * c.D)) || (rc = dalloc(m, &m->gu, (size_t)B * 2 * I)) ||
         (rc = dalloc(m, &m->mlp, (size_t)B * I)) || (rc = dalloc(m, &m->logits, (size_t)8 * V)) ||
         (rc = dalloc(m, &m->part, partFloats)) || (rc = dalloc(m, &m->bmax, (V + 255) / 256)) ||
-        (rc = dalloc(m, &m->barg, (V + 255) / 256)) || (rc = dalloc(m, &m->xbf, (size_t)B * Kmax)) || (rc = dalloc(m, &m->diag, 8)))
+        (rc = dalloc(m, &m->barg, (V + 255) / 256)) || (rc = dalloc(m, &m->xbf, (size_t)B * Kmax)) || (rc = dalloc(m, &m->xsc, (size_t)B)) || (rc = dalloc(m, &m->diag, 8)))
         return fail(rc);
     HIPCHECK(hipMemset(m->hist, 0, (seq + 1) * 4));
     HIPCHECK(hipMemset(m->status, 0, (seq + 1) * 4));
@@ -592,7 +593,8 @@ int project(Model* m, const Lin* parts, int n, const float* x, int xs, float* y,
     int col = 0;
     for (int i = 0; i < n; i++) {
         QGemmArgs g; g.m = parts[i].m; g.K = parts[i].K; g.bits = parts[i].bits; g.gs = parts[i].gs; g.st = parts[i].st;
-        g.O = parts[i].O; g.T = T; g.x = x; g.x_stride = xs; g.y = y + col; g.y_stride = ys; g.xbf = m->xbf;
+        g.O = parts[i].O; g.T = T; g.x = x; g.x_stride = xs; g.y = y + col; g.y_stride = ys; g.xbf = m->xbf; g.xsc = m->xsc;
+        g.x_ready = i > 0 && parts[i].K == parts[0].K && parts[i].bits == parts[0].bits && parts[i].gs == parts[0].gs;
         HIPCHECK(launch_qgemm(g, s));
         col += parts[i].O;
     }
@@ -655,16 +657,28 @@ int encode_decode(Model* m, const mlxr_sample_params* sp, bool sparse, bool logi
 
 // A batch of T tokens (2..max_batch) at positions *dpos .. *dpos + T - 1 (prefill chunk / verify).
 // all_logits: logits of every row ([T][V], T <= 8); else of the last row only.
+// Prefill GEMM over a repacked phase: the f16 pre-pass of x, then the tile GEMM.
+int project_tiles(Model* m, const MvPhaseDesc& p, const float* x, int xs, float* y, int ys, int T) {
+    HIPCHECK(launch_x_to_f16(x, xs, p.K, T, m->xbf, m->xsc, m->stream));
+    HIPCHECK(launch_tile_gemm(p, m->xbf, m->xsc, T, y, ys, m->stream));
+    return MLXR_OK;
+}
+
 int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
     const Config& c = m->cfg;
     hipStream_t s = m->stream;
     const int H = c.H, I = c.I;
+    // prefill chunks on the repacked tiles when the model has them (fused q|k|v and gate|up, SiLU
+    // in the gate|up epilogue); verify batches (T <= 8) keep the small-batch kernels
+    const bool tiles = T > 8 && (int)m->tile_layers.size() == c.L;
     HIPCHECK(launch_qembed(m->embed.m, H, m->embed.bits, m->embed.gs, m->embed.st, m->hist, m->dpos, T, m->h, s));
     HIPCHECK(launch_rms_norm(m->h, m->xn, m->layers[0].in_norm, H, T, H, c.eps, s));
     for (int li = 0; li < c.L; li++) {
         Layer& ly = m->layers[li];
         const Lin qkvp[3] = {ly.q, ly.k, ly.v};
-        if (int rc = project(m, qkvp, 3, m->xn, H, m->qkv, m->qkv_cols, T)) return rc;
+        const LayerDev* tl = tiles ? &m->tile_layers[li] : nullptr;
+        if (int rc = tl ? project_tiles(m, tl->qkv, m->xn, H, m->qkv, m->qkv_cols, T)
+                        : project(m, qkvp, 3, m->xn, H, m->qkv, m->qkv_cols, T)) return rc;
         QkvPostArgs pa; pa.qkv = m->qkv; pa.row_stride = m->qkv_cols; pa.inv_freq = m->inv_freq; pa.kc = ly.kc; pa.vc = ly.vc;
         pa.pt = m->page_table; pa.qn = ly.q_norm; pa.kn = ly.k_norm; pa.D = c.D; pa.nH = c.nH; pa.nKV = c.nKV;
         pa.rot_dim = c.rot_dim; pa.traditional = c.traditional; pa.T = T; pa.dpos = m->dpos; pa.eps = c.eps;
@@ -682,12 +696,18 @@ int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
             aa.nsplit = m->nsplit_dec; aa.dpos = m->dpos; aa.scale = scale;
             HIPCHECK(launch_attn_decode(aa, s));
         }
-        if (int rc = project(m, &ly.o, 1, m->attn, c.nH * c.D, m->tmp, H, T)) return rc;
+        if (int rc = tl ? project_tiles(m, tl->o, m->attn, c.nH * c.D, m->tmp, H, T)
+                        : project(m, &ly.o, 1, m->attn, c.nH * c.D, m->tmp, H, T)) return rc;
         HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, ly.post_norm, H, T, c.eps, s));
-        const Lin gup[2] = {ly.gate, ly.up};
-        if (int rc = project(m, gup, 2, m->xn, H, m->gu, 2 * I, T)) return rc;
-        HIPCHECK(launch_silu_mul(m->gu, m->mlp, I, T, s));
-        if (int rc = project(m, &ly.down, 1, m->mlp, I, m->tmp, H, T)) return rc;
+        if (tl) {
+            if (int rc = project_tiles(m, tl->gu, m->xn, H, m->mlp, I, T)) return rc;
+        } else {
+            const Lin gup[2] = {ly.gate, ly.up};
+            if (int rc = project(m, gup, 2, m->xn, H, m->gu, 2 * I, T)) return rc;
+            HIPCHECK(launch_silu_mul(m->gu, m->mlp, I, T, s));
+        }
+        if (int rc = tl ? project_tiles(m, tl->down, m->mlp, I, m->tmp, H, T)
+                        : project(m, &ly.down, 1, m->mlp, I, m->tmp, H, T)) return rc;
         const bool last = li + 1 == c.L;
         if (last && !want_logits) continue;
         HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, last ? m->final_norm : m->layers[li + 1].in_norm, H, T, c.eps, s));

@@ -62,7 +62,7 @@ struct Model {
     int* dpos = nullptr;                 // position of the step being processed (device)
     float *h = nullptr, *xn = nullptr, *tmp = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *mlp = nullptr;
     float* logits = nullptr; float* part = nullptr; float* bmax = nullptr; int* barg = nullptr;
-    uint16_t* xbf = nullptr;
+    uint16_t* xbf = nullptr; float* xsc = nullptr;
     int* diag = nullptr;
     // sparse
     bool sparse_alloc = false; bool sparse_on = false;
@@ -89,6 +89,7 @@ struct Model {
     int decode_mode = 1;             // 1: persistent kernel when eligible, 0: kernel per op
     MegaArgs mega{};
     LayerDev* mega_layers = nullptr;
+    std::vector<LayerDev> tile_layers;  // host copy of the repacked phases: the prefill GEMMs use them too
     int mega_nwg = 0; size_t mega_lds = 0;
     std::string mega_reason;
     double last_gpu_time = 0;

@@ -1,0 +1,267 @@
+// Prefill GEMM over the repacked decode tiles (DPack): Y[T][rows] = X[T][K] * W^T, 4-bit, bf16
+// scales, f16 operands on v_mfma_f32_16x16x32_f16.
+//
+// Semantics: the reference's prefill tiles (Kernels.swift:785-851, `qgemm`). Precision is the 4-bit
+// GEMM path's (gemm.hip): x is scaled per row by the power of two 2^e that puts max|x| in
+// [2^13, 2^14) and rounded to f16 (x_to_f16_kernel), each weight is f16(fma(s, q, b)), products
+// accumulate in fp32 and the row is scaled back by 2^-e.
+//
+// Why the repacked tiles: a DPack code block is 1 KB of one 16-row tile x 128 k with each lane's 16
+// bytes already in the MFMA A-operand layout (lane (r, kq), dword j: row r, k = 32 j + 8 kq + 0..7),
+// and a scale block is 1 KB of (scale | bias << 16) for 16 rows x 16 groups. Every buffer -> LDS
+// copy therefore reads 1 KB of consecutive bytes; copying the MLX layout instead (16-byte pieces of
+// 32 rows, 4-byte scale words) costs about three times the L1 accesses, which bounded the GEMM.
+//
+// Tile: a 512-thread workgroup owns 128 tokens x 16 DPack tiles (256 rows). Wave (wq, kc) computes
+// the tiles 4 wq .. 4 wq + 3 against all 128 tokens (8 X fragments x 4 W fragments = 32 MFMAs per
+// 32-k step) for the steps 2 kc, 2 kc + 1 of every 128-k block; the two waves of a pair share a
+// SIMD (one issues MFMAs while the other waits on memory) and their partial sums are added through
+// LDS at the end. The X block (128 tokens x 128 k, f16, 16-byte chunks XOR-swizzled by (row & 15))
+// and the 16 code blocks are copied buffer -> LDS (two stages); the scale blocks of a scale group
+// (16 groups) once per group (two buffers). Gated phases (gate rows in tile rows 0-7, up rows in
+// 8-15) finish with SiLU(gate) * up in the epilogue, so the MLP activation is written directly.
+#include "decode.h"
+
+namespace mlxr {
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int PT_M = 128, PT_TILES = 16, PT_KB = 128;
+constexpr int PT_XB = PT_M * 256;                   // X block
+constexpr int PT_CB = PT_TILES * 1024;              // code blocks
+constexpr int PT_STAGE = PT_XB + PT_CB;
+constexpr int PT_NST = 2;
+constexpr int PT_SC = PT_TILES * 1024;              // scale blocks of one scale group
+constexpr int PT_LDS = PT_NST * PT_STAGE + 2 * PT_SC;
+constexpr int PT_RSRC_W3 = 0x00020000;              // raw buffer, 32-bit data format
+
+struct TileGemmArgs {
+    MvPhaseDesc p;
+    const uint16_t* xh; const float* inv; float* y;
+    int ys, T, nT, ntiles;
+};
+
+__device__ __forceinline__ half2_t bf16_half2(uint32_t raw16) {
+    const _Float16 h = (_Float16)__uint_as_float(raw16 << 16);
+    return half2_t{h, h};
+}
+
+template <int GATED>
+__global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t pt_lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wq = wave & 3, kc = wave >> 2;
+    // tile order: XCD x runs workgroups x, x + 8, ...; give it a contiguous run of tiles so that
+    // the workgroups of one XCD share weight tiles in its L2
+    const int g = blockIdx.x, xcd = g & 7, per = a.ntiles >> 3, rem = a.ntiles & 7;
+    const int tile = xcd * per + min(xcd, rem) + (g >> 3);
+    const int ot = tile / a.nT, tt = tile - ot * a.nT;
+    const int t0 = ot * PT_TILES, m0 = tt * PT_M;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int K = a.p.K, FB = a.p.gs >> 3, nb = K / PT_KB, NF = (nb + FB - 1) / FB;
+    const uint32_t tile_bytes = (uint32_t)NF * (FB + 1) * 1024;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.xh, 0, a.T * K * 2, PT_RSRC_W3);
+    // tiles past the matrix read out of range (zeros)
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.p.code, 0, (int)(a.p.tiles * tile_bytes),
+                                                                         PT_RSRC_W3);
+    f32x4_t acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc[i][u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // this wave's copies of block blk: X rows 16 w .. 16 w + 15 (4 x 1 KB), the code blocks of
+    // workgroup tiles 2 w, 2 w + 1, and at a scale group's first block their scale blocks
+    auto issue = [&](int blk) {
+        uint8_t* st = pt_lds + (blk % PT_NST) * PT_STAGE;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int qq = wave * 4 + q, r = 4 * qq + kq;
+            const uint32_t off = (uint32_t)(m0 + r) * (uint32_t)K * 2u + blk * 256 + 16 * (r16 ^ (r & 15));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr_t)(st + qq * 1024), 16, off, 0, 0, 0);
+        }
+        const int f = blk / FB, pos = blk - f * FB + 1;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int tw = 2 * wave + c;
+            const uint32_t base = (uint32_t)(t0 + tw) * tile_bytes + (uint32_t)f * (FB + 1) * 1024 + lane * 16;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(st + PT_XB + tw * 1024), 16, base + pos * 1024, 0, 0, 0);
+            if (pos == 1)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(pt_lds + PT_NST * PT_STAGE + (f & 1) * PT_SC + tw * 1024),
+                                                         16, base, 0, 0, 0);
+        }
+    };
+
+    // this wave's half of block blk: steps j = 2 kc + jj. Step j uses code dword j of the lane's
+    // 16 bytes of each code block (k = 32 j + 8 kq + 0..7) and the X fragment of the same k.
+    auto compute = [&](int blk, int pf) {
+        const uint8_t* st = pt_lds + (blk % PT_NST) * PT_STAGE;
+        const int f = blk / FB, bl = blk - f * FB;
+        const uint8_t* sc = pt_lds + PT_NST * PT_STAGE + (f & 1) * PT_SC;
+        u32x2_t cw[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) cw[u] = *reinterpret_cast<const u32x2_t*>(st + PT_XB + (4 * wq + u) * 1024 + lane * 16 + 8 * kc);
+        // (scale | bias << 16) of row r16, local group gl: lane (r16 >> 2) * 16 + gl, dword r16 & 3
+        half2_t s2[2][4], b2[2][4];
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+            const int gl = ((bl * PT_KB + 32 * (2 * kc + jj)) >> 3) / FB;   // (k within the scale group) / gs
+            const int so = ((r16 >> 2) * 16 + gl) * 16 + (r16 & 3) * 4;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(sc + (4 * wq + u) * 1024 + so);
+                s2[jj][u] = bf16_half2(w & 0xFFFFu);
+                b2[jj][u] = bf16_half2(w >> 16);
+            }
+        }
+        auto dequant = [&](int jj, half8_t* wf) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t wv = cw[u][jj];
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    // (w & 0x000F000F) | 0x64006400 = the f16 pair (1024 + q_p, 1024 + q_p+4)
+                    const uint32_t t = __builtin_amdgcn_bitop3_b32(wv >> (4 * p), 0x000F000Fu, 0x64006400u, 0xEA);
+                    const half2_t q = __builtin_bit_cast(half2_t, t) - half2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+                    const half2_t v = q * s2[jj][u] + b2[jj][u];
+                    wf[u][2 * p] = v[0];
+                    wf[u][2 * p + 1] = v[1];
+                }
+            }
+        };
+        auto xload = [&](int jj, half8_t* xf) {
+            const int j = 2 * kc + jj;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                xf[i] = *reinterpret_cast<const half8_t*>(st + (16 * i + r16) * 256 + 16 * ((4 * j + kq) ^ r16));
+        };
+        half8_t xf[2][8], wf[2][4];
+        xload(0, xf[0]);
+        dequant(0, wf[0]);
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+            __builtin_amdgcn_sched_barrier(0);
+            // three of the next block's copies per step (the memory pipeline takes them while the
+            // pair's other wave issues MFMAs)
+            if (pf >= 0 && jj == 0) issue(pf);
+            if (jj == 0) { xload(1, xf[1]); dequant(1, wf[1]); }
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    acc[i][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[jj][u], xf[jj][i], acc[i][u], 0, 0, 0);
+            if (jj == 0) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+                for (int k = 0; k < 32; k++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    issue(0);
+    for (int blk = 0; blk < nb; blk++) {
+        // this wave's copies of block blk have landed (nothing newer is in flight) ...
+        __builtin_amdgcn_s_waitcnt(0);
+        // ... and every wave's; block blk - 1's stage is no longer read. A bare s_barrier:
+        // __syncthreads' fence adds nothing here.
+        __builtin_amdgcn_s_barrier();
+        compute(blk, blk + 1 < nb ? blk + 1 : -1);
+    }
+    // the pair's partial sums: wave kc = 1 hands its accumulators to wave kc = 0 through LDS
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(pt_lds) + wq * (32 * 4 * 64);
+    if (kc == 1) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                *reinterpret_cast<f32x4_t*>(red + ((i * 4 + u) * 64 + lane) * 4) = acc[i][u];
+    }
+    __syncthreads();
+    if (kc == 1) return;
+    // lane holds, for token m0 + 16 i + r16, rows 4 kq .. 4 kq + 3 of tile t0 + 4 wq + u
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int t = t0 + 4 * wq + u;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int m = m0 + 16 * i + r16;
+            const f32x4_t o = *reinterpret_cast<const f32x4_t*>(red + ((i * 4 + u) * 64 + lane) * 4);
+            const float iv = m < a.T ? a.inv[m] : 0.0f;
+            f32x4_t v = (acc[i][u] + o) * iv;
+            if constexpr (GATED) {
+                // lanes kq < 2: gate rows 8t + 4kq + r; lanes kq >= 2: the matching up rows
+                const int n = 8 * t + 4 * (kq & 1);
+                f32x4_t up;
+#pragma unroll
+                for (int r = 0; r < 4; r++) up[r] = __shfl_xor(v[r], 32);
+                if (kq >= 2 || m >= a.T || n >= a.p.o1) continue;
+                float* yp = a.y + (int64_t)m * a.ys + n;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float gt = v[r], ut = up[r];
+                    if (n + r < a.p.o1) {
+                        if (a.p.bias[0]) gt += bf16_to_f32(a.p.bias[0][n + r]);
+                        if (a.p.bias[1]) ut += bf16_to_f32(a.p.bias[1][n + r]);
+                        yp[r] = (gt / (1.0f + expf(-gt))) * ut;
+                    }
+                }
+            } else {
+                const int n = 16 * t + 4 * kq;
+                if (m >= a.T || n >= a.p.rows) continue;
+                float* yp = a.y + (int64_t)m * a.ys + n;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int nr = n + r;
+                    const int part = nr < a.p.o1 ? 0 : nr < a.p.o1 + a.p.o2 ? 1 : 2;
+                    const int row = nr - (part > 0 ? a.p.o1 : 0) - (part > 1 ? a.p.o2 : 0);
+                    const uint16_t* bp = a.p.bias[part];
+                    if (bp) v[r] += bf16_to_f32(bp[row]);
+                }
+                if (n + 4 <= a.p.rows && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) *reinterpret_cast<f32x4_t*>(yp) = v;
+                else
+                    for (int r = 0; r < 4 && n + r < a.p.rows; r++) yp[r] = v[r];
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool tile_gemm_supported(const MvPhaseDesc& p) {
+    return p.code && (p.gs == 32 || p.gs == 64) && p.K % PT_KB == 0 && p.tiles > 0;
+}
+
+hipError_t launch_tile_gemm(const MvPhaseDesc& p, const uint16_t* xh, const float* inv, int T, float* y, int ys,
+                            hipStream_t s) {
+    if (!tile_gemm_supported(p) || T < 1) return hipErrorInvalidValue;
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute((const void*)tile_gemm_kernel<0>, hipFuncAttributeMaxDynamicSharedMemorySize, PT_LDS) != hipSuccess ||
+            hipFuncSetAttribute((const void*)tile_gemm_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, PT_LDS) != hipSuccess)
+            return hipErrorInvalidValue;
+        attr = true;
+    }
+    TileGemmArgs a;
+    a.p = p; a.xh = xh; a.inv = inv; a.y = y; a.ys = ys; a.T = T;
+    a.nT = (T + PT_M - 1) / PT_M;
+    const int nO = (p.tiles + PT_TILES - 1) / PT_TILES;
+    a.ntiles = a.nT * nO;
+    if (p.gated) hipLaunchKernelGGL(tile_gemm_kernel<1>, dim3(a.ntiles), dim3(512), PT_LDS, s, a);
+    else hipLaunchKernelGGL(tile_gemm_kernel<0>, dim3(a.ntiles), dim3(512), PT_LDS, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace mlxr

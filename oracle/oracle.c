@@ -108,33 +108,79 @@ void orc_dequant_row(const orc_qlinear* l, int r, float* out) {
     }
     for (int k = 0; k < l->K; k++) out[k] = (float)code_at(row, k, l->bits) * s[k / l->gs] + b[k / l->gs];
 }
-static void qlinear_impl(const orc_qlinear* l, const float* x, int T, float* y, int round_bf16) {
+/* Round a double to the nearest f16 value (ties to even; subnormals kept), returned as double. */
+double orc_round_f16_d(double v) {
+    if (v == 0.0 || !isfinite(v)) return v;
+    int e; frexp(v, &e);                       /* |v| in [2^(e-1), 2^e) */
+    const int q = e - 11 < -24 ? -24 : e - 11; /* ulp exponent: 11 significant bits, floor 2^-24 */
+    const double r = ldexp(nearbyint(ldexp(v, -q)), q);
+    return fabs(r) > 65504.0 ? copysign(INFINITY, v) : r;
+}
+/* The 4-bit prefill GEMM's precision (mlx-runner_amd/csrc/gemm.hip, qgemm4_kernel): each token row
+ * is scaled by the power of two 2^e that puts max|x| in [2^13, 2^14) and rounded to f16; each weight
+ * is f16(fma(s16, q, b16)) with s, b converted to f16; products accumulate exactly here (f32 on the
+ * GPU) and the row is scaled back by 2^-e. */
+static int f16_mode(const orc_qlinear* l) {
+    return l->bits == 4 && (l->gs == 32 || l->gs == 64 || l->gs == 128) && (l->K / l->gs) % 2 == 0;
+}
+static void qlinear_impl(const orc_qlinear* l, const float* x, int T, float* y, int mode) {
     float* xr = NULL;
-    if (round_bf16) {
+    double* inv = NULL;
+    if (mode == 1) {
         xr = (float*)malloc((size_t)T * l->K * sizeof(float));
         for (int64_t i = 0; i < (int64_t)T * l->K; i++) xr[i] = orc_round_bf16(x[i]);
         x = xr;
+    } else if (mode == 2) {
+        xr = (float*)malloc((size_t)T * l->K * sizeof(float));
+        inv = (double*)malloc((size_t)T * sizeof(double));
+        for (int t = 0; t < T; t++) {
+            const float* xt = x + (int64_t)t * l->K;
+            float mx = 0.0f;
+            for (int k = 0; k < l->K; k++) mx = fmaxf(mx, fabsf(xt[k]));
+            int e = 0;
+            if (mx > 0.0f && mx <= 3.0e38f) { frexpf(mx, &e); e = 14 - e; e = e < -126 ? -126 : (e > 126 ? 126 : e); }
+            inv[t] = ldexp(1.0, -e);
+            for (int k = 0; k < l->K; k++) xr[(int64_t)t * l->K + k] = (float)orc_round_f16_d((double)ldexpf(xt[k], e));
+        }
+        x = xr;
     }
+    const int groups = l->K / l->gs;
     #pragma omp parallel
     {
         float* w = (float*)malloc((size_t)l->K * sizeof(float));
         #pragma omp for schedule(static)
         for (int o = 0; o < l->O; o++) {
-            orc_dequant_row(l, o, w);
-            if (round_bf16) for (int k = 0; k < l->K; k++) w[k] = orc_round_bf16(w[k]);
+            if (mode == 2) {
+                const uint8_t* row = l->w + (int64_t)o * (l->K / 2);
+                for (int k = 0; k < l->K; k++) {
+                    const double sg = orc_round_f16_d(l->scales[(int64_t)o * groups + k / l->gs]);
+                    const double bg = orc_round_f16_d(l->biases[(int64_t)o * groups + k / l->gs]);
+                    const int q = (row[k >> 1] >> ((k & 1) * 4)) & 15;
+                    w[k] = (float)orc_round_f16_d(sg * q + bg);
+                }
+            } else {
+                orc_dequant_row(l, o, w);
+                if (mode == 1) for (int k = 0; k < l->K; k++) w[k] = orc_round_bf16(w[k]);
+            }
             for (int t = 0; t < T; t++) {
                 const float* xt = x + (int64_t)t * l->K;
                 double acc = 0;
                 for (int k = 0; k < l->K; k++) acc += (double)w[k] * (double)xt[k];
+                if (mode == 2) acc *= inv[t];
                 y[(int64_t)t * l->O + o] = (float)acc + (l->bias ? l->bias[o] : 0.0f);
             }
         }
         free(w);
     }
     free(xr);
+    free(inv);
 }
 void orc_qlinear_f64(const orc_qlinear* l, const float* x, int T, float* y) { qlinear_impl(l, x, T, y, 0); }
 void orc_qlinear_bf16(const orc_qlinear* l, const float* x, int T, float* y) { qlinear_impl(l, x, T, y, 1); }
+void orc_qlinear_f16(const orc_qlinear* l, const float* x, int T, float* y) { qlinear_impl(l, x, T, y, 2); }
+/* The GPU GEMM path (T > 8 tokens): f16 operands for 4-bit with gs 32/64/128 and an even number of
+ * groups per row, else bf16. */
+void orc_qlinear_prefill(const orc_qlinear* l, const float* x, int T, float* y) { qlinear_impl(l, x, T, y, f16_mode(l) ? 2 : 1); }
 
 /* ------------------------------------------------------------------ norms, RoPE */
 void orc_rms_norm(const float* x, float* y, const float* w, int dim, int rows, float eps) {
@@ -597,7 +643,7 @@ int orc_model_set_kv(orc_model* m, int layer, const float* k, const float* v, in
 }
 
 static void lin_apply(const olin* l, const float* x, int T, float* y, int bf16) {
-    if (bf16) orc_qlinear_bf16(&l->l, x, T, y); else orc_qlinear_f64(&l->l, x, T, y);
+    if (bf16) orc_qlinear_prefill(&l->l, x, T, y); else orc_qlinear_f64(&l->l, x, T, y);
 }
 /* Transformer.swift:1323-1584 for qwen3 / qwen2 / llama layers (no sliding window, no gates). */
 int orc_forward(orc_model* m, const int32_t* tokens, int n, int offset, int small_t, float* logits) {

@@ -50,6 +50,9 @@ typedef struct {
 void orc_qlinear_f64(const orc_qlinear* l, const float* x, int T, float* y);
 /* The same product with bf16-rounded operands (the prefill GEMM's declared precision). */
 void orc_qlinear_bf16(const orc_qlinear* l, const float* x, int T, float* y);
+void orc_qlinear_f16(const orc_qlinear* l, const float* x, int T, float* y);
+void orc_qlinear_prefill(const orc_qlinear* l, const float* x, int T, float* y);
+double orc_round_f16_d(double v);
 /* One row of dequantized weights (fp32 `s*q+b`, SieveImport.swift:108). */
 void orc_dequant_row(const orc_qlinear* l, int row, float* out);
 

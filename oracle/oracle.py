@@ -29,6 +29,8 @@ def _load():
         "orc_f16_to_f32": (F, [C.c_uint16]), "orc_f32_to_f16": (C.c_uint16, [F]), "orc_round_bf16": (F, [F]),
         "orc_pack": (None, [P, C.c_int64, I, P]), "orc_unpack": (None, [P, C.c_int64, I, P]),
         "orc_qlinear_f64": (None, [P, P, I, P]), "orc_qlinear_bf16": (None, [P, P, I, P]),
+        "orc_qlinear_f16": (None, [P, P, I, P]), "orc_qlinear_prefill": (None, [P, P, I, P]),
+        "orc_round_f16_d": (C.c_double, [C.c_double]),
         "orc_dequant_row": (None, [P, I, P]),
         "orc_rms_norm": (None, [P, P, P, I, I, F]), "orc_inv_freq": (None, [C.c_double, I, P]),
         "orc_rope": (None, [P, I, I, I, I, P]), "orc_silu_mul": (F, [F, F]),
@@ -105,6 +107,21 @@ class QMatrix:
         x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.K)
         y = np.zeros((x.shape[0], self.O), np.float32)
         lib.orc_qlinear_bf16(C.byref(self.s), x.ctypes.data, x.shape[0], y.ctypes.data)
+        return y
+
+    def matmul_f16(self, x):
+        """4-bit prefill GEMM precision: per-row power-of-two scaled f16 x, f16(fma(s, q, b)) weights."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.K)
+        y = np.zeros((x.shape[0], self.O), np.float32)
+        lib.orc_qlinear_f16(C.byref(self.s), x.ctypes.data, x.shape[0], y.ctypes.data)
+        return y
+
+    def matmul_prefill(self, x):
+        """The GEMM path's declared precision for this matrix (f16 for 4-bit gs 32/64/128 with K / gs
+        even, else bf16)."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.K)
+        y = np.zeros((x.shape[0], self.O), np.float32)
+        lib.orc_qlinear_prefill(C.byref(self.s), x.ctypes.data, x.shape[0], y.ctypes.data)
         return y
 
     def dequant_row(self, r):

@@ -113,20 +113,83 @@ def qgemm(mlxr, fx, x):
     return dy.numpy()
 
 
-@pytest.mark.parametrize("bits", [3, 4, 8])
-def test_qgemm_prefill_tiles(gpu, bits):
+@pytest.mark.parametrize("bits,gs", [(3, 32), (4, 32), (4, 64), (4, 128), (8, 32)])
+def test_qgemm_prefill_tiles(gpu, bits, gs):
     """prefillTilesMatchReference shapes (KernelTests.swift:150-164), against the oracle in the
-    GEMM's declared precision (bf16 operands, fp32/f64 accumulation)."""
-    for T, O, K in ((64, 41, 1088), (128, 41, 576), (517, 41, 576), (96, 2050, 576), (128, 2050, 576), (517, 520, 576)):
-        fx = QuantFixture(O, K, bits, 32, seed=T + O, fast=True)
+    GEMM's declared precision: f16 operands for 4-bit (x scaled per row by a power of two,
+    weights f16(fma(s, q, b))) when K / gs is even, bf16 operands otherwise (K = 1088 at gs 64, and
+    K / 128 = 9 exercise that fallback); fp32/f64 accumulation."""
+    shapes = ((64, 41, 1088), (128, 41, 576), (517, 41, 576), (96, 2050, 576), (128, 2050, 576), (517, 520, 576))
+    if gs == 128:
+        shapes = ((64, 41, 1152), (517, 41, 640), (128, 2050, 640), (300, 520, 1152))
+    for T, O, K in shapes:
+        fx = QuantFixture(O, K, bits, gs, seed=T + O, fast=True)
         x = np.random.default_rng(T * 7 + bits).uniform(-1, 1, (T, K)).astype(np.float32)
         got = qgemm(gpu, fx, x)
-        assert max_rel_err(got, fx.oracle(oracle).matmul_bf16(x)) < TOL, (T, O, K)
+        assert max_rel_err(got, fx.oracle(oracle).matmul_prefill(x)) < TOL, (T, O, K)
         # distance to the fp32-operand product (the reference's precision): rounding x and each
-        # dequantized weight to bf16 changes each product by at most 2^-8 relative, so
-        # |got - exact| <= 2^-8 * sum_k |w_k x_k| (+ fp32 accumulation slack)
-        bound = 2.0 ** -8 * (np.abs(x).astype(np.float64) @ np.abs(fx.dense()).astype(np.float64).T) + 1e-4
+        # dequantized weight changes each product by at most 2^-10 (f16) / 2^-8 (bf16) relative,
+        # so |got - exact| <= that * sum_k |w_k x_k| (+ fp32 accumulation slack)
+        rel = 2.0 ** -10 if bits == 4 and (K // gs) % 2 == 0 else 2.0 ** -8
+        bound = rel * (np.abs(x).astype(np.float64) @ np.abs(fx.dense()).astype(np.float64).T) + 1e-4
         assert np.all(np.abs(got - fx.oracle(oracle).matmul_f64(x)) <= bound)
+
+
+def test_qgemm_row_scaling(gpu):
+    """4-bit GEMM on rows of very different magnitude (the per-row power-of-two scaling keeps each
+    row's f16 precision), a zero row, bias, and f16 scales."""
+    O, K, T = 300, 1024, 40
+    for st in ("bf16", "f16"):
+        fx = QuantFixture(O, K, 4, 64, st=st, seed=5, with_bias=True, fast=True)
+        x = np.random.default_rng(9).normal(0, 1, (T, K)).astype(np.float32)
+        x *= (10.0 ** np.linspace(-6, 6, T)).astype(np.float32)[:, None]
+        x[7] = 0.0
+        got = qgemm(gpu, fx, x)
+        ref = fx.oracle(oracle).matmul_prefill(x)
+        scale = np.maximum(np.abs(ref).max(axis=1, keepdims=True), 1e-30)
+        assert np.all(np.abs(got - ref) / scale < 1e-5), st
+        assert np.all(np.isfinite(got))
+
+
+def qgemm_tiles(mlxr, fxs, x, gated=False):
+    T = x.shape[0]
+    qm = (mlxr.QMat * len(fxs))(*[f.device(mlxr) for f in fxs])
+    cols = fxs[0].O if gated else sum(f.O for f in fxs)
+    dx = mlxr.DeviceArray.from_numpy(x)
+    dy = mlxr.DeviceArray.from_numpy(np.full((T, cols), np.nan, np.float32))
+    mlxr.check(mlxr.lib.mlxr_k_qgemm_tiles(qm, len(fxs), fxs[0].K, fxs[0].gs, int(gated), T, dx.ptr, x.shape[1], dy.ptr, cols))
+    mlxr.synchronize()
+    return dy.numpy()
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_qgemm_tiles(gpu, gs):
+    """The prefill GEMM over repacked tiles (model prefill's path for 4-bit bf16-scale models):
+    fused parts [A|B|C] with per-part bias (or none) and ragged row counts, against the oracle's 4-bit GEMM
+    precision per part; T not a multiple of the 128-token tile."""
+    K = 512
+    for T in (9, 130, 300):
+        fxs = [QuantFixture(O, K, 4, gs, seed=O + T, with_bias=T != 130, fast=True) for O in (264, 40, 88)]
+        x = np.random.default_rng(T).normal(0, 1, (T, K)).astype(np.float32)
+        got = qgemm_tiles(gpu, fxs, x)
+        ref = np.concatenate([f.oracle(oracle).matmul_f16(x) for f in fxs], axis=1)
+        assert max_rel_err(got, ref) < TOL, T
+        assert np.max(np.abs(got - ref)) < 1e-4, T
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_qgemm_tiles_gated(gpu, gs):
+    """Gate|up on the repacked tiles with SiLU(gate) * up in the epilogue (silu_mul,
+    Kernels.swift:2004-2013) against the oracle's GEMM precision and orc_silu_mul."""
+    K, I = 768, 200
+    for T in (17, 257):
+        g, u = (QuantFixture(I, K, 4, gs, seed=s, fast=True) for s in (1 + T, 2 + T))
+        x = np.random.default_rng(T).normal(0, 1, (T, K)).astype(np.float32)
+        got = qgemm_tiles(gpu, [g, u], x, gated=True)
+        gr, ur = g.oracle(oracle).matmul_f16(x), u.oracle(oracle).matmul_f16(x)
+        ref = (gr / (1.0 + np.exp(-gr.astype(np.float64)))).astype(np.float32) * ur
+        assert np.all(np.isfinite(got))
+        assert max_rel_err(got, ref) < TOL, T
 
 
 def test_qgemm_batch_invariant(gpu):

@@ -67,6 +67,51 @@ def test_qlinear_against_numpy(bits, gs):
     assert np.allclose(q.matmul_bf16(x), xb @ wb.T, rtol=1e-6, atol=1e-6)
 
 
+def test_round_f16_matches_numpy():
+    """orc_round_f16_d against numpy's correctly rounded double -> half conversion: normals, ties,
+    subnormals, overflow."""
+    rng = np.random.default_rng(0)
+    v = np.concatenate([rng.normal(0, 1, 4000), rng.normal(0, 1e-5, 2000), rng.normal(0, 1e4, 1000),
+                        (np.arange(-2048, 2048) + 0.5) * 2.0 ** -3,        # exact ties at ulp 2^-2 .. 2^-3
+                        np.array([0.0, -0.0, 65504.0, 65519.9, 65520.0, 1e6, 2.0 ** -25, 3 * 2.0 ** -25])])
+    got = np.array([oracle.lib.orc_round_f16_d(float(a)) for a in v])
+    with np.errstate(over="ignore"):
+        ref = v.astype(np.float16).astype(np.float64)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_qlinear_f16_precision(gs):
+    """The 4-bit GEMM precision against a numpy restatement (numpy's own f16 rounding) and the
+    rounding bound to the exact product: each operand is within 2^-11 relative of its exact value
+    (x scaled so that f16 keeps 11 bits), so |y - exact| <= 2^-10 * sum|w x| (+ subnormal slack)."""
+    K, O, T = 512, 40, 5
+    fx = QuantFixture(O, K, 4, gs, seed=gs, fast=True)
+    x = np.random.default_rng(gs).normal(0, 3, (T, K)).astype(np.float32)
+    x[1] *= 1e-3
+    x[2, :] = 0.0
+    x[3] *= 300.0
+    q = fx.oracle(oracle)
+    got = q.matmul_f16(x)
+    g = np.repeat(np.arange(K // gs), gs)
+    s16 = fx.scales.astype(np.float16).astype(np.float64)[:, g]
+    b16 = fx.biases.astype(np.float16).astype(np.float64)[:, g]
+    w16 = (s16 * fx.codes + b16).astype(np.float16).astype(np.float64)
+    mx = np.abs(x).max(axis=1)
+    e = np.where(mx > 0, 14 - np.frexp(mx)[1], 0)
+    xh = (x.astype(np.float64) * 2.0 ** e[:, None]).astype(np.float16).astype(np.float64)
+    ref = (xh @ w16.T) * 2.0 ** -e[:, None]
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-9)
+    assert np.all(np.abs(xh * 2.0 ** -e[:, None]).max(axis=1) <= mx * (1 + 2.0 ** -11))
+    exact = x.astype(np.float64) @ fx.dense().astype(np.float64).T
+    bound = 2.0 ** -10 * (np.abs(x).astype(np.float64) @ np.abs(fx.dense()).astype(np.float64).T) + 1e-6
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.array_equal(got[2], np.zeros(O, np.float32))
+    assert np.array_equal(q.matmul_prefill(x), got)
+    fx3 = QuantFixture(8, 128, 3, 32, seed=1, fast=True)
+    assert np.array_equal(fx3.oracle(oracle).matmul_prefill(x[:, :128]), fx3.oracle(oracle).matmul_bf16(x[:, :128]))
+
+
 def test_qlinear_special_cases():
     """All codes 0: y = sum_g b_g * sum(x in g); scales 0 and biases 0: y = 0; bias added per row."""
     K, O, gs = 128, 4, 64
