@@ -333,7 +333,8 @@ def run_flash(mlxr, q, kc, vc, nH, nKV, offset, T, scale):
     return out.numpy().reshape(T, nH, D)
 
 
-@pytest.mark.parametrize("nH,nKV,offset,T", [(4, 2, 0, 1), (4, 2, 0, 45), (32, 8, 37, 200), (40, 8, 64, 130), (16, 2, 5, 96)])
+@pytest.mark.parametrize("nH,nKV,offset,T", [(4, 2, 0, 1), (4, 2, 0, 45), (32, 8, 37, 200), (40, 8, 64, 130), (16, 2, 5, 96),
+                                            (8, 8, 0, 97), (12, 4, 3, 350)])
 def test_flash_prefill(gpu, nH, nKV, offset, T):
     """flash_prefill (Kernels.swift:1839-2000): token t of the chunk (position offset + t) attends keys
     0..offset + t; every token's output against the reference attention (oracle), and rows past the
