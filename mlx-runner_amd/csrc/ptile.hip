@@ -13,13 +13,12 @@
 // 32 rows, 4-byte scale words) costs about three times the L1 accesses, which bounded the GEMM.
 //
 // Tile: a 512-thread workgroup owns 128 tokens x 16 DPack tiles (256 rows). Wave (wq, kc) computes
-// the tiles 4 wq .. 4 wq + 3 against all 128 tokens (8 X fragments x 4 W fragments = 32 MFMAs per
-// 32-k step) for the steps 2 kc, 2 kc + 1 of every 128-k block; the two waves of a pair share a
-// SIMD (one issues MFMAs while the other waits on memory) and their partial sums are added through
-// LDS at the end. The X block (128 tokens x 128 k, f16, 16-byte chunks XOR-swizzled by (row & 15))
-// and the 16 code blocks are copied buffer -> LDS (two stages); the scale blocks of a scale group
-// (16 groups) once per group (two buffers). Gated phases (gate rows in tile rows 0-7, up rows in
-// 8-15) finish with SiLU(gate) * up in the epilogue, so the MLP activation is written directly.
+// the tiles 4 wq + 2 kc, + 1 against all 128 tokens (8 X fragments x 2 W fragments = 16 MFMAs per
+// 32-k step); two waves share each SIMD, so one issues MFMAs while the other waits on memory or
+// dequantizes. The X block (128 tokens x 128 k, f16, 16-byte chunks XOR-swizzled by (row & 15),
+// read by all eight waves) and the 16 code blocks are copied buffer -> LDS (two stages); the scale
+// blocks of a scale group (16 groups) once per group (two buffers). Gated phases (gate rows in tile rows 0-7, up rows in 8-15) finish with
+// SiLU(gate) * up in the epilogue, so the MLP activation is written directly.
 #include "decode.h"
 
 namespace mlxr {
@@ -28,7 +27,7 @@ namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t q4u4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -71,11 +70,11 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
     // tiles past the matrix read out of range (zeros)
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.p.code, 0, (int)(a.p.tiles * tile_bytes),
                                                                          PT_RSRC_W3);
-    f32x4_t acc[8][4];
+    f32x4_t acc[8][2];
 #pragma unroll
     for (int i = 0; i < 8; i++)
 #pragma unroll
-        for (int u = 0; u < 4; u++) acc[i][u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int u = 0; u < 2; u++) acc[i][u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     // this wave's copies of block blk: X rows 16 w .. 16 w + 15 (4 x 1 KB), the code blocks of
     // workgroup tiles 2 w, 2 w + 1, and at a scale group's first block their scale blocks
@@ -99,69 +98,65 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
         }
     };
 
-    // this wave's half of block blk: steps j = 2 kc + jj. Step j uses code dword j of the lane's
-    // 16 bytes of each code block (k = 32 j + 8 kq + 0..7) and the X fragment of the same k.
+    // one 128-k block: step j uses code dword j of the lane's 16 bytes of each code block
+    // (k = 32 j + 8 kq + 0..7) and the X fragment of the same k; step j + 1's X fragments and
+    // dequantized W are produced while step j's MFMAs run.
     auto compute = [&](int blk, int pf) {
         const uint8_t* st = pt_lds + (blk % PT_NST) * PT_STAGE;
         const int f = blk / FB, bl = blk - f * FB;
         const uint8_t* sc = pt_lds + PT_NST * PT_STAGE + (f & 1) * PT_SC;
-        u32x2_t cw[4];
+        q4u4_t cw[2];
 #pragma unroll
-        for (int u = 0; u < 4; u++) cw[u] = *reinterpret_cast<const u32x2_t*>(st + PT_XB + (4 * wq + u) * 1024 + lane * 16 + 8 * kc);
-        // (scale | bias << 16) of row r16, local group gl: lane (r16 >> 2) * 16 + gl, dword r16 & 3
-        half2_t s2[2][4], b2[2][4];
+        for (int u = 0; u < 2; u++) cw[u] = *reinterpret_cast<const q4u4_t*>(st + PT_XB + (4 * wq + 2 * kc + u) * 1024 + lane * 16);
+        half2_t s2[4][2], b2[4][2];
 #pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
-            const int gl = ((bl * PT_KB + 32 * (2 * kc + jj)) >> 3) / FB;   // (k within the scale group) / gs
+        for (int j = 0; j < 4; j++) {
+            const int gl = ((bl * PT_KB + 32 * j) >> 3) / FB;   // (k within the scale group) / gs
             const int so = ((r16 >> 2) * 16 + gl) * 16 + (r16 & 3) * 4;
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(sc + (4 * wq + u) * 1024 + so);
-                s2[jj][u] = bf16_half2(w & 0xFFFFu);
-                b2[jj][u] = bf16_half2(w >> 16);
+            for (int u = 0; u < 2; u++) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(sc + (4 * wq + 2 * kc + u) * 1024 + so);
+                s2[j][u] = bf16_half2(w & 0xFFFFu);
+                b2[j][u] = bf16_half2(w >> 16);
             }
         }
-        auto dequant = [&](int jj, half8_t* wf) {
+        auto dequant = [&](int j, half8_t* wf) {
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const uint32_t wv = cw[u][jj];
+            for (int u = 0; u < 2; u++) {
+                const uint32_t wv = cw[u][j];
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
                     // (w & 0x000F000F) | 0x64006400 = the f16 pair (1024 + q_p, 1024 + q_p+4)
                     const uint32_t t = __builtin_amdgcn_bitop3_b32(wv >> (4 * p), 0x000F000Fu, 0x64006400u, 0xEA);
                     const half2_t q = __builtin_bit_cast(half2_t, t) - half2_t{(_Float16)1024.0f, (_Float16)1024.0f};
-                    const half2_t v = q * s2[jj][u] + b2[jj][u];
+                    const half2_t v = q * s2[j][u] + b2[j][u];
                     wf[u][2 * p] = v[0];
                     wf[u][2 * p + 1] = v[1];
                 }
             }
         };
-        auto xload = [&](int jj, half8_t* xf) {
-            const int j = 2 * kc + jj;
+        auto xload = [&](int j, half8_t* xf) {
 #pragma unroll
             for (int i = 0; i < 8; i++)
                 xf[i] = *reinterpret_cast<const half8_t*>(st + (16 * i + r16) * 256 + 16 * ((4 * j + kq) ^ r16));
         };
-        half8_t xf[2][8], wf[2][4];
+        half8_t xf[2][8], wf[2][2];
         xload(0, xf[0]);
         dequant(0, wf[0]);
 #pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
+        for (int j = 0; j < 4; j++) {
             __builtin_amdgcn_sched_barrier(0);
-            // three of the next block's copies per step (the memory pipeline takes them while the
-            // pair's other wave issues MFMAs)
-            if (pf >= 0 && jj == 0) issue(pf);
-            if (jj == 0) { xload(1, xf[1]); dequant(1, wf[1]); }
+            if (pf >= 0 && j == 0) issue(pf);
+            if (j < 3) { xload(j + 1, xf[(j + 1) & 1]); dequant(j + 1, wf[(j + 1) & 1]); }
 #pragma unroll
             for (int i = 0; i < 8; i++)
 #pragma unroll
-                for (int u = 0; u < 4; u++)
-                    acc[i][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[jj][u], xf[jj][i], acc[i][u], 0, 0, 0);
-            if (jj == 0) {
-                __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);
+                for (int u = 0; u < 2; u++)
+                    acc[i][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j & 1][u], xf[j & 1][i], acc[i][u], 0, 0, 0);
+            if (j < 3) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-                for (int k = 0; k < 32; k++) {
+                for (int k = 0; k < 16; k++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
                 }
@@ -179,28 +174,15 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
         __builtin_amdgcn_s_barrier();
         compute(blk, blk + 1 < nb ? blk + 1 : -1);
     }
-    // the pair's partial sums: wave kc = 1 hands its accumulators to wave kc = 0 through LDS
-    __syncthreads();
-    float* red = reinterpret_cast<float*>(pt_lds) + wq * (32 * 4 * 64);
-    if (kc == 1) {
+    // lane holds, for token m0 + 16 i + r16, rows 4 kq .. 4 kq + 3 of tile t0 + 4 wq + 2 kc + u
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-                *reinterpret_cast<f32x4_t*>(red + ((i * 4 + u) * 64 + lane) * 4) = acc[i][u];
-    }
-    __syncthreads();
-    if (kc == 1) return;
-    // lane holds, for token m0 + 16 i + r16, rows 4 kq .. 4 kq + 3 of tile t0 + 4 wq + u
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int t = t0 + 4 * wq + u;
+    for (int u = 0; u < 2; u++) {
+        const int t = t0 + 4 * wq + 2 * kc + u;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int m = m0 + 16 * i + r16;
-            const f32x4_t o = *reinterpret_cast<const f32x4_t*>(red + ((i * 4 + u) * 64 + lane) * 4);
             const float iv = m < a.T ? a.inv[m] : 0.0f;
-            f32x4_t v = (acc[i][u] + o) * iv;
+            f32x4_t v = acc[i][u] * iv;
             if constexpr (GATED) {
                 // lanes kq < 2: gate rows 8t + 4kq + r; lanes kq >= 2: the matching up rows
                 const int n = 8 * t + 4 * (kq & 1);
