@@ -65,6 +65,11 @@ hipError_t launch_rms_norm(const float* x, float* y, const float* w, int dim, in
                            hipStream_t s);
 hipError_t launch_add_rms_norm(float* h, const float* r, float* y, const float* w, int dim, int rows, float eps,
                                hipStream_t s);
+// The same with the output in the 4-bit GEMM's f16 operand format (launch_x_to_f16's xh / inv).
+hipError_t launch_rms_norm_f16(const float* x, const float* w, int dim, int rows, int row_stride, float eps, uint16_t* xh,
+                               float* inv, hipStream_t s);
+hipError_t launch_add_rms_norm_f16(float* h, const float* r, const float* w, int dim, int rows, float eps, uint16_t* xh,
+                                   float* inv, hipStream_t s);
 
 // Fused post-projection: per-head q/k RMSNorm, RoPE, q in place, K/V appended to the bf16 paged cache.
 struct QkvPostArgs {

@@ -80,6 +80,79 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, float* y,
     }
 }
 
+// RMSNorm (optionally after h += r) whose output is the 4-bit GEMM's f16 operand instead of fp32:
+// the normalised row (the same fp32 values rms_norm_kernel stores) scaled by the power of two that
+// puts its max |y| in [2^13, 2^14), rounded to f16, each 8-group stored as 0,4,1,5,2,6,3,7;
+// inv[row] = the inverse scale (x_to_f16_kernel's format).
+__global__ __launch_bounds__(256) void rms_norm_f16_kernel(const float* x, const float* w, int dim, int row_stride,
+                                                           float eps, int add, float* h, const float* r, uint16_t* xh,
+                                                           float* invs) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, ng = dim >> 3;
+    float ss = 0.0f;
+    const float* xr = (add ? h : x) + (int64_t)row * row_stride;
+    for (int gi = threadIdx.x; gi < ng; gi += 256) {
+        float4 a = *reinterpret_cast<const float4*>(xr + 8 * gi), b = *reinterpret_cast<const float4*>(xr + 8 * gi + 4);
+        if (add) {
+            const float* rr = r + (int64_t)row * row_stride + 8 * gi;
+            const float4 ua = *reinterpret_cast<const float4*>(rr), ub = *reinterpret_cast<const float4*>(rr + 4);
+            a.x += ua.x; a.y += ua.y; a.z += ua.z; a.w += ua.w;
+            b.x += ub.x; b.y += ub.y; b.z += ub.z; b.w += ub.w;
+            float* hr = h + (int64_t)row * row_stride + 8 * gi;
+            *reinterpret_cast<float4*>(hr) = a;
+            *reinterpret_cast<float4*>(hr + 4) = b;
+        }
+        ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
+    }
+    ss = block_sum_256(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    auto norm8 = [&](int gi, float* o) {
+        const float4 a = *reinterpret_cast<const float4*>(xr + 8 * gi), b = *reinterpret_cast<const float4*>(xr + 8 * gi + 4);
+        const float4 wa = *reinterpret_cast<const float4*>(w + 8 * gi), wb = *reinterpret_cast<const float4*>(w + 8 * gi + 4);
+        o[0] = a.x * inv * wa.x; o[1] = a.y * inv * wa.y; o[2] = a.z * inv * wa.z; o[3] = a.w * inv * wa.w;
+        o[4] = b.x * inv * wb.x; o[5] = b.y * inv * wb.y; o[6] = b.z * inv * wb.z; o[7] = b.w * inv * wb.w;
+    };
+    float mx = 0.0f;
+    for (int gi = threadIdx.x; gi < ng; gi += 256) {
+        float o[8];
+        norm8(gi, o);
+        for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(o[e]));
+    }
+    __syncthreads();   // red is reused
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e2 = 0;
+    if (mx > 0.0f && mx <= 3.0e38f) { frexpf(mx, &e2); e2 = 14 - e2; e2 = e2 < -126 ? -126 : (e2 > 126 ? 126 : e2); }
+    const float sc = ldexpf(1.0f, e2);
+    if (threadIdx.x == 0) invs[row] = ldexpf(1.0f, -e2);
+    for (int gi = threadIdx.x; gi < ng; gi += 256) {
+        float o[8];
+        norm8(gi, o);
+        uint4 q;
+        q.x = (uint32_t)f32_to_f16(o[0] * sc) | ((uint32_t)f32_to_f16(o[4] * sc) << 16);
+        q.y = (uint32_t)f32_to_f16(o[1] * sc) | ((uint32_t)f32_to_f16(o[5] * sc) << 16);
+        q.z = (uint32_t)f32_to_f16(o[2] * sc) | ((uint32_t)f32_to_f16(o[6] * sc) << 16);
+        q.w = (uint32_t)f32_to_f16(o[3] * sc) | ((uint32_t)f32_to_f16(o[7] * sc) << 16);
+        reinterpret_cast<uint4*>(xh + (int64_t)row * dim)[gi] = q;
+    }
+}
+
+hipError_t launch_rms_norm_f16(const float* x, const float* w, int dim, int rows, int row_stride, float eps, uint16_t* xh,
+                               float* inv, hipStream_t s) {
+    if (dim % 8 || row_stride % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rms_norm_f16_kernel, dim3(rows), dim3(256), 0, s, x, w, dim, row_stride, eps, 0, (float*)nullptr,
+                       (const float*)nullptr, xh, inv);
+    return hipGetLastError();
+}
+hipError_t launch_add_rms_norm_f16(float* h, const float* r, const float* w, int dim, int rows, float eps, uint16_t* xh,
+                                   float* inv, hipStream_t s) {
+    if (dim % 8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rms_norm_f16_kernel, dim3(rows), dim3(256), 0, s, (const float*)h, w, dim, dim, eps, 1, h, r, xh, inv);
+    return hipGetLastError();
+}
+
 hipError_t launch_rms_norm(const float* x, float* y, const float* w, int dim, int rows, int row_stride, float eps,
                            hipStream_t s) {
     hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, s, x, y, w, dim, row_stride, eps, 0, (float*)nullptr,

@@ -657,9 +657,10 @@ int encode_decode(Model* m, const mlxr_sample_params* sp, bool sparse, bool logi
 
 // A batch of T tokens (2..max_batch) at positions *dpos .. *dpos + T - 1 (prefill chunk / verify).
 // all_logits: logits of every row ([T][V], T <= 8); else of the last row only.
-// Prefill GEMM over a repacked phase: the f16 pre-pass of x, then the tile GEMM.
+// Prefill GEMM over a repacked phase: the f16 pre-pass of x (x == nullptr: the fused norm already
+// wrote m->xbf / m->xsc), then the tile GEMM.
 int project_tiles(Model* m, const MvPhaseDesc& p, const float* x, int xs, float* y, int ys, int T) {
-    HIPCHECK(launch_x_to_f16(x, xs, p.K, T, m->xbf, m->xsc, m->stream));
+    if (x) HIPCHECK(launch_x_to_f16(x, xs, p.K, T, m->xbf, m->xsc, m->stream));
     HIPCHECK(launch_tile_gemm(p, m->xbf, m->xsc, T, y, ys, m->stream));
     return MLXR_OK;
 }
@@ -672,12 +673,13 @@ int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
     // in the gate|up epilogue); verify batches (T <= 8) keep the small-batch kernels
     const bool tiles = T > 8 && (int)m->tile_layers.size() == c.L;
     HIPCHECK(launch_qembed(m->embed.m, H, m->embed.bits, m->embed.gs, m->embed.st, m->hist, m->dpos, T, m->h, s));
-    HIPCHECK(launch_rms_norm(m->h, m->xn, m->layers[0].in_norm, H, T, H, c.eps, s));
+    if (tiles) HIPCHECK(launch_rms_norm_f16(m->h, m->layers[0].in_norm, H, T, H, c.eps, m->xbf, m->xsc, s));
+    else HIPCHECK(launch_rms_norm(m->h, m->xn, m->layers[0].in_norm, H, T, H, c.eps, s));
     for (int li = 0; li < c.L; li++) {
         Layer& ly = m->layers[li];
         const Lin qkvp[3] = {ly.q, ly.k, ly.v};
         const LayerDev* tl = tiles ? &m->tile_layers[li] : nullptr;
-        if (int rc = tl ? project_tiles(m, tl->qkv, m->xn, H, m->qkv, m->qkv_cols, T)
+        if (int rc = tl ? project_tiles(m, tl->qkv, nullptr, H, m->qkv, m->qkv_cols, T)
                         : project(m, qkvp, 3, m->xn, H, m->qkv, m->qkv_cols, T)) return rc;
         QkvPostArgs pa; pa.qkv = m->qkv; pa.row_stride = m->qkv_cols; pa.inv_freq = m->inv_freq; pa.kc = ly.kc; pa.vc = ly.vc;
         pa.pt = m->page_table; pa.qn = ly.q_norm; pa.kn = ly.k_norm; pa.D = c.D; pa.nH = c.nH; pa.nKV = c.nKV;
@@ -698,10 +700,11 @@ int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
         }
         if (int rc = tl ? project_tiles(m, tl->o, m->attn, c.nH * c.D, m->tmp, H, T)
                         : project(m, &ly.o, 1, m->attn, c.nH * c.D, m->tmp, H, T)) return rc;
-        HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, ly.post_norm, H, T, c.eps, s));
         if (tl) {
-            if (int rc = project_tiles(m, tl->gu, m->xn, H, m->mlp, I, T)) return rc;
+            HIPCHECK(launch_add_rms_norm_f16(m->h, m->tmp, ly.post_norm, H, T, c.eps, m->xbf, m->xsc, s));
+            if (int rc = project_tiles(m, tl->gu, nullptr, H, m->mlp, I, T)) return rc;
         } else {
+            HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, ly.post_norm, H, T, c.eps, s));
             const Lin gup[2] = {ly.gate, ly.up};
             if (int rc = project(m, gup, 2, m->xn, H, m->gu, 2 * I, T)) return rc;
             HIPCHECK(launch_silu_mul(m->gu, m->mlp, I, T, s));
@@ -710,7 +713,8 @@ int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
                         : project(m, &ly.down, 1, m->mlp, I, m->tmp, H, T)) return rc;
         const bool last = li + 1 == c.L;
         if (last && !want_logits) continue;
-        HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, last ? m->final_norm : m->layers[li + 1].in_norm, H, T, c.eps, s));
+        if (tl && !last) HIPCHECK(launch_add_rms_norm_f16(m->h, m->tmp, m->layers[li + 1].in_norm, H, T, c.eps, m->xbf, m->xsc, s));
+        else HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, last ? m->final_norm : m->layers[li + 1].in_norm, H, T, c.eps, s));
     }
     if (!want_logits) return MLXR_OK;
     if (all_logits) {
