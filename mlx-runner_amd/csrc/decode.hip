@@ -78,30 +78,36 @@ __device__ __forceinline__ void prof_mark(unsigned long long* prof, int ev) {
 }
 
 __device__ __forceinline__ void grid_arrive(MegaSync* sync, unsigned e) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(&sync->flag[blockIdx.x], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);   // this workgroup's stores have completed ...
+    __syncthreads();                 // ... in every wave
+    if (threadIdx.x == 0) {
+        const int nwg = gridDim.x, ng = min(MEGA_GROUPS, nwg), x = blockIdx.x % ng;
+        const unsigned per = (unsigned)((nwg + ng - 1 - x) / ng);
+        const unsigned old = __hip_atomic_fetch_add(&sync->cnt[x][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1u == e * per) __hip_atomic_fetch_add(&sync->gcnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 __device__ __forceinline__ void grid_wait(MegaSync* sync, unsigned e, int* abort_host) {
-    if (threadIdx.x < 64) {
-        const int nwg = gridDim.x, lane = threadIdx.x;
+    if (threadIdx.x == 0) {
+        const unsigned target = e * (unsigned)min(MEGA_GROUPS, (int)gridDim.x);
         unsigned spins = 0;
         for (;;) {
-            bool ok = true;
-            for (int w = lane; w < nwg; w += 64) ok = ok && (int)(ld_ag(&sync->flag[w]) - e) >= 0;
-            if (__all(ok)) break;
+            if ((int)(ld_ag(&sync->gcnt) - target) >= 0) break;
             if (ld_ag(&sync->abort)) break;
             __builtin_amdgcn_s_sleep(1);
             if (++spins > (1u << 20)) {   // far beyond any phase: let every wave run to the end instead
-                if (lane == 0) {
-                    __hip_atomic_store(&sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(abort_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                }
+                __hip_atomic_store(&sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(abort_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 break;
             }
         }
     }
     __syncthreads();
+}
+// Every workgroup is past its last barrier of the launch: zero the counters for the next one.
+__device__ __forceinline__ void grid_reset(MegaSync* sync) {
+    __hip_atomic_store(&sync->gcnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int x = 0; x < MEGA_GROUPS; x++) __hip_atomic_store(&sync->cnt[x][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------------------- matvec phase
@@ -600,11 +606,11 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         }
     }
     unsigned epoch = 0;                                   // barrier phases of this launch
-    const unsigned base = ld_ag(&a.sync->launch) << 10;   // unique arrival numbers across launches
+    const unsigned launch = ld_ag(&a.sync->launch);
     prof_mark(a.prof, 0);
-    prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
+    prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
     mv_prefetch<FB>(a.layers[0].qkv, wg, nwg, wave, lane, ring);
-    grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+    grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
     const int nsplit = nwg / nKV;
     for (int li = 0; li < a.L; li++) {
@@ -616,13 +622,13 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_run<FB>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkv, nullptr, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
         // prefetch this workgroup's K/V rows (positions < pos are final)
         const int item = wg;                       // nwg == nKV * nsplit
         const int kvh = item / nsplit, split = item % nsplit;
         int n0, n1; att_range(L, nsplit, split, n0, n1);
         att_prefetch(a, ly, kvh, n0, min(n1, pos), 0, kvpf);
-        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- B: attention for (kvh, split): scores on the matrix cores (K rows from the bf16 cache as
         // the A operand, q as bf16 hi + lo parts in B), softmax over chunks of 128 keys with running
@@ -841,9 +847,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 }
             }
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
         mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- C: o_proj, h += W_o attn
         {
@@ -853,9 +859,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_run<FB>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.h, ml.hown, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
         mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- D: gate|up with SiLU
         {
@@ -864,9 +870,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_run<FB>(ly.gu, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_GATED, FB>(ly.gu, us, wg, nwg, ml.part, a.mlp, nullptr, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
         mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- E: down, h += W_d mlp
         {
@@ -876,10 +882,10 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_run<FB>(ly.down, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.h, ml.hown, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, base + ++epoch);
+        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
         if (li + 1 < a.L) mv_prefetch<FB>(a.layers[li + 1].qkv, wg, nwg, wave, lane, ring);
         else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, base + epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
     }
 
     // ---- lm_head with the final norm, logits and the greedy token
@@ -894,9 +900,10 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         __builtin_amdgcn_s_waitcnt(0);
         const unsigned done = add_ag(a.head_done, 1u);
         flag = done == (unsigned)nwg - 1;
-        if (flag) {   // every workgroup is past its last barrier: reset the counter, count the launch
+        if (flag) {   // every workgroup is past its last barrier: reset the counters, count the launch
             __hip_atomic_store(a.head_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&a.sync->launch, (base >> 10) + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            grid_reset(a.sync);
+            __hip_atomic_store(&a.sync->launch, launch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();
