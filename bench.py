@@ -5,6 +5,7 @@ group 64 (bf16 scale/bias), bf16 KV cache; a 4096-token prompt of random ids is 
 batch-1 greedy decode. A "step" is one decode token: W untimed steps, then K timed steps issued as
 the reference's pipelined loop does (step n+1 committed before step n is read back, Engine.swift:740-763),
 bracketed by device synchronisation. value = decode tokens/s of the whole job (one GPU).
+`--mode prefill` runs configs[2] instead (Llama-3-8B shape, one 2048-token prefill per step).
 
 Extra objects on the JSON line:
 - roofline: the dominant kernel, the persistent decode step (one launch per token: every layer,
@@ -14,7 +15,8 @@ Extra objects on the JSON line:
   FETCH_SIZE + WRITE_SIZE (copy-kernel calibrated), read from profiles/decode_step_traffic.json
   when that file is for the same config (null otherwise), with the context it was measured at;
 - step_roofline: the same accounting for the whole decode step (bytes per token at the mean context);
-- prefill: prompt tokens/s of the 4096-token prefill (the config's second metric);
+- prefill: prompt tokens/s of the 4096-token prefill (the config's second metric), with its flops
+  (prefill_flops) against the MFMA peak;
 - cpu_baseline: the CPU oracle (C restatement of the reference's semantics, all host cores) timed on
   a bounded sample: decode steps at the same context, starting from the GPU-built KV cache.
 """
@@ -72,6 +74,57 @@ def step_bytes(cfg, ctx):
     return weight_bytes(cfg) + kv + H * (q["bits"] / 8 + 4 / q["group_size"]) + V * 4 * 2
 
 
+MFMA_PEAK_TFS = 2500.0   # MI355X dense bf16 / f16
+
+
+def prefill_flops(cfg, T, pos0=0):
+    """Algorithmic flops of a T-token prefill chunk at position pos0: every projection (2 flops per
+    weight per token), causal attention (q.k and p.v: 4 * head_dim flops per query, key, head) and the
+    lm_head for the last token."""
+    H, I, L, V = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"], cfg["vocab_size"]
+    D, nH, nKV = cfg["head_dim"], cfg["num_attention_heads"], cfg["num_key_value_heads"]
+    per_layer = H * (nH + 2 * nKV) * D + nH * D * H + 3 * H * I
+    keys = T * pos0 + T * (T + 1) // 2
+    return L * (2 * T * per_layer + 4 * D * nH * keys) + 2 * H * V
+
+
+def prefill_main(a):
+    """one sequence of random ids through the prefill (quantized GEMMs + causal flash
+    attention); value = prompt tok/s, roofline = the whole prefill's flops against the MFMA peak."""
+    cfg = configs.CONFIGS[a.config]
+    d = model_dir(a.config, a.seed)
+    model = mlxr.Transformer(d, context_length=a.context + 64)
+    greedy = mlxr.SamplingParameters.greedy()
+    prompt = np.random.default_rng(a.seed).integers(0, model.vocab_size, a.context).astype(np.int32)
+    for _ in range(max(1, a.warmup)):
+        model.prefill(prompt, 0, greedy)
+    mlxr.synchronize()
+    times = []
+    for _ in range(max(1, a.steps)):
+        t = time.perf_counter()
+        model.prefill(prompt, 0, greedy)
+        mlxr.synchronize()
+        times.append(time.perf_counter() - t)
+    el = sum(times) / len(times)
+    fl = prefill_flops(cfg, a.context)
+    tfs = fl / el / 1e12
+    log(f"[bench] prefill {a.context} tokens: {el * 1e3:.1f} ms ({a.context / el:.0f} tok/s, {tfs:.0f} TFLOP/s)")
+    result = {
+        "metric": "prefill tok/s (2048-token prompt, 8B-shape 4-bit g64) + % MFMA peak",
+        "value": round(a.context / el, 1), "unit": "tok/s", "n_gpus": 1, "steps": len(times), "warmup": max(1, a.warmup),
+        "ms_per_step": round(el * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u4 weights (affine g64, bf16 scale/bias); f16 GEMM operands, bf16 hi/lo attention, fp32 accumulate",
+        "data": "synthetic: random-init weights N(0,0.02) from a seed, uniform random prompt ids",
+        "config": {"workload": f"{a.config}: one {a.context}-token prefill (configs[2])", "model": a.config,
+                   "global_batch": 1, "seq_len": a.context, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "kernel": "whole prefill (tile GEMMs, flash attention, norms)",
+                     "achieved": round(tfs, 1), "peak": MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                     "frac": round(tfs / MFMA_PEAK_TFS, 4), "traffic": None, "flops": int(fl)},
+    }
+    model.close()
+    print(json.dumps(result), flush=True)
+
+
 def cpu_baseline(d, model, cfg, ctx, tokens, budget_s):
     import oracle
     t0 = time.time()
@@ -109,6 +162,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=360)
     ap.add_argument("--step-iters", type=int, default=64)
+    ap.add_argument("--mode", default="decode", choices=["decode", "prefill"],
+                    help="decode: configs[1] (default); prefill: configs[2] (llama3-8b, 2048 tokens unless given)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run 3 device-to-device copy kernels of MB MiB each (calibrates rocprofv3 byte counters)")
     a = ap.parse_args()
@@ -128,6 +183,16 @@ def main():
     if mlxr.device_count() < 1:
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if a.mode == "prefill":
+        if "--config" not in sys.argv:
+            a.config = "llama3-8b"
+        if "--context" not in sys.argv:
+            a.context = 2048
+        if "--steps" not in sys.argv:
+            a.steps = 5
+        if "--warmup" not in sys.argv:
+            a.warmup = 1
+        return prefill_main(a)
     cfg = configs.CONFIGS[a.config]
     d = model_dir(a.config, a.seed)
     need = a.context + a.warmup + a.steps + a.step_iters + 16
@@ -207,7 +272,9 @@ def main():
         "step_roofline": {"achieved": round(sb * tok_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(sb * tok_s / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_token": int(sb),
                           "tok_s_at_100pct": round(HBM_PEAK_GBS * 1e9 / sb, 1)},
-        "prefill": {"tokens": a.context, "tok_s": round(a.context / prefill_s, 1), "ms": round(prefill_s * 1e3, 1)},
+        "prefill": {"tokens": a.context, "tok_s": round(a.context / prefill_s, 1), "ms": round(prefill_s * 1e3, 1),
+                    "tflops": round(prefill_flops(cfg, a.context) / prefill_s / 1e12, 1),
+                    "mfma_frac": round(prefill_flops(cfg, a.context) / prefill_s / 1e12 / MFMA_PEAK_TFS, 4)},
         "kernels_us": {k: round(v["ms"] * 1e3, 2) for k, v in kern.items()},
         "first_tokens": [first] + toks[:8],
     }

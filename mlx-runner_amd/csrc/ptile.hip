@@ -57,11 +57,13 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wq = wave & 3, kc = wave >> 2;
-    // tile order: XCD x runs workgroups x, x + 8, ...; give it a contiguous run of tiles so that
-    // the workgroups of one XCD share weight tiles in its L2
+    // tile order: XCD x runs workgroups x, x + 8, ...; give it a contiguous run of tiles, and
+    // enumerate tiles in columns of 8 row-tiles so that the ~32 workgroups an XCD runs at once cover
+    // 4 token tiles x 8 row tiles (X and W blocks each shared in its L2 by several workgroups)
     const int g = blockIdx.x, xcd = g & 7, per = a.ntiles >> 3, rem = a.ntiles & 7;
     const int tile = xcd * per + min(xcd, rem) + (g >> 3);
-    const int ot = tile / a.nT, tt = tile - ot * a.nT;
+    const int nO = a.ntiles / a.nT, ob = tile / (8 * a.nT), ow = min(8, nO - 8 * ob), r8 = tile - ob * 8 * a.nT;
+    const int tt = r8 / ow, ot = 8 * ob + (r8 - tt * ow);
     const int t0 = ot * PT_TILES, m0 = tt * PT_M;
     const int r16 = lane & 15, kq = lane >> 4;
     const int K = a.p.K, FB = a.p.gs >> 3, nb = K / PT_KB, NF = (nb + FB - 1) / FB;
