@@ -34,21 +34,13 @@ struct LayerDev {
     uint16_t* kc; uint16_t* vc;
 };
 
-// Grid-barrier state: a two-level counter. Workgroup g arrives on group counter g % ng (ng =
-// min(8, workgroups)); the group's last arriver adds one to the global count, which every
-// workgroup polls. Phase e of a launch is complete when the global count reaches e * ng. The last
-// workgroup of a launch (every workgroup past its last barrier) zeroes the counters for the next
-// launch. One contended address per 32 workgroups instead of 256 writers and pollers: a barrier
-// costs about half the flat flag array's time on MI355X.
+// Launch state of the persistent step: the launch count (the high part of every exchange tag) and
+// the abort flag a stalled wait raises. Phases hand data over through tagged vectors (MegaArgs).
 constexpr int MEGA_MAX_WG = 1024;
-constexpr int MEGA_GROUPS = 8;
 struct MegaSync {
     unsigned launch;      // launches completed
-    unsigned abort;       // set when a barrier wait expires
+    unsigned abort;       // set when a wait for a tagged value expires
     unsigned pad0[30];
-    unsigned gcnt;        // groups arrived (cumulative within a launch)
-    unsigned pad1[31];
-    unsigned cnt[MEGA_GROUPS][32];   // per-group arrivals, each on its own 128-byte line
 };
 
 struct MegaArgs {
@@ -60,7 +52,11 @@ struct MegaArgs {
     float eps, scale;
     const int* pt;
     int* hist; int* status; int* dpos;
-    float *h, *qkv, *attn, *mlp, *logits, *part;
+    float *logits, *part;
+    // Tagged exchange vectors: element i is (value bits, tag) written by one 8-byte store; a reader
+    // polls until the tag of the phase that produces it appears (no grid barrier between phases).
+    // hA: h after down (and the embedding), hB: h after o_proj; q|k|v; attention output; SiLU(g)*u.
+    uint2 *hA, *hB, *qkvT, *attnT, *mlpT;
     float* wg_best; int* wg_idx;
     unsigned* kv_done; unsigned* head_done;
     MegaSync* sync;

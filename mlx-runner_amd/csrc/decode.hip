@@ -1,13 +1,15 @@
 // Persistent decode step: the whole batch-1 token step (every layer, lm_head and the greedy token)
-// in ONE launch of exactly one 512-thread workgroup per CU, phases separated by grid barriers.
+// in ONE launch of exactly one 512-thread workgroup per CU.
 //
 // Why: a kernel-per-op step issues ~5 launches per layer, and each launch boundary on MI355X costs
 // ~1.6 us of idle HBM inside a hipGraph, which alone caps an 8B decode near half of the bandwidth
-// roofline. Here every workgroup, before it waits at a barrier, issues the loads of its share of
-// the NEXT phase's weights (and of its K/V rows: the cache up to the previous position does not
-// depend on the current step), so HBM streams through the barrier.
+// roofline. Here every workgroup, before it waits for a phase's input, issues the loads of its share
+// of that phase's weights (and of its K/V rows: the cache up to the previous position does not
+// depend on the current step), so HBM streams while the inputs are still being produced.
 //
-// Phases per layer (one grid barrier after each):
+// Phases per layer; each hands its output to the next through a tagged vector (value, tag pairs:
+// a reader polls the elements it needs until the producing phase's tag appears, one round trip
+// instead of a grid barrier plus a fetch):
 //   A  q|k|v matvec      x = RMSNorm(h) * input_norm (each workgroup normalises h itself)
 //   B  attention         per (KV head, key range): q/k-norm + RoPE of its heads, K/V append by the
 //                        range holding the new position, scores, softmax partial, P.V; the last
@@ -20,11 +22,12 @@
 // token to hist[pos + 1] and the host ring, and advances *dpos.
 //
 // Semantics per phase are those of the separate kernels (qmv.hip, misc.hip, attn.hip): fp32
-// activations and accumulation, bf16 K/V. Matvec work unit: one 32-code chunk of one row per lane
-// (16 bytes at 4 bits), a ring of DEPTH units in flight per lane.
+// activations and accumulation, bf16 K/V. Matvec phases run on the matrix cores over the repacked
+// weight tiles (the matvec section below).
 //
-// Safety: the grid barrier spins with a bounded count; on expiry it raises an abort flag that every
-// later barrier honours, so every wave reaches the end of the kernel and the host reports an error.
+// Safety: every wait for a tagged value spins with a bounded count; on expiry it raises an abort
+// flag (device and host-mapped) that every later wait honours, so every wave reaches the end of the
+// kernel and the host reports an error.
 #include "decode.h"
 
 namespace mlxr {
@@ -67,47 +70,53 @@ __device__ __forceinline__ unsigned add_ag(unsigned* p, unsigned v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ------------------------------------------------------------------------------- grid barrier
-// Split barrier. `arrive`: every wave waits for its own stores to complete, then one thread stores
-// the workgroup's arrival number e into its slot (no read-modify-write round trip). The caller then
-// issues its next-phase loads, and `wait` has one wave read every slot (4 per lane, coherent) until
-// all hold e or later. An expired wait sets `abort` (device and host copies), which every later
-// wait honours, so every wave reaches the end of the kernel.
-__device__ __forceinline__ void prof_mark(unsigned long long* prof, int ev) {
-    if (prof && threadIdx.x == 0 && ev < MEGA_PROF_EVENTS) prof[(size_t)blockIdx.x * MEGA_PROF_EVENTS + ev] = wall_clock64();
+// ------------------------------------------------------------------------------- tagged exchange
+// Phase outputs other workgroups read (h, q|k|v, attention output, SiLU(g)*u) are (value, tag)
+// pairs, each written by one 8-byte agent-scope store, so a reader sees the value and its tag
+// together. The tag names the launch and the phase that produced the value: (launch << 10) +
+// phase index. A reader polls the elements it needs until their tags appear; that one round trip
+// replaces a grid barrier plus the fetch after it. No buffer is overwritten while it can still be
+// read: every phase's consumers depend (through the next layer's full-vector reads) on every
+// workgroup having moved past the phase, and h alternates between two buffers.
+constexpr unsigned TAG_SPIN_LIMIT = 1u << 20;
+__device__ __forceinline__ unsigned phase_tag(unsigned launch, int idx) { return (launch << 10) + (unsigned)idx; }
+__device__ __forceinline__ void st_tag(uint2* p, float v, unsigned tag) {
+    const unsigned long long w = (unsigned long long)__float_as_uint(v) | ((unsigned long long)tag << 32);
+    __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+struct TagWait { MegaSync* sync; int* abort_host; };
+// Gives up after TAG_SPIN_LIMIT polls: raises the abort flags (every later wait returns at once and
+// the host reports the step as failed), so every wave still reaches the end of the kernel.
+__device__ __forceinline__ bool tag_spin(const TagWait& tw, unsigned& spins) {
+    if (ld_ag(&tw.sync->abort)) return false;
+    __builtin_amdgcn_s_sleep(1);
+    if (++spins > TAG_SPIN_LIMIT) {
+        __hip_atomic_store(&tw.sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(tw.abort_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return false;
+    }
+    return true;
+}
+// Pairs i, i + 1 (i even) of base[0..n): two values once both carry the tag.
+__device__ __forceinline__ float2 ld_tag2(const uint2* base, int i, int n, unsigned tag, const TagWait& tw) {
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint2*>(base), 0, n * 8, 0x00020000);
+    coh_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, i * 8, 0, 16);
+    unsigned spins = 0;
+    while ((v.y != tag || v.w != tag) && tag_spin(tw, spins)) v = __builtin_amdgcn_raw_buffer_load_b128(r, i * 8, 0, 16);
+    return float2{__uint_as_float(v.x), __uint_as_float(v.z)};
+}
+__device__ __forceinline__ float ld_tag1(const uint2* base, int i, int n, unsigned tag, const TagWait& tw) {
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint2*>(base), 0, n * 8, 0x00020000);
+    typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+    u32x2v v = __builtin_amdgcn_raw_buffer_load_b64(r, i * 8, 0, 16);
+    unsigned spins = 0;
+    while (v.y != tag && tag_spin(tw, spins)) v = __builtin_amdgcn_raw_buffer_load_b64(r, i * 8, 0, 16);
+    return __uint_as_float(v.x);
 }
 
-__device__ __forceinline__ void grid_arrive(MegaSync* sync, unsigned e) {
-    __builtin_amdgcn_s_waitcnt(0);   // this workgroup's stores have completed ...
-    __syncthreads();                 // ... in every wave
-    if (threadIdx.x == 0) {
-        const int nwg = gridDim.x, ng = min(MEGA_GROUPS, nwg), x = blockIdx.x % ng;
-        const unsigned per = (unsigned)((nwg + ng - 1 - x) / ng);
-        const unsigned old = __hip_atomic_fetch_add(&sync->cnt[x][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1u == e * per) __hip_atomic_fetch_add(&sync->gcnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-__device__ __forceinline__ void grid_wait(MegaSync* sync, unsigned e, int* abort_host) {
-    if (threadIdx.x == 0) {
-        const unsigned target = e * (unsigned)min(MEGA_GROUPS, (int)gridDim.x);
-        unsigned spins = 0;
-        for (;;) {
-            if ((int)(ld_ag(&sync->gcnt) - target) >= 0) break;
-            if (ld_ag(&sync->abort)) break;
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > (1u << 20)) {   // far beyond any phase: let every wave run to the end instead
-                __hip_atomic_store(&sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(abort_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                break;
-            }
-        }
-    }
-    __syncthreads();
-}
-// Every workgroup is past its last barrier of the launch: zero the counters for the next one.
-__device__ __forceinline__ void grid_reset(MegaSync* sync) {
-    __hip_atomic_store(&sync->gcnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int x = 0; x < MEGA_GROUPS; x++) __hip_atomic_store(&sync->cnt[x][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Profile marks (optional): wall clock of phase boundaries, per workgroup.
+__device__ __forceinline__ void prof_mark(unsigned long long* prof, int ev) {
+    if (prof && threadIdx.x == 0 && ev < MEGA_PROF_EVENTS) prof[(size_t)blockIdx.x * MEGA_PROF_EVENTS + ev] = wall_clock64();
 }
 
 // ------------------------------------------------------------------------------- matvec phase
@@ -364,8 +373,8 @@ __device__ __forceinline__ float tile_row(const float* part, int tl, int r, int 
 // for data other workgroups read). ARGMAX returns the workgroup's largest row (lowest index among
 // equals; NaN rows never win) to every thread.
 template <int MODE, int FB>
-__device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, int wg, int nwg, const float* part, float* out,
-                                              const float* hown, float* red, int* redi) {
+__device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, int wg, int nwg, const float* part, uint2* out,
+                                              unsigned tag, float* logits, const float* hown, float* red, int* redi) {
     __syncthreads();
     const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
     const int nfw = g.nt * g.NF;
@@ -376,7 +385,7 @@ __device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, i
             if (o < p.o1) {
                 const float gv = tile_row(part, tl, j, nfw, g.NF) * unscale;
                 const float uv = tile_row(part, tl, j + 8, nfw, g.NF) * unscale;
-                st_ag(out + o, (gv / (1.0f + expf(-gv))) * uv);
+                st_tag(out + o, (gv / (1.0f + expf(-gv))) * uv, tag);
             }
         }
         return res;
@@ -385,10 +394,10 @@ __device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, i
         const int row = 16 * g.t0 + i;
         if (row >= p.rows) break;
         const float v = tile_row(part, i >> 4, i & 15, nfw, g.NF) * unscale + row_bias(p, row);
-        if (MODE == OUT_STORE) st_ag(out + row, v);
-        else if (MODE == OUT_ADD) st_ag(out + row, hown[i] + v);
+        if (MODE == OUT_STORE) st_tag(out + row, v, tag);
+        else if (MODE == OUT_ADD) st_tag(out + row, hown[i] + v, tag);
         else {
-            out[row] = v;   // logits: read by the host after the launch
+            logits[row] = v;   // read by the host after the launch
             if (v > res.best) { res.best = v; res.best_idx = row; }
         }
     }
@@ -409,26 +418,31 @@ __device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, i
     return res;
 }
 
-// Loads src[0..K) (written by other workgroups) into xf (f32, contiguous): 8 coherent 16-byte loads
-// per thread in flight per batch; returns this thread's sum of squares and max |x|.
+// Loads the tagged vector src[0..K) (written by other workgroups) into xf (f32, contiguous):
+// MK_LDB 16-byte loads (two pairs each) per thread in flight per batch, each polled until its tag
+// appears; returns this thread's sum of squares and max |x|.
 constexpr int MK_LDB = 4;
-__device__ __forceinline__ float2 fetch_to_lds(const float* src, int K, float* xf) {
+__device__ __forceinline__ float2 fetch_to_lds(const uint2* src, int K, unsigned tag, const TagWait& tw, float* xf) {
     float ss = 0.0f, mx = 0.0f;
-    const int K4 = K >> 2;
-    for (int base = 0; base < K4; base += MK_THREADS * MK_LDB) {
-        float4 v[MK_LDB];
+    const int K2 = K >> 1;
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint2*>(src), 0, K * 8, 0x00020000);
+    for (int base = 0; base < K2; base += MK_THREADS * MK_LDB) {
+        coh_u32x4 v[MK_LDB];
 #pragma unroll
         for (int j = 0; j < MK_LDB; j++) {
-            const int i4 = min(base + j * MK_THREADS + (int)threadIdx.x, K4 - 1);
-            v[j] = ld_coh4(src, i4 * 4, K);
+            const int i2 = min(base + j * MK_THREADS + (int)threadIdx.x, K2 - 1);
+            v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, i2 * 16, 0, 16);
         }
 #pragma unroll
         for (int j = 0; j < MK_LDB; j++) {
-            const int i4 = base + j * MK_THREADS + (int)threadIdx.x;
-            if (i4 < K4) {
-                *reinterpret_cast<float4*>(xf + i4 * 4) = v[j];
-                ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+            const int i2 = base + j * MK_THREADS + (int)threadIdx.x;
+            if (i2 < K2) {
+                unsigned spins = 0;
+                while ((v[j].y != tag || v[j].w != tag) && tag_spin(tw, spins)) v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, i2 * 16, 0, 16);
+                const float x0 = __uint_as_float(v[j].x), x1 = __uint_as_float(v[j].z);
+                *reinterpret_cast<float2*>(xf + i2 * 2) = float2{x0, x1};
+                ss += x0 * x0 + x1 * x1;
+                mx = fmaxf(mx, fmaxf(fabsf(x0), fabsf(x1)));
             }
         }
     }
@@ -448,8 +462,9 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 
 // x := RMSNorm(src) * w, packed to the f16 matvec layout (every workgroup computes the same
 // values). Returns the unscale factor of the packing.
-__device__ __forceinline__ float norm_to_lds(const float* src, const float* w, int K, float eps, const MvLds& L, int gsh, float* red) {
-    const float ss = wave_sum(fetch_to_lds(src, K, L.xf).x);
+__device__ __forceinline__ float norm_to_lds(const uint2* src, unsigned tag, const TagWait& tw, const float* w, int K, float eps,
+                                            const MvLds& L, int gsh, float* red) {
+    const float ss = wave_sum(fetch_to_lds(src, K, tag, tw, L.xf).x);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
@@ -468,12 +483,12 @@ __device__ __forceinline__ float norm_to_lds(const float* src, const float* w, i
 
 // x := src packed to the f16 matvec layout, plus this workgroup's residual rows h[row0 .. row1)
 // into hown (for the accumulate epilogue, so no row needs its own round trip).
-__device__ __forceinline__ float copy_to_lds(const float* src, int K, const MvLds& L, int gsh, const float* h, int H, int row0,
-                                             int row1, float* red) {
+__device__ __forceinline__ float copy_to_lds(const uint2* src, unsigned tag, const TagWait& tw, int K, const MvLds& L, int gsh,
+                                             const uint2* h, unsigned htag, int H, int row0, int row1, float* red) {
     const int n = row1 - row0;
     float hv = 0.0f;
-    if ((int)threadIdx.x < n) hv = ld_coh1(h, row0 + threadIdx.x, H);
-    const float mx = fetch_to_lds(src, K, L.xf).y;
+    if ((int)threadIdx.x < n) hv = ld_tag1(h, row0 + threadIdx.x, H, htag, tw);
+    const float mx = fetch_to_lds(src, K, tag, tw, L.xf).y;
     if ((int)threadIdx.x < n) L.hown[threadIdx.x] = hv;
     return pack_x16(L.xf, K, block_max(mx, red), L, gsh);
 }
@@ -593,7 +608,12 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
     Ring<FB> ring;
     KVPrefetch kvpf;
 
-    // embedding row of hist[pos] -> h (each workgroup writes a slice), and the first prefetch
+    const unsigned launch = ld_ag(&a.sync->launch);
+    const TagWait tw{a.sync, a.abort_host};
+    // tags: embedding 1; layer l: q|k|v 2 + 5l, attention 3 + 5l, h after o_proj 4 + 5l,
+    // SiLU(g)*u 5 + 5l, h after down 6 + 5l
+    auto tag_of = [&](int idx) { return phase_tag(launch, idx); };
+    // embedding row of hist[pos] -> hA (each workgroup writes a slice), and the first prefetch
     {
         const int tok = a.hist[pos];
         const int gpr = H / a.embed_gs;
@@ -602,33 +622,32 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const int g = (c * 8) / a.embed_gs;
             const float s = bf16_to_f32(a.embed_s[(int64_t)tok * gpr + g]), b = bf16_to_f32(a.embed_b[(int64_t)tok * gpr + g]);
 #pragma unroll
-            for (int j = 0; j < 8; j++) st_ag(a.h + c * 8 + j, (float)((w >> (4 * j)) & 15u) * s + b);
+            for (int j = 0; j < 8; j++) st_tag(a.hA + c * 8 + j, (float)((w >> (4 * j)) & 15u) * s + b, tag_of(1));
         }
     }
-    unsigned epoch = 0;                                   // barrier phases of this launch
-    const unsigned launch = ld_ag(&a.sync->launch);
+    unsigned epoch = 0;                                   // phase boundaries of this launch (profile marks)
     prof_mark(a.prof, 0);
-    prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+    prof_mark(a.prof, 2 * epoch); ++epoch;
     mv_prefetch<FB>(a.layers[0].qkv, wg, nwg, wave, lane, ring);
-    grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+    prof_mark(a.prof, 2 * epoch - 1);
 
     const int nsplit = nwg / nKV;
     for (int li = 0; li < a.L; li++) {
         const LayerDev& ly = a.layers[li];
         // ---- A: q|k|v
         {
-            const float us = norm_to_lds(a.h, ly.in_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
+            const float us = norm_to_lds(a.hA, tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), tw, ly.in_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 0);
             mv_run<FB>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
-            mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkv, nullptr, red, redi);
+            mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkvT, tag_of(2 + 5 * li), nullptr, nullptr, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); ++epoch;
         // prefetch this workgroup's K/V rows (positions < pos are final)
         const int item = wg;                       // nwg == nKV * nsplit
         const int kvh = item / nsplit, split = item % nsplit;
         int n0, n1; att_range(L, nsplit, split, n0, n1);
         att_prefetch(a, ly, kvh, n0, min(n1, pos), 0, kvpf);
-        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- B: attention for (kvh, split): scores on the matrix cores (K rows from the bf16 cache as
         // the A operand, q as bf16 hi + lo parts in B), softmax over chunks of 128 keys with running
@@ -652,10 +671,11 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const int grp = tid >> 7, i = tid & 127;
             const int QKV = (nH + 2 * nKV) * D;
             // every value this workgroup needs from q|k|v, loaded at once
-            const float qv0 = ld_coh1(a.qkv, (kvh * G + min(grp, G - 1)) * D + i, QKV);
-            const float qv1 = ld_coh1(a.qkv, (kvh * G + min(grp + 4, G - 1)) * D + i, QKV);
-            const float kraw = ld_coh1(a.qkv, (nH + kvh) * D + i, QKV);
-            const float vraw = ld_coh1(a.qkv, (nH + nKV + kvh) * D + i, QKV);
+            const unsigned qtag = tag_of(2 + 5 * li);
+            const float qv0 = ld_tag1(a.qkvT, (kvh * G + min(grp, G - 1)) * D + i, QKV, qtag, tw);
+            const float qv1 = ld_tag1(a.qkvT, (kvh * G + min(grp + 4, G - 1)) * D + i, QKV, qtag, tw);
+            const float kraw = ld_tag1(a.qkvT, (nH + kvh) * D + i, QKV, qtag, tw);
+            const float vraw = ld_tag1(a.qkvT, (nH + nKV + kvh) * D + i, QKV, qtag, tw);
             for (int base = 0; base < G; base += 4) {
                 const int g = base + grp;
                 const float v = g < G ? (base == 0 ? qv0 : qv1) : 0.0f;
@@ -843,55 +863,57 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
 #pragma unroll
                         for (int q = 0; q < 32; q++) if (s0 + q < nsplit) o += v[q] * wts[g * nsplit + s0 + q];
                     }
-                    st_ag(a.attn + (kvh * G + g) * 128 + d, o * mrow[g]);
+                    st_tag(a.attnT + (kvh * G + g) * 128 + d, o * mrow[g], tag_of(3 + 5 * li));
                 }
             }
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); ++epoch;
         mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- C: o_proj, h += W_o attn
         {
             const MvGeom<FB> gg = mv_geom<FB>(ly.o, wg, nwg, 0);
-            const float us = copy_to_lds(a.attn, nH * D, ml, FB == 4 ? 5 : 6, a.h, H, 16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
+            const float us = copy_to_lds(a.attnT, tag_of(3 + 5 * li), tw, nH * D, ml, FB == 4 ? 5 : 6, a.hA,
+                                         tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), H, 16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 4);
             mv_run<FB>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
-            mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.h, ml.hown, red, redi);
+            mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.hB, tag_of(4 + 5 * li), nullptr, ml.hown, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); ++epoch;
         mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- D: gate|up with SiLU
         {
-            const float us = norm_to_lds(a.h, ly.post_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
+            const float us = norm_to_lds(a.hB, tag_of(4 + 5 * li), tw, ly.post_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 5);
             mv_run<FB>(ly.gu, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
-            mv_finish<OUT_GATED, FB>(ly.gu, us, wg, nwg, ml.part, a.mlp, nullptr, red, redi);
+            mv_finish<OUT_GATED, FB>(ly.gu, us, wg, nwg, ml.part, a.mlpT, tag_of(5 + 5 * li), nullptr, nullptr, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); ++epoch;
         mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- E: down, h += W_d mlp
         {
             const MvGeom<FB> gg = mv_geom<FB>(ly.down, wg, nwg, 0);
-            const float us = copy_to_lds(a.mlp, a.I, ml, FB == 4 ? 5 : 6, a.h, H, 16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
+            const float us = copy_to_lds(a.mlpT, tag_of(5 + 5 * li), tw, a.I, ml, FB == 4 ? 5 : 6, a.hB, tag_of(4 + 5 * li), H,
+                                         16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 6);
             mv_run<FB>(ly.down, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
-            mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.h, ml.hown, red, redi);
+            mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.hA, tag_of(6 + 5 * li), nullptr, ml.hown, red, redi);
         }
-        prof_mark(a.prof, 2 * epoch); grid_arrive(a.sync, ++epoch);
+        prof_mark(a.prof, 2 * epoch); ++epoch;
         if (li + 1 < a.L) mv_prefetch<FB>(a.layers[li + 1].qkv, wg, nwg, wave, lane, ring);
         else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
-        grid_wait(a.sync, epoch, a.abort_host); prof_mark(a.prof, 2 * epoch - 1);
+        prof_mark(a.prof, 2 * epoch - 1);
     }
 
     // ---- lm_head with the final norm, logits and the greedy token
-    const float us = norm_to_lds(a.h, a.final_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
+    const float us = norm_to_lds(a.hA, tag_of(6 + 5 * (a.L - 1)), tw, a.final_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
     mv_run<FB>(a.head, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
-    const MvResult best = mv_finish<OUT_ARGMAX, FB>(a.head, us, wg, nwg, ml.part, a.logits, nullptr, red, redi);
+    const MvResult best = mv_finish<OUT_ARGMAX, FB>(a.head, us, wg, nwg, ml.part, nullptr, 0u, a.logits, nullptr, red, redi);
     prof_mark(a.prof, 2 * epoch);
     __shared__ float bv[MK_WAVES];
     __shared__ int bi[MK_WAVES];
@@ -900,9 +922,8 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         __builtin_amdgcn_s_waitcnt(0);
         const unsigned done = add_ag(a.head_done, 1u);
         flag = done == (unsigned)nwg - 1;
-        if (flag) {   // every workgroup is past its last barrier: reset the counters, count the launch
+        if (flag) {   // every workgroup has finished its phases: reset the counter, count the launch
             __hip_atomic_store(a.head_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            grid_reset(a.sync);
             __hip_atomic_store(&a.sync->launch, launch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }

@@ -334,6 +334,7 @@ static int mega_setup(Model* m) {
         for (const Lin* l : {&ly.q, &ly.k, &ly.v, &ly.o, &ly.gate, &ly.up, &ly.down})
             if (!four_bf16(*l)) return no("a projection is not 4-bit with bf16 scales");
     if (c.D != 128 || c.nH / c.nKV > 8 || c.rot_dim > 128) return no("head shape");
+    if (5 * c.L + 2 > 1023) return no("too many layers for the exchange tags");
     hipDeviceProp_t prop;
     HIPCHECK(hipGetDeviceProperties(&prop, 0));
     int cus = prop.multiProcessorCount;
@@ -396,7 +397,18 @@ static int mega_setup(Model* m) {
     a.final_norm = m->final_norm; a.inv_freq = m->inv_freq;
     a.eps = c.eps; a.scale = c.query_scale * c.rope_attention_factor * c.rope_attention_factor;
     a.pt = m->page_table; a.hist = m->hist; a.status = m->status; a.dpos = m->dpos;
-    a.h = m->h; a.qkv = m->qkv; a.attn = m->attn; a.mlp = m->mlp; a.logits = m->logits;
+    a.logits = m->logits;
+    {   // tagged exchange vectors (zeroed: tag 0 names no phase)
+        const size_t qkv_n = (size_t)(c.nH + 2 * c.nKV) * c.D;
+        if ((rc = dalloc(m, &a.hA, (size_t)c.H)) || (rc = dalloc(m, &a.hB, (size_t)c.H)) || (rc = dalloc(m, &a.qkvT, qkv_n)) ||
+            (rc = dalloc(m, &a.attnT, (size_t)c.nH * c.D)) || (rc = dalloc(m, &a.mlpT, (size_t)c.I)))
+            return rc;
+        HIPCHECK(hipMemset(a.hA, 0, sizeof(uint2) * c.H));
+        HIPCHECK(hipMemset(a.hB, 0, sizeof(uint2) * c.H));
+        HIPCHECK(hipMemset(a.qkvT, 0, sizeof(uint2) * qkv_n));
+        HIPCHECK(hipMemset(a.attnT, 0, sizeof(uint2) * c.nH * c.D));
+        HIPCHECK(hipMemset(a.mlpT, 0, sizeof(uint2) * c.I));
+    }
     if ((rc = dalloc(m, &a.part, (size_t)c.nH * nsplit * (c.D + 2))) || (rc = dalloc(m, &a.wg_best, nwg)) ||
         (rc = dalloc(m, &a.wg_idx, nwg)) || (rc = dalloc(m, &a.kv_done, 64 * 32)) || (rc = dalloc(m, &a.head_done, 64)) ||
         (rc = dalloc(m, &a.sync, 1)))
