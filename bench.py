@@ -5,7 +5,9 @@ group 64 (bf16 scale/bias), bf16 KV cache; a 4096-token prompt of random ids is 
 batch-1 greedy decode. A "step" is one decode token: W untimed steps, then K timed steps issued as
 the reference's pipelined loop does (step n+1 committed before step n is read back, Engine.swift:740-763),
 bracketed by device synchronisation. value = decode tokens/s of the whole job (one GPU).
-`--mode prefill` runs configs[2] instead (Llama-3-8B shape, one 2048-token prefill per step).
+`--mode prefill` runs configs[2] instead (Llama-3-8B shape, one 2048-token prefill per step),
+`--mode sweep` configs[3] (the matvec / GEMM sweep), `--mode long` configs[4] (Qwen2.5-32B shape,
+32K context, sparse decode attention, reused prefix).
 
 Extra objects on the JSON line:
 - roofline: the dominant kernel, the persistent decode step (one launch per token: every layer,
@@ -21,6 +23,7 @@ Extra objects on the JSON line:
   a bounded sample: decode steps at the same context, starting from the GPU-built KV cache.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -125,6 +128,132 @@ def prefill_main(a):
     print(json.dumps(result), flush=True)
 
 
+def sweep_main(a):
+    """the quantized matvec / GEMM sweep on 8B-shape projections. Weights are random code
+    words with random bf16 scales / biases (every bit pattern is a valid code stream at any width;
+    parity is the kernel tests' job), activations N(0, 1). T = 1: the decode matvec (mlxr_k_qmv),
+    T = 4: the small-batch kernel (mlxr_k_qmm), T = 512: the prefill GEMM (mlxr_k_qgemm). HIP events
+    around `iters` back-to-back calls; bytes = N*K*(b/8 + 4/gs) + T*K*4 + T*N*4, flops = 2*T*N*K."""
+    rng = np.random.default_rng(a.seed)
+    shapes = [(4096, 14336), (14336, 4096), (4096, 151936)]
+    quants = [(3, 32), (4, 64), (6, 128), (8, 64)]
+    cells = []
+    for K, N in shapes:
+        for bits, gs in quants:
+            w = mlxr.DeviceArray.from_numpy(rng.integers(0, 2**32, (N, K * bits // 32), dtype=np.uint32))
+            sc = mlxr.DeviceArray.from_numpy((rng.uniform(0.001, 0.05, (N, K // gs)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+            bi = mlxr.DeviceArray.from_numpy((rng.uniform(-0.2, 0.2, (N, K // gs)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+            qm = (mlxr.QMat * 1)(mlxr.QMat(w.ptr, sc.ptr, bi.ptr, None, N))
+            for T in (1, 4, 512):
+                x = mlxr.DeviceArray.from_numpy(rng.normal(0, 1, (T, K)).astype(np.float32))
+                y = mlxr.DeviceArray.zeros((T, N), np.float32)
+                if T == 1:
+                    call = lambda: mlxr.lib.mlxr_k_qmv(qm, 1, K, bits, gs, 0, x.ptr, None, 0.0, y.ptr, 0)
+                elif T == 4:
+                    call = lambda: mlxr.lib.mlxr_k_qmm(qm, 1, K, bits, gs, 0, T, x.ptr, K, y.ptr, N)
+                else:
+                    call = lambda: mlxr.lib.mlxr_k_qgemm(qm, K, bits, gs, 0, T, x.ptr, K, y.ptr, N)
+                mlxr.check(call())
+                mlxr.synchronize()
+                iters = 20 if T == 512 else 50
+                mlxr.check(mlxr.lib.mlxr_timer_start())
+                for _ in range(iters):
+                    mlxr.check(call())
+                ms = ctypes.c_float()
+                mlxr.check(mlxr.lib.mlxr_timer_stop(ms))
+                us = ms.value * 1e3 / iters
+                byt = N * K * (bits / 8 + 4 / gs) + T * K * 4 + T * N * 4
+                cell = {"K": K, "N": N, "bits": bits, "gs": gs, "T": T, "us": round(us, 2),
+                        "GBs": round(byt / us / 1e3, 1), "TFLOPs": round(2 * T * N * K / us / 1e6, 2)}
+                cells.append(cell)
+                log(f"[bench] sweep K={K} N={N} {bits}b g{gs} T={T}: {us:8.1f} us  {cell['GBs']:7.0f} GB/s  {cell['TFLOPs']:6.1f} TFLOP/s")
+                x.free(); y.free()
+            w.free(); sc.free(); bi.free()
+    dec = [c for c in cells if c["T"] == 1]
+    gemm = [c for c in cells if c["T"] == 512]
+    best_dec = max(dec, key=lambda c: c["GBs"])
+    result = {
+        "metric": "quantized matvec / GEMM sweep (8B-shape projections, configs[3])",
+        "value": round(sum(c["GBs"] for c in dec) / len(dec), 1), "unit": "GB/s (mean over the T = 1 cells)",
+        "n_gpus": 1, "steps": len(cells), "warmup": 1, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u3/u4/u6/u8 weights (bf16 scale/bias), fp32 activations",
+        "data": "synthetic: random code words and bf16 scales / biases, N(0,1) activations",
+        "config": {"workload": "configs[3]: K,N in (4096,14336),(14336,4096),(4096,151936) x 3b g32, 4b g64, 6b g128, 8b g64 x T in 1,4,512"},
+        "roofline": {"bound": "hbm", "kernel": f"qmv_kernel, best cell K={best_dec['K']} N={best_dec['N']} {best_dec['bits']}b",
+                     "achieved": best_dec["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(best_dec["GBs"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "gemm_T512": {"best_TFLOPs": max(c["TFLOPs"] for c in gemm), "peak": MFMA_PEAK_TFS},
+        "cells": cells,
+    }
+    print(json.dumps(result), flush=True)
+
+
+def long_main(a):
+    """Qwen2.5-32B shape, 32768-token context with sparse decode attention. Turn 1
+    prefills the first 30000 ids; turn 2 reuses that prefix (reusable_prefix), prefills the remaining
+    ids and decodes `steps` greedy tokens (two in flight)."""
+    cfg = configs.CONFIGS[a.config]
+    d = model_dir(a.config, a.seed)
+    model = mlxr.Transformer(d, context_length=a.context, sparse=mlxr.SparseAttention(min_context=5128))
+    total = model.max_seq - a.steps - a.warmup - 8      # the prompt leaves room for the decoded tokens
+    first_turn = min(30000, total - 8)
+    greedy = mlxr.SamplingParameters.greedy()
+    ids = np.random.default_rng(a.seed).integers(0, model.vocab_size, total).astype(np.int32)
+    t = time.perf_counter()
+    model.prefill(ids[:first_turn], 0, greedy)
+    mlxr.synchronize()
+    t1 = time.perf_counter() - t
+    reuse = model.reusable_prefix(first_turn, first_turn)
+    t = time.perf_counter()
+    tok = model.prefill(ids[reuse:], reuse, greedy)
+    mlxr.synchronize()
+    t2 = time.perf_counter() - t
+    log(f"[bench] turn 1 prefill {first_turn} tokens: {t1:.2f} s; turn 2 reuses {reuse}, prefills {total - reuse} in {t2 * 1e3:.0f} ms")
+    pos = total
+
+    def run(n, pos, first):
+        toks = []
+        cur = model.begin_decode_step(pos, greedy)
+        for i in range(n):
+            nxt = model.begin_decode_step(cur.offset + 1, greedy) if i + 1 < n else None
+            toks.append(model.finish(cur))
+            cur = nxt
+        return toks
+
+    run(a.warmup, pos, tok)
+    pos += a.warmup
+    mlxr.synchronize()
+    t = time.perf_counter()
+    toks = run(a.steps, pos, tok)
+    mlxr.synchronize()
+    el = time.perf_counter() - t
+    tok_s = a.steps / el
+    # sparse accounting (SURVEY 8d): weights + per layer the index scan and the attended keys
+    L, nKV, D = cfg["num_hidden_layers"], cfg["num_key_value_heads"], cfg["head_dim"]
+    ctx = pos + a.steps // 2
+    blocks = (ctx - 512) // 4
+    attended = 4 + 4 * min(512, blocks) + 512
+    sb = weight_bytes(cfg) + L * (blocks * nKV * D * 2 + attended * nKV * D * 2 * 2)
+    log(f"[bench] long-context decode {a.steps} steps: {el * 1e3:.1f} ms, {tok_s:.1f} tok/s ({sb * tok_s / 1e9:.0f} GB/s algorithmic)")
+    result = {
+        "metric": "decode tok/s (bs1, 32B-shape 4-bit g64, 32K context, sparse attention) + % HBM roofline",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(el * 1e3 / a.steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u4 weights (affine g64, bf16 scale/bias), fp32 activations, bf16 KV",
+        "data": "synthetic: random-init weights N(0,0.02) from a seed, uniform random ids",
+        "config": {"workload": f"{a.config}: {total}-token context, {reuse}-token reused prefix, sparse decode (configs[4])",
+                   "model": a.config, "global_batch": 1, "seq_len": total + a.warmup + a.steps, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "whole decode step (kernel-per-op graph; sparse attention)",
+                     "achieved": round(sb * tok_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(sb * tok_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_token": int(sb)},
+        "prefill": {"turn1_tokens": first_turn, "turn1_s": round(t1, 3), "reused": reuse, "turn2_tokens": total - reuse,
+                    "turn2_ms": round(t2 * 1e3, 1)},
+        "first_tokens": toks[:8],
+    }
+    model.close()
+    print(json.dumps(result), flush=True)
+
+
 def cpu_baseline(d, model, cfg, ctx, tokens, budget_s):
     import oracle
     t0 = time.time()
@@ -162,8 +291,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=360)
     ap.add_argument("--step-iters", type=int, default=64)
-    ap.add_argument("--mode", default="decode", choices=["decode", "prefill"],
-                    help="decode: configs[1] (default); prefill: configs[2] (llama3-8b, 2048 tokens unless given)")
+    ap.add_argument("--mode", default="decode", choices=["decode", "prefill", "sweep", "long"],
+                    help="decode: configs[1] (default); prefill: configs[2] (llama3-8b, 2048 tokens unless given); "
+                         "sweep: configs[3]; long: configs[4] (qwen2.5-32b, 32768-token context, sparse)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run 3 device-to-device copy kernels of MB MiB each (calibrates rocprofv3 byte counters)")
     a = ap.parse_args()
@@ -193,6 +323,18 @@ def main():
         if "--warmup" not in sys.argv:
             a.warmup = 1
         return prefill_main(a)
+    if a.mode == "sweep":
+        return sweep_main(a)
+    if a.mode == "long":
+        if "--config" not in sys.argv:
+            a.config = "qwen2.5-32b"
+        if "--context" not in sys.argv:
+            a.context = 32768
+        if "--steps" not in sys.argv:
+            a.steps = 128
+        if "--warmup" not in sys.argv:
+            a.warmup = 4
+        return long_main(a)
     cfg = configs.CONFIGS[a.config]
     d = model_dir(a.config, a.seed)
     need = a.context + a.warmup + a.steps + a.step_iters + 16
