@@ -6,15 +6,6 @@
 // hi + lo pair of bf16 values (x = hi + lo exactly to ~2^-16), K and V are the bf16 cache itself,
 // and every product accumulates in fp32, so the result matches fp32 arithmetic to ~1e-5 relative.
 //
-// MI355X layout: one workgroup per (KV head, block of 32 queries), one wave per query head of the
-// group (the G heads share every K / V tile). Per tile of 64 keys (one cache page):
-//   S^T = K Q^T   A = K rows from LDS (16 keys x 32 dims per MFMA), B = q (registers);
-//                 the accumulator holds 4 keys x 1 query per lane (query = lane & 15);
-//   online softmax per query column (two lane exchanges);
-//   O^T += V^T P^T  B = P^T straight from the S^T accumulators: the MFMA's k order is chosen so
-//                 that a lane's 8 k-slots are its 4 keys of two 16-key blocks; A = V^T from a
-//                 transposed LDS copy of the tile read in that same key order.
-// Query blocks are launched heaviest (latest) first, so the causal imbalance evens out over the CUs.
 #include "kernels.h"
 
 namespace mlxr {
@@ -22,193 +13,9 @@ namespace mlxr {
 typedef __bf16 fbf16x8_t __attribute__((ext_vector_type(8)));
 typedef float ff32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int FP_QB = 32;     // queries per workgroup (each wave: one head, 2 blocks of 16)
-constexpr int FP_KT = 64;     // keys per tile (= one cache page)
-constexpr int FP_KS = 136;    // LDS row stride of the K tile (bf16): 128 + 8 (bank spread)
-constexpr int FP_VS = 72;     // LDS row stride of the V^T tile (bf16): 64 + 8
-
-__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
-
-// x -> (hi, lo) bf16 with hi + lo = x to ~2^-16 relative.
-__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
-    hi = f32_to_bf16(x);
-    lo = f32_to_bf16(x - bf16_to_f32(hi));
-}
-
-template <int NW>
-__global__ __launch_bounds__(NW * 64) void flash_prefill_kernel(FlashArgs a, int nb) {
-    constexpr int NT = NW * 64;
-    constexpr int PIECES = FP_KT * 16 / NT;       // 16-byte pieces of a K (or V) tile per thread
-    __shared__ __attribute__((aligned(16))) uint16_t ks[FP_KT * FP_KS];   // K tile, [key][dim]
-    __shared__ __attribute__((aligned(16))) uint16_t vt[128 * FP_VS];     // V tile transposed, [dim][key]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int b = nb - 1 - (int)blockIdx.x, kvh = blockIdx.y;
-    const int G = a.nH / a.nKV, h = kvh * G + wave;
-    const bool active = wave < G;
-    const int pos0 = *a.dpos;
-    const int q0 = b * FP_QB, nq = min(FP_QB, a.T - q0);
-    const int kend = pos0 + q0 + nq;                             // keys [0, kend)
-    const int ntiles = (kend + FP_KT - 1) / FP_KT;
-    const int col = lane & 15, grp = lane >> 4;
-
-    // q of this wave's head as B fragments: [db][qb] x (hi, lo), dims 32 db + 8 grp .. +8, query 16 qb + col
-    fbf16x8_t qf[4][2][2];
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-        const int t = min(q0 + 16 * qb + col, a.T - 1);
-        const float* qp = a.q + (size_t)t * a.q_stride + (size_t)(active ? h : 0) * 128;
-#pragma unroll
-        for (int db = 0; db < 4; db++) {
-            const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * db + 8 * grp);
-            const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * db + 8 * grp + 4);
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            uint16_t hi[8], lo[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) split_bf16(xs[e] * a.scale, hi[e], lo[e]);
-            const uint4 uh = {pack2(hi[0], hi[1]), pack2(hi[2], hi[3]), pack2(hi[4], hi[5]), pack2(hi[6], hi[7])};
-            const uint4 ul = {pack2(lo[0], lo[1]), pack2(lo[2], lo[3]), pack2(lo[4], lo[5]), pack2(lo[6], lo[7])};
-            qf[db][qb][0] = __builtin_bit_cast(fbf16x8_t, uh);
-            qf[db][qb][1] = __builtin_bit_cast(fbf16x8_t, ul);
-        }
-    }
-
-    ff32x4_t o[8][2];                            // O^T: dims 16 nb + 4 grp + i, query 16 qb + col
-#pragma unroll
-    for (int n = 0; n < 8; n++)
-#pragma unroll
-        for (int qb = 0; qb < 2; qb++) o[n][qb] = ff32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
-
-    // tile loads: piece p = tid + NT j: key p >> 4, dims 8 (p & 15) .. +8
-    uint4 kp[PIECES], vp[PIECES];
-    auto load_tile = [&](int tile) {
-        const int64_t base = ((int64_t)a.pt[tile] * a.nKV + kvh) * FP_KT * 128;
-#pragma unroll
-        for (int j = 0; j < PIECES; j++) {
-            const int p = tid + NT * j, key = p >> 4, part = p & 15;
-            kp[j] = *reinterpret_cast<const uint4*>(a.kc + base + key * 128 + part * 8);
-            vp[j] = *reinterpret_cast<const uint4*>(a.vc + base + key * 128 + part * 8);
-        }
-    };
-    load_tile(0);
-    for (int tile = 0; tile < ntiles; tile++) {
-        __syncthreads();                          // the previous tile's LDS reads are done
-#pragma unroll
-        for (int j = 0; j < PIECES; j++) {
-            const int p = tid + NT * j, key = p >> 4, part = p & 15;
-            *reinterpret_cast<uint4*>(ks + key * FP_KS + part * 8) = kp[j];
-            // rows past the chunk's last key may hold anything: zero V (its weight is 0, and 0 * NaN is not)
-            const bool live = tile * FP_KT + key < kend;
-            const uint32_t w[4] = {live ? vp[j].x : 0u, live ? vp[j].y : 0u, live ? vp[j].z : 0u, live ? vp[j].w : 0u};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                vt[(part * 8 + 2 * e) * FP_VS + key] = (uint16_t)(w[e] & 0xffffu);
-                vt[(part * 8 + 2 * e + 1) * FP_VS + key] = (uint16_t)(w[e] >> 16);
-            }
-        }
-        __syncthreads();
-        if (tile + 1 < ntiles) load_tile(tile + 1);   // overlaps this tile's math
-        if (!active) continue;
-        const int k0 = tile * FP_KT;
-
-        // S^T tiles [kb][qb]: keys k0 + 16 kb + 4 grp + i, query 16 qb + col
-        ff32x4_t s[4][2];
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
-            s[kb][0] = s[kb][1] = ff32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int db = 0; db < 4; db++) {
-                const fbf16x8_t ka = __builtin_bit_cast(fbf16x8_t, *reinterpret_cast<const uint4*>(ks + (16 * kb + col) * FP_KS + 32 * db + 8 * grp));
-#pragma unroll
-                for (int qb = 0; qb < 2; qb++) {
-                    s[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[db][qb][0], s[kb][qb], 0, 0, 0);
-                    s[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[db][qb][1], s[kb][qb], 0, 0, 0);
-                }
-            }
-        }
-        // causal mask (only the tiles reaching past the block's first query), online softmax
-        const bool diag = k0 + FP_KT - 1 > pos0 + q0;
-        ff32x4_t pr[4][2];
-#pragma unroll
-        for (int qb = 0; qb < 2; qb++) {
-            const int qpos = pos0 + q0 + 16 * qb + col;
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int kpos = k0 + 16 * kb + 4 * grp + i;
-                    if (diag && kpos > qpos) s[kb][qb][i] = -INFINITY;
-                    mx = fmaxf(mx, s[kb][qb][i]);
-                }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64)); mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = fmaxf(m[qb], mx);
-            const float alpha = mn == -INFINITY ? 1.0f : expf(m[qb] - mn);
-            float sum = 0.0f;
-#pragma unroll
-            for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float p = mn == -INFINITY ? 0.0f : expf(s[kb][qb][i] - mn);
-                    pr[kb][qb][i] = p;
-                    sum += p;
-                }
-            sum += __shfl_xor(sum, 16, 64); sum += __shfl_xor(sum, 32, 64);
-            l[qb] = l[qb] * alpha + sum;
-            m[qb] = mn;
-#pragma unroll
-            for (int n = 0; n < 8; n++) o[n][qb] *= alpha;
-        }
-        // O^T += V^T P^T over two 32-key steps: k-slots 0..3 = keys 16 (2 ks) + 4 grp + i,
-        // k-slots 4..7 = keys 16 (2 ks + 1) + 4 grp + i (both operands in that order)
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-            fbf16x8_t pb[2][2];
-#pragma unroll
-            for (int qb = 0; qb < 2; qb++) {
-                uint16_t hi[8], lo[8];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    split_bf16(pr[2 * st][qb][i], hi[i], lo[i]);
-                    split_bf16(pr[2 * st + 1][qb][i], hi[4 + i], lo[4 + i]);
-                }
-                const uint4 uh = {pack2(hi[0], hi[1]), pack2(hi[2], hi[3]), pack2(hi[4], hi[5]), pack2(hi[6], hi[7])};
-                const uint4 ul = {pack2(lo[0], lo[1]), pack2(lo[2], lo[3]), pack2(lo[4], lo[5]), pack2(lo[6], lo[7])};
-                pb[qb][0] = __builtin_bit_cast(fbf16x8_t, uh);
-                pb[qb][1] = __builtin_bit_cast(fbf16x8_t, ul);
-            }
-#pragma unroll
-            for (int n = 0; n < 8; n++) {
-                const uint16_t* vr = vt + (16 * n + col) * FP_VS + 32 * st + 4 * grp;
-                const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
-                const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 16);
-                const fbf16x8_t va = __builtin_bit_cast(fbf16x8_t, uint4{v0.x, v0.y, v1.x, v1.y});
-#pragma unroll
-                for (int qb = 0; qb < 2; qb++) {
-                    o[n][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[qb][0], o[n][qb], 0, 0, 0);
-                    o[n][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[qb][1], o[n][qb], 0, 0, 0);
-                }
-            }
-        }
-    }
-    if (!active) return;
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-        const int t = q0 + 16 * qb + col;
-        if (t >= a.T) continue;
-        const float inv = 1.0f / l[qb];
-        float* op = a.out + (size_t)t * a.out_stride + (size_t)h * 128 + 4 * grp;
-#pragma unroll
-        for (int n = 0; n < 8; n++)
-            *reinterpret_cast<float4*>(op + 16 * n) = float4{o[n][qb][0] * inv, o[n][qb][1] * inv, o[n][qb][2] * inv, o[n][qb][3] * inv};
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
-// G <= 4 heads per KV head: the paired-block kernel.
-//
-// A 512-thread workgroup serves one KV head and two blocks of 32 queries, a light one (b) and its
-// causal mirror (nb - 1 - b): waves 0-3 take the light block's heads, waves 4-7 the heavy block's,
+// MI355X layout: a 512-thread workgroup serves one KV head (up to 4 of its query heads; G > 4 takes
+// ceil(G / 4) head groups) and two blocks of 32 queries, a light one (b) and its causal mirror
+// (nb - 1 - b): waves 0-3 take the light block's heads, waves 4-7 the heavy block's,
 // so every workgroup does the same work and the two waves on a SIMD hide each other's latency.
 // Both blocks read the same K / V tiles, copied from the paged cache straight into LDS
 // (buffer -> LDS, [key][128] bf16 with 16-byte chunks XOR-swizzled by (key & 15), two stages).
@@ -233,16 +40,17 @@ __device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_
     lo = __builtin_bit_cast(uint32_t, l);
 }
 
-template <int G>
-__global__ __launch_bounds__(512) void flash2_kernel(FlashArgs a, int nb) {
+__global__ __launch_bounds__(512) void flash2_kernel(FlashArgs a, int nb, int ngroups) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t f2_lds[];   // [2 stages][K tile, V tile]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int hh = wave & 3, half = wave >> 2, kvh = blockIdx.y;
+    const int G = a.nH / a.nKV, kvh = (int)blockIdx.y / ngroups, grp = (int)blockIdx.y - kvh * ngroups;
+    const int gw = min(4, G - 4 * grp);                                  // heads of this group
+    const int hh = wave & 3, half = wave >> 2;
     const int blight = (int)blockIdx.x, bheavy = nb - 1 - blight;
     const int blk = half ? bheavy : blight;
-    const bool active = hh < G && (half == 0 || bheavy != blight);
-    const int h = kvh * G + (hh < G ? hh : 0);
+    const bool active = hh < gw && (half == 0 || bheavy != blight);
+    const int h = kvh * G + 4 * grp + min(hh, gw - 1);
     const int pos0 = *a.dpos;
     const int q0 = blk * 32, nq = min(32, a.T - q0);
     const int kend = pos0 + q0 + nq;                                      // this wave's keys [0, kend)
@@ -410,21 +218,9 @@ __global__ __launch_bounds__(512) void flash2_kernel(FlashArgs a, int nb) {
 
 hipError_t launch_flash_prefill(const FlashArgs& a, hipStream_t s) {
     if (a.D != 128 || a.nKV < 1 || a.nH % a.nKV || a.nH / a.nKV > 8 || a.T < 1) return hipErrorInvalidValue;
-    const int G = a.nH / a.nKV;
-    if (G <= 4) {
-        const int nb = (a.T + 31) / 32, npair = (nb + 1) / 2;
-        const dim3 grid(npair, a.nKV);
-        switch (G) {
-            case 1: hipLaunchKernelGGL(flash2_kernel<1>, grid, dim3(512), 4 * F2_TILE, s, a, nb); break;
-            case 2: hipLaunchKernelGGL(flash2_kernel<2>, grid, dim3(512), 4 * F2_TILE, s, a, nb); break;
-            case 3: hipLaunchKernelGGL(flash2_kernel<3>, grid, dim3(512), 4 * F2_TILE, s, a, nb); break;
-            default: hipLaunchKernelGGL(flash2_kernel<4>, grid, dim3(512), 4 * F2_TILE, s, a, nb); break;
-        }
-        return hipGetLastError();
-    }
-    const int nb = (a.T + FP_QB - 1) / FP_QB;
-    if (a.nH / a.nKV <= 4) hipLaunchKernelGGL(flash_prefill_kernel<4>, dim3(nb, a.nKV), dim3(256), 0, s, a, nb);
-    else hipLaunchKernelGGL(flash_prefill_kernel<8>, dim3(nb, a.nKV), dim3(512), 0, s, a, nb);
+    const int G = a.nH / a.nKV, ngroups = (G + 3) / 4;
+    const int nb = (a.T + 31) / 32, npair = (nb + 1) / 2;
+    hipLaunchKernelGGL(flash2_kernel, dim3(npair, a.nKV * ngroups), dim3(512), 4 * F2_TILE, s, a, nb, ngroups);
     return hipGetLastError();
 }
 
