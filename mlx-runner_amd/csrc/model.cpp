@@ -325,14 +325,61 @@ void sparse_clamp(mlxr_sparse_cfg& c) {   // SparseAttention.init (SparseAttenti
 
 // The persistent decode step (decode.hip) covers 4-bit bf16-scaled models with head_dim 128,
 // at most 8 query heads per KV head and a KV-head count dividing the workgroup count.
+// The repacked copy (DPack) of every layer's phases, built when every projection is 4-bit with
+// bf16 scales, gs 32/64, K % 128 == 0 and each fused phase shares one group size. The prefill tile
+// GEMMs read it; the persistent decode step (mega_setup) reads it too, plus a repacked lm_head.
+static MvPhaseDesc repack_phase(Model* m, const Lin* parts, int n, bool gated, int& rc) {
+    MvPhaseDesc d{};
+    DPackSrc src{};
+    for (int i = 0; i < 3; i++) {
+        const Lin& l = parts[i < n ? i : n - 1];
+        src.w[i] = reinterpret_cast<const uint8_t*>(l.m.w); src.s[i] = l.m.s; src.b[i] = l.m.b;
+        d.bias[i] = i < n ? l.m.bias : nullptr;
+    }
+    d.o1 = src.o1 = parts[0].O; d.o2 = src.o2 = n > 1 ? parts[1].O : 0;
+    int rows = 0; for (int i = 0; i < n; i++) rows += parts[i].O;
+    d.rows = src.rows = rows; d.K = src.K = parts[0].K; d.gs = src.gs = parts[0].gs; d.gated = src.gated = gated ? 1 : 0;
+    d.tiles = dpack_tiles(src);
+    uint8_t* code = nullptr;
+    if (rc == MLXR_OK) rc = dalloc(m, &code, dpack_bytes(src));
+    if (rc == MLXR_OK && launch_dpack(src, code, m->stream) != hipSuccess) rc = set_error(MLXR_E_GPU, "repack launch");
+    d.code = code;
+    return d;
+}
+static bool repackable(const Lin& l) { return l.bits == 4 && l.st == 0 && l.K % 128 == 0 && (l.gs == 32 || l.gs == 64); }
+static int tiles_setup(Model* m) {
+    const Config& c = m->cfg;
+    for (auto& ly : m->layers) {
+        for (const Lin* l : {&ly.q, &ly.k, &ly.v, &ly.o, &ly.gate, &ly.up, &ly.down})
+            if (!repackable(*l)) return MLXR_OK;
+        if (ly.q.gs != ly.k.gs || ly.q.gs != ly.v.gs || ly.gate.gs != ly.up.gs) return MLXR_OK;
+    }
+    int rc = MLXR_OK;
+    std::vector<LayerDev> host(c.L);
+    for (int i = 0; i < c.L; i++) {
+        const Layer& ly = m->layers[i];
+        const Lin qkv[3] = {ly.q, ly.k, ly.v}, gu[2] = {ly.gate, ly.up};
+        LayerDev& d = host[i];
+        d.qkv = repack_phase(m, qkv, 3, false, rc); d.o = repack_phase(m, &ly.o, 1, false, rc);
+        d.gu = repack_phase(m, gu, 2, true, rc); d.down = repack_phase(m, &ly.down, 1, false, rc);
+        if (rc) return rc;
+        d.in_norm = ly.in_norm; d.post_norm = ly.post_norm; d.q_norm = ly.q_norm; d.k_norm = ly.k_norm;
+        d.kc = ly.kc; d.vc = ly.vc;
+    }
+    HIPCHECK(hipStreamSynchronize(m->stream));
+    m->tile_layers = host;
+    return MLXR_OK;
+}
+
 static int mega_setup(Model* m) {
     const Config& c = m->cfg;
     auto no = [&](const std::string& why) { m->mega_ok = false; m->mega_reason = why; return MLXR_OK; };
-    auto four_bf16 = [&](const Lin& l) { return l.bits == 4 && l.st == 0 && l.K % 128 == 0 && (l.gs == 32 || l.gs == 64) && l.gs == m->head.gs; };
+    auto four_bf16 = [&](const Lin& l) { return repackable(l) && l.gs == m->head.gs; };
     if (!four_bf16(m->embed) || !four_bf16(m->head)) return no("embedding / lm_head not 4-bit bf16");
+    if ((int)m->tile_layers.size() != c.L) return no("projections not repackable (4-bit, bf16 scales, gs 32/64, K % 128)");
     for (auto& ly : m->layers)
         for (const Lin* l : {&ly.q, &ly.k, &ly.v, &ly.o, &ly.gate, &ly.up, &ly.down})
-            if (!four_bf16(*l)) return no("a projection is not 4-bit with bf16 scales");
+            if (!four_bf16(*l)) return no("a projection's group size differs from the lm_head's");
     if (c.D != 128 || c.nH / c.nKV > 8 || c.rot_dim > 128) return no("head shape");
     if (5 * c.L + 2 > 1023) return no("too many layers for the exchange tags");
     hipDeviceProp_t prop;
@@ -356,41 +403,12 @@ static int mega_setup(Model* m) {
     if (lds > 150 * 1024) return no("LDS need " + std::to_string(lds >> 10) + " KiB");
     if (mega_set_lds_limit(lds) != hipSuccess) return no("LDS attribute");
     if (nwg > MEGA_MAX_WG) return no("too many workgroups");
-    // each phase's matrices, repacked once into the decode tile layout (a second copy of the weights)
+    // the layers' repacked phases (tiles_setup), plus the lm_head's
     int rc = MLXR_OK;
-    auto desc = [&](const Lin* parts, int n, bool gated) {
-        MvPhaseDesc d{};
-        DPackSrc src{};
-        for (int i = 0; i < 3; i++) {
-            const Lin& l = parts[i < n ? i : n - 1];
-            src.w[i] = reinterpret_cast<const uint8_t*>(l.m.w); src.s[i] = l.m.s; src.b[i] = l.m.b;
-            d.bias[i] = l.m.bias;
-        }
-        d.o1 = src.o1 = parts[0].O; d.o2 = src.o2 = n > 1 ? parts[1].O : 0;
-        int rows = 0; for (int i = 0; i < n; i++) rows += parts[i].O;
-        d.rows = src.rows = rows; d.K = src.K = parts[0].K; d.gs = src.gs = parts[0].gs; d.gated = src.gated = gated ? 1 : 0;
-        d.tiles = dpack_tiles(src);
-        uint8_t* code = nullptr;
-        if (rc == MLXR_OK) rc = dalloc(m, &code, dpack_bytes(src));
-        if (rc == MLXR_OK && launch_dpack(src, code, m->stream) != hipSuccess) rc = set_error(MLXR_E_GPU, "repack launch");
-        d.code = code;
-        return d;
-    };
-    std::vector<LayerDev> host(c.L);
-    for (int i = 0; i < c.L; i++) {
-        const Layer& ly = m->layers[i];
-        const Lin qkv[3] = {ly.q, ly.k, ly.v}, gu[2] = {ly.gate, ly.up};
-        LayerDev& d = host[i];
-        d.qkv = desc(qkv, 3, false); d.o = desc(&ly.o, 1, false); d.gu = desc(gu, 2, true); d.down = desc(&ly.down, 1, false);
-        if (rc) return rc;
-        d.in_norm = ly.in_norm; d.post_norm = ly.post_norm; d.q_norm = ly.q_norm; d.k_norm = ly.k_norm;
-        d.kc = ly.kc; d.vc = ly.vc;
-    }
     if ((rc = dalloc(m, &m->mega_layers, c.L))) return rc;
-    HIPCHECK(hipMemcpy(m->mega_layers, host.data(), sizeof(LayerDev) * c.L, hipMemcpyHostToDevice));
-    m->tile_layers = host;
+    HIPCHECK(hipMemcpy(m->mega_layers, m->tile_layers.data(), sizeof(LayerDev) * c.L, hipMemcpyHostToDevice));
     a.layers = m->mega_layers; a.L = c.L;
-    a.head = desc(&m->head, 1, false);
+    a.head = repack_phase(m, &m->head, 1, false, rc);
     if (rc) return rc;
     HIPCHECK(hipStreamSynchronize(m->stream));
     a.embed_w = m->embed.m.w; a.embed_s = m->embed.m.s; a.embed_b = m->embed.m.b; a.embed_gs = m->embed.gs;
@@ -557,7 +575,7 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
     *m->abort_host = 0;
     for (auto& s : m->slots) { HIPCHECK(hipEventCreate(&s.start)); HIPCHECK(hipEventCreate(&s.stop)); }
     if ((rc = model_seed(m, 0))) return fail(rc);
-    if ((rc = mega_setup(m))) return fail(rc);
+    if ((rc = tiles_setup(m)) || (rc = mega_setup(m))) return fail(rc);
     *out = m;
     return MLXR_OK;
 }
