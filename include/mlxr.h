@@ -115,8 +115,10 @@ int mlxr_read_kv(mlxr_model* m, int layer, int rows, float* k_out, float* v_out)
  * algorithmic bytes per launch. Profiling hook in the spirit of Transformer.profile()
  * (Transformer.swift:1696-1798). */
 int mlxr_profile_kernel(mlxr_model* m, const char* kind, int iters, int context, double* avg_ms, int64_t* bytes);
-/* Decode step implementation: 1 (default) = the persistent kernel (one launch per token, grid
- * barriers between phases) where the model allows it, 0 = one kernel per operation. */
+/* Decode step implementation: 1 (default) = the persistent kernel (one launch per token, tagged
+ * hand-over between phases) where the model allows it, 0 = one kernel per operation (projections
+ * over the repacked weight tiles where the model has them), 2 = one kernel per operation on the
+ * MLX weight layout. Fails while a step is in flight. */
 int mlxr_set_decode_mode(mlxr_model* m, int mode);
 /* Runs one persistent greedy decode step at `offset` with wall-clock marks at every phase boundary:
  * out[3e..3e+2] = mean start, mean end, latest end (us) of interval e over the workgroups

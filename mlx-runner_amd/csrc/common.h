@@ -27,17 +27,49 @@ template <int ST> __device__ __forceinline__ float ld_scale(const uint16_t* p) {
     return ST == 0 ? bf16_to_f32(*p) : f16_to_f32(*p);
 }
 
-// Wave reductions (64 lanes) ---------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Cross-lane reductions (64 lanes) without LDS: DPP within rows of 16 lanes, then the gfx950
+// permlane swaps across rows. Every lane receives the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_sum(float v) {   // lanes 4q .. 4q + 3
+    v += dpp<0xB1>(v);            // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);            // quad_perm [2,3,0,1]
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+__device__ __forceinline__ float row16_sum(float v) {
+    v = quad_sum(v);
+    v += dpp<0x141>(v);           // row_half_mirror: 8-lane sums
+    v += dpp<0x140>(v);           // row_mirror: 16-lane sums
     return v;
 }
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    return v;
+}
+// v[l] (+) v[l ^ 16] and v[l] (+) v[l ^ 32]: the swap returns (own row pair, partner row pair).
+__device__ __forceinline__ float xor16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float wave_sum(float v) { return xor32_sum(xor16_sum(row16_sum(v))); }
+__device__ __forceinline__ float wave_max(float v) { return xor32_max(xor16_max(row16_max(v))); }
 
 // KV cache addressing: layer cache [n_pages][nKV][PAGE][D] bf16; pt maps logical page -> physical.
 __device__ __forceinline__ int64_t kv_row(const int* __restrict__ pt, int nKV, int kvh, int pos) {

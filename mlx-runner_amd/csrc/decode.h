@@ -28,6 +28,12 @@ bool tile_gemm_supported(const MvPhaseDesc& p);
 hipError_t launch_tile_gemm(const MvPhaseDesc& p, const uint16_t* xh, const float* inv, int T, float* y, int ys,
                             hipStream_t s);
 
+// Batch-1 matvec over a repacked matrix (the kernel-per-op decode step): mode 0 y = W x (+ bias),
+// 1 y += W x (+ bias), 2 y[o1] = SiLU(gate) * up; norm_w: x := RMSNorm(x) * norm_w first.
+bool dpack_mv_supported(const MvPhaseDesc& p);
+hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* norm_w, float eps, float* y, int mode,
+                           hipStream_t s);
+
 struct LayerDev {
     MvPhaseDesc qkv, o, gu, down;
     const float* in_norm; const float* post_norm; const float* q_norm; const float* k_norm;

@@ -81,6 +81,7 @@ struct QkvPostArgs {
     int D = 128, nH = 0, nKV = 0, rot_dim = 128, traditional = 0, T = 1;
     const int* dpos = nullptr; int pos_add = 0;
     float eps = 1e-6f;
+    uint16_t* idx = nullptr;            // sparse block index: written for a block the step completes (T == 1)
 };
 hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
 

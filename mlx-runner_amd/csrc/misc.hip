@@ -200,8 +200,18 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
         const float c = cosf(ang), sn = sinf(ang);
         out = first ? v * c - buf[partner] * sn : v * c + buf[partner] * sn;
     }
-    if (isQ) base[i] = out;
-    else a.kc[kv_row(a.pt, a.nKV, h - a.nH, pos) * D + i] = f32_to_bf16(out);
+    if (isQ) { base[i] = out; return; }
+    const int kvh = h - a.nH;
+    const uint16_t kb = f32_to_bf16(out);
+    a.kc[kv_row(a.pt, a.nKV, kvh, pos) * D + i] = kb;
+    if (a.idx && a.T == 1 && (pos & 3) == 3) {
+        // the block of keys pos - 3 .. pos is complete: its index row is the bf16 mean of the four
+        // keys, summed in position order as sparse_index_kernel does
+        float sum = 0.0f;
+        for (int j = pos - 3; j < pos; j++) sum += bf16_to_f32(a.kc[kv_row(a.pt, a.nKV, kvh, j) * D + i]);
+        sum += bf16_to_f32(kb);
+        a.idx[((int64_t)(pos >> 2) * a.nKV + kvh) * D + i] = f32_to_bf16(sum / 4.0f);
+    }
 }
 
 hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {

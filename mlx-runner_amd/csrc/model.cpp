@@ -366,6 +366,8 @@ static int tiles_setup(Model* m) {
         d.in_norm = ly.in_norm; d.post_norm = ly.post_norm; d.q_norm = ly.q_norm; d.k_norm = ly.k_norm;
         d.kc = ly.kc; d.vc = ly.vc;
     }
+    if (repackable(m->head)) m->tile_head = repack_phase(m, &m->head, 1, false, rc);
+    if (rc) return rc;
     HIPCHECK(hipStreamSynchronize(m->stream));
     m->tile_layers = host;
     return MLXR_OK;
@@ -408,9 +410,7 @@ static int mega_setup(Model* m) {
     if ((rc = dalloc(m, &m->mega_layers, c.L))) return rc;
     HIPCHECK(hipMemcpy(m->mega_layers, m->tile_layers.data(), sizeof(LayerDev) * c.L, hipMemcpyHostToDevice));
     a.layers = m->mega_layers; a.L = c.L;
-    a.head = repack_phase(m, &m->head, 1, false, rc);
-    if (rc) return rc;
-    HIPCHECK(hipStreamSynchronize(m->stream));
+    a.head = m->tile_head;
     a.embed_w = m->embed.m.w; a.embed_s = m->embed.m.s; a.embed_b = m->embed.m.b; a.embed_gs = m->embed.gs;
     a.final_norm = m->final_norm; a.inv_freq = m->inv_freq;
     a.eps = c.eps; a.scale = c.query_scale * c.rope_attention_factor * c.rope_attention_factor;
@@ -442,7 +442,15 @@ static int mega_setup(Model* m) {
 }
 
 int model_set_decode_mode(Model* m, int mode) {
-    if (mode != 0 && mode != 1) return set_error(MLXR_E_INVALID_ARG, "decode mode: 0 (kernel per op) or 1 (persistent)");
+    if (mode < 0 || mode > 2)
+        return set_error(MLXR_E_INVALID_ARG, "decode mode: 0 (kernel per op), 1 (persistent) or 2 (kernel per op, MLX layout)");
+    for (auto& s : m->slots)
+        if (s.busy) return set_error(MLXR_E_INVALID_ARG, "decode mode change with a step in flight");
+    if (mode != m->decode_mode) {   // captured steps hold the previous mode's kernels
+        HIPCHECK(hipStreamSynchronize(m->stream));
+        for (auto& g : m->graphs) hipGraphExecDestroy(g.second);
+        m->graphs.clear();
+    }
     m->decode_mode = mode;
     return MLXR_OK;
 }
@@ -654,18 +662,22 @@ int encode_decode(Model* m, const mlxr_sample_params* sp, bool sparse, bool logi
         sa.min_context = m->sparse.min_context; sa.dplan = m->sp_plan;
         HIPCHECK(launch_sparse_plan(sa, s));
     }
+    // projections over the repacked tiles where the model has them (decode mode 2: the MLX layout)
+    const bool dmv = m->decode_mode != 2 && (int)m->tile_layers.size() == c.L;
     for (int li = 0; li < c.L; li++) {
         Layer& ly = m->layers[li];
+        const LayerDev* tl = dmv ? &m->tile_layers[li] : nullptr;
         const Lin qkvp[3] = {ly.q, ly.k, ly.v};
-        HIPCHECK(launch_qmv(qmv_args(qkvp, 3, m->h, ly.in_norm, c.eps, m->qkv, EPI_STORE), s));
+        if (tl) HIPCHECK(launch_dpack_mv(tl->qkv, m->h, ly.in_norm, c.eps, m->qkv, 0, s));
+        else HIPCHECK(launch_qmv(qmv_args(qkvp, 3, m->h, ly.in_norm, c.eps, m->qkv, EPI_STORE), s));
         QkvPostArgs pa; pa.qkv = m->qkv; pa.row_stride = m->qkv_cols; pa.inv_freq = m->inv_freq; pa.kc = ly.kc; pa.vc = ly.vc;
         pa.pt = m->page_table; pa.qn = ly.q_norm; pa.kn = ly.k_norm; pa.D = c.D; pa.nH = c.nH; pa.nKV = c.nKV;
         pa.rot_dim = c.rot_dim; pa.traditional = c.traditional; pa.T = 1; pa.dpos = m->dpos; pa.eps = c.eps;
+        pa.idx = m->sparse_alloc ? ly.idx : nullptr;   // the index row of a block this step completes
         HIPCHECK(launch_qkv_post(pa, s));
         AttnArgs aa; aa.q = m->qkv; aa.q_stride = m->qkv_cols; aa.kc = ly.kc; aa.vc = ly.vc; aa.pt = m->page_table;
         aa.out = m->attn; aa.out_stride = c.nH * c.D; aa.part = m->part; aa.D = c.D; aa.nH = c.nH; aa.nKV = c.nKV; aa.T = 1;
         aa.nsplit = m->nsplit_dec; aa.dpos = m->dpos; aa.scale = c.query_scale * c.rope_attention_factor * c.rope_attention_factor;
-        if (m->sparse_alloc) HIPCHECK(launch_sparse_index(ly.kc, m->page_table, ly.idx, c.nKV, c.D, m->dpos, 0, 1, s));
         if (sparse) {
             SparseArgs sa; sa.kc = ly.kc; sa.pt = m->page_table; sa.idx = ly.idx; sa.q = m->qkv; sa.scores = m->sp_scores;
             sa.lists = m->sp_lists; sa.list_stride = m->sparse.per_head ? m->max_seq : 0; sa.nKV = c.nKV; sa.nH = c.nH; sa.D = c.D;
@@ -675,12 +687,21 @@ int encode_decode(Model* m, const mlxr_sample_params* sp, bool sparse, bool logi
             aa.lists = m->sp_lists; aa.list_stride = sa.list_stride; aa.splan = m->sp_plan;
         }
         HIPCHECK(launch_attn_decode(aa, s));
-        HIPCHECK(launch_qmv(qmv_args(&ly.o, 1, m->attn, nullptr, 0, m->h, EPI_ADD), s));
         const Lin gup[2] = {ly.gate, ly.up};
-        HIPCHECK(launch_qmv(qmv_args(gup, 2, m->h, ly.post_norm, c.eps, m->mlp, EPI_GATED), s));
-        HIPCHECK(launch_qmv(qmv_args(&ly.down, 1, m->mlp, nullptr, 0, m->h, EPI_ADD), s));
+        if (tl) {
+            HIPCHECK(launch_dpack_mv(tl->o, m->attn, nullptr, 0, m->h, 1, s));
+            HIPCHECK(launch_dpack_mv(tl->gu, m->h, ly.post_norm, c.eps, m->mlp, 2, s));
+            HIPCHECK(launch_dpack_mv(tl->down, m->mlp, nullptr, 0, m->h, 1, s));
+        } else {
+            HIPCHECK(launch_qmv(qmv_args(&ly.o, 1, m->attn, nullptr, 0, m->h, EPI_ADD), s));
+            HIPCHECK(launch_qmv(qmv_args(gup, 2, m->h, ly.post_norm, c.eps, m->mlp, EPI_GATED), s));
+            HIPCHECK(launch_qmv(qmv_args(&ly.down, 1, m->mlp, nullptr, 0, m->h, EPI_ADD), s));
+        }
     }
-    if (logits || sp) HIPCHECK(launch_qmv(qmv_args(&m->head, 1, m->h, m->final_norm, c.eps, m->logits, EPI_STORE), s));
+    if (logits || sp) {
+        if (dmv && m->tile_head.code) HIPCHECK(launch_dpack_mv(m->tile_head, m->h, m->final_norm, c.eps, m->logits, 0, s));
+        else HIPCHECK(launch_qmv(qmv_args(&m->head, 1, m->h, m->final_norm, c.eps, m->logits, EPI_STORE), s));
+    }
     if (sp) return encode_sample(m, c.V, sp, true);
     return MLXR_OK;
 }

@@ -86,10 +86,11 @@ struct Model {
     bool use_graphs = true;
     // persistent decode step (decode.hip)
     bool mega_ok = false;            // the model fits the persistent kernel's constraints
-    int decode_mode = 1;             // 1: persistent kernel when eligible, 0: kernel per op
+    int decode_mode = 1;             // 1: persistent kernel when eligible, 0: kernel per op, 2: kernel per op on the MLX layout
     MegaArgs mega{};
     LayerDev* mega_layers = nullptr;
     std::vector<LayerDev> tile_layers;  // host copy of the repacked phases: the prefill GEMMs use them too
+    MvPhaseDesc tile_head{};            // repacked lm_head (code == nullptr: none)
     int mega_nwg = 0; size_t mega_lds = 0;
     std::string mega_reason;
     double last_gpu_time = 0;

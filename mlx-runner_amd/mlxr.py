@@ -281,8 +281,10 @@ class Transformer:
         check(lib.mlxr_profile_kernel(self._h, kind.encode(), iters, context, C.byref(ms), C.byref(b)))
         return ms.value, b.value
 
-    def set_decode_mode(self, persistent: bool):
-        check(lib.mlxr_set_decode_mode(self._h, 1 if persistent else 0))
+    def set_decode_mode(self, mode):
+        """True / 1: the persistent step where the model allows it; False / 0: one kernel per operation
+        (repacked tiles where the model has them); 2: one kernel per operation on the MLX layout."""
+        check(lib.mlxr_set_decode_mode(self._h, int(mode)))
 
     @property
     def persistent_decode(self) -> bool:

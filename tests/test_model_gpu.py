@@ -116,6 +116,25 @@ def test_persistent_decode_matches_kernel_per_op(gpu, models, name):
             assert abs(logits[a[i]] - logits[b[i]]) < LOGIT_TOL
 
 
+@pytest.mark.parametrize("name", ["qwen3", "qwen2", "llama"])
+def test_decode_tiles_match_mlx_layout(gpu, models, name):
+    """Single-token steps of the kernel-per-op path: the matvecs over the repacked tiles (decode mode
+    0) against the MLX-layout matvecs (mode 2) and the oracle, logits within the 2e-2 gate."""
+    d = models[name]
+    toks = prompt(12, 1000, seed=21)
+    with mlxr.Transformer(d, context_length=512) as m:
+        ref = oracle.Model(d, m.max_seq)
+        want = ref.forward(toks, 0)
+        got = {}
+        for mode in (0, 2):
+            m.set_decode_mode(mode)
+            for i, t in enumerate(toks):
+                got[mode] = m.forward(np.array([t], np.int32), i)
+        assert np.max(np.abs(got[0] - got[2])) < LOGIT_TOL
+        assert np.max(np.abs(got[0] - want)) < LOGIT_TOL
+        assert np.argmax(got[0]) == np.argmax(want)
+
+
 def test_prefill_vs_incremental_decode(gpu, models):
     """ModelTests.swift:50-69: same argmax and max |d logit| < 0.1 (here: the 2e-2 gate)."""
     d = models["qwen3"]
