@@ -366,31 +366,20 @@ __device__ __forceinline__ uint32_t sparse_key(float f) {
 
 // Exact selection (Kernels.swift:1628-1710): the p highest keys (ties: earlier block first), the
 // attended positions written in ascending order. One 1024-thread workgroup per row.
-// The row's keys are read once into LDS. Four 8-bit radix passes find the p-th largest key: a
-// wave folds lanes that share a bin into one LDS add (the leading passes see few distinct bins, so
-// plain atomics would serialise), and one wave scans the 256 bins with a lane prefix sum. A final
+// The row's keys are read once into LDS. Four 8-bit radix passes find the p-th largest key. The
+// histogram has 16 copies (lane % 16 picks one), so lanes adding to the same bin, common in the
+// leading passes, rarely hit the same LDS address; one wave sums the copies and scans the 256 bins
+// with a lane prefix sum. A final
 // pass counts, per thread's contiguous range, keys above the threshold and equal to it, and a
 // workgroup scan gives each range its output slots.
 constexpr int SEL_NT = 1024;
-constexpr int SEL_MAXN = 36864;   // keys per row held in LDS (max)
-__device__ __forceinline__ void sel_hist_add(uint32_t* hist, uint32_t bin, bool on) {
-    // fold lanes that share a bin: up to 4 leaders, then plain atomics for the rest
-    uint64_t act = __ballot(on);
-    for (int it = 0; it < 4 && act; it++) {
-        const int ld = __ffsll((long long)act) - 1;
-        const uint32_t lb = (uint32_t)__builtin_amdgcn_readlane((int)bin, ld);
-        const uint64_t m = __ballot(on && bin == lb);
-        if ((int)(threadIdx.x & 63) == ld) atomicAdd(&hist[lb], (uint32_t)__popcll(m));
-        if (bin == lb) on = false;
-        act &= ~m;
-    }
-    if (on) atomicAdd(&hist[bin], 1u);
-}
+constexpr int SEL_MAXN = 32768;   // keys per row held in LDS (max; 128 KiB beside the 16 KiB histogram)
 __global__ __launch_bounds__(SEL_NT) void sparse_select_kernel(const float* all_scores, int* all_lists, int list_stride,
                                                                int score_stride, const SparsePlanDev* plan,
                                                                SparsePlanDev fixed) {
     extern __shared__ uint32_t keys[];
-    __shared__ uint32_t hist[256];
+    constexpr int HC = 16;                      // histogram copies
+    __shared__ uint32_t hist[256 * HC];         // [bin][copy]
     __shared__ uint32_t pick[2];
     __shared__ uint32_t sgt[16], seq_[16];
     SparsePlanDev P = fixed;
@@ -408,19 +397,24 @@ __global__ __launch_bounds__(SEL_NT) void sparse_select_kernel(const float* all_
     }
     uint32_t prefix = 0, mask = 0, want = (uint32_t)P.p;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        if (tid < 256) hist[tid] = 0;
+        for (int i = tid; i < 256 * HC; i += SEL_NT) hist[i] = 0;
         __syncthreads();
-        for (int nb = 0; nb < N; nb += SEL_NT) {   // uniform trip count: every lane takes part in the ballots
-            const int n = nb + tid;
-            const uint32_t k = n < N ? keys[n] : 0u;
-            sel_hist_add(hist, (k >> shift) & 255u, n < N && (k & mask) == prefix);
+        for (int n = tid; n < N; n += SEL_NT) {
+            const uint32_t k = keys[n];
+            if ((k & mask) == prefix) atomicAdd(&hist[((k >> shift) & 255u) * HC + (lane & (HC - 1))], 1u);
         }
         __syncthreads();
         if (wave == 0) {
             // lane l: bins 255 - 4l .. 252 - 4l (descending); inclusive prefix over lanes = keys in bins >= 252 - 4l
             uint32_t c[4], tot = 0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) { c[i] = hist[255 - 4 * lane - i]; tot += c[i]; }
+            for (int i = 0; i < 4; i++) {
+                const uint4* h4 = reinterpret_cast<const uint4*>(hist + (255 - 4 * lane - i) * HC);
+                uint32_t sum = 0;
+#pragma unroll
+                for (int q = 0; q < HC / 4; q++) { const uint4 v = h4[q]; sum += (v.x + v.y) + (v.z + v.w); }
+                c[i] = sum; tot += sum;
+            }
             uint32_t inc = tot;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
