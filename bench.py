@@ -291,6 +291,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=360)
     ap.add_argument("--step-iters", type=int, default=64)
+    ap.add_argument("--decode-mode", type=int, default=1, choices=[0, 1, 2],
+                    help="1: persistent decode step, 0: kernel per op (repacked tiles), 2: kernel per op (MLX layout)")
     ap.add_argument("--mode", default="decode", choices=["decode", "prefill", "sweep", "long"],
                     help="decode: configs[1] (default); prefill: configs[2] (llama3-8b, 2048 tokens unless given); "
                          "sweep: configs[3]; long: configs[4] (qwen2.5-32b, 32768-token context, sparse)")
@@ -341,6 +343,7 @@ def main():
     t = time.time()
     model = mlxr.Transformer(d, context_length=need)
     log(f"[bench] model loaded in {time.time() - t:.1f}s ({model.weight_bytes / 1e9:.2f} GB of weights, {model.quant_description})")
+    model.set_decode_mode(a.decode_mode)
     greedy = mlxr.SamplingParameters.greedy()
     prompt = np.random.default_rng(a.seed).integers(0, model.vocab_size, a.context).astype(np.int32)
 

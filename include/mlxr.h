@@ -184,6 +184,13 @@ int mlxr_k_qgemm(const mlxr_qmat* mat, int K, int bits, int gs, int st, int T, c
  * (the MLP's gate|up, silu_mul Kernels.swift:2004-2013). Repacks into a temporary buffer per call. */
 int mlxr_k_qgemm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int gated, int T, const float* x,
                        int x_stride, float* y, int y_stride);
+/* Batch-1 matvec over the repacked tiles, the kernel-per-op decode step's projection (`qmv` with
+ * its fused epilogues, Kernels.swift:60-113, 1037-1070, 2004-2013): mode 0 y = W x (+ bias),
+ * 1 y += W x (+ bias), 2 (two parts of equal O) y[o] = silu(A x)[o] * (B x)[o]; norm_w (or NULL)
+ * first replaces x by RMSNorm(x) * norm_w (eps). Same quantization limits as mlxr_k_qgemm_tiles,
+ * K <= 32768. `reps` launches back to back (timing; mode 1 then adds reps times). */
+int mlxr_k_qmv_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode, const float* x, const float* norm_w,
+                     float eps, float* y, int reps);
 /* Quantized embedding rows (`qembed`, Kernels.swift:1002-1023): ids device int32 [T]. */
 int mlxr_k_qembed(const mlxr_qmat* mat, int K, int bits, int gs, int st, const int32_t* ids, int T, float* out);
 /* RMSNorm rows (`rms_norm`, Kernels.swift:1037-1070), fp32 weights; add_rms_norm with r != NULL. */

@@ -227,19 +227,15 @@ int mlxr_k_qgemm(const mlxr_qmat* mat, int K, int bits, int gs, int st, int T, c
     return done(launch_qgemm(a, g_stream));
 }
 
-int mlxr_k_qgemm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int gated, int T, const float* x, int x_stride,
-                       float* y, int y_stride) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    if (int rc = ensure_stream()) return rc;
+// Repacks the parts into a temporary DPack (freed by the caller).
+static int tiles_pack(const mlxr_qmat* parts, int nparts, int K, int gs, int gated, MvPhaseDesc& d, uint8_t*& code) {
     if (int rc = check_parts(parts, nparts)) return rc;
     if ((gs != 32 && gs != 64) || K % 128) return set_error(MLXR_E_INVALID_ARG, "repacked tiles need gs 32/64 and K % 128 == 0");
     if (gated && (nparts != 2 || parts[0].O != parts[1].O)) return set_error(MLXR_E_INVALID_ARG, "gated: two parts of equal O");
+    DPackSrc src{};
+    d = MvPhaseDesc{};
     int rows = 0;
     for (int i = 0; i < nparts; i++) rows += parts[i].O;
-    const int out_cols = gated ? parts[0].O : rows;
-    if (T < 1 || !x || !y || x_stride < K || y_stride < out_cols || x_stride % 4) return set_error(MLXR_E_INVALID_ARG, "T / strides");
-    DPackSrc src{};
-    MvPhaseDesc d{};
     for (int i = 0; i < 3; i++) {
         const mlxr_qmat& q = parts[i < nparts ? i : nparts - 1];
         src.w[i] = static_cast<const uint8_t*>(q.w);
@@ -249,14 +245,44 @@ int mlxr_k_qgemm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int ga
     d.o1 = src.o1 = parts[0].O; d.o2 = src.o2 = nparts > 1 ? parts[1].O : 0;
     d.rows = src.rows = rows; d.K = src.K = K; d.gs = src.gs = gs; d.gated = src.gated = gated ? 1 : 0;
     d.tiles = dpack_tiles(src);
-    if (int rc = ensure_buf(g_xbf, g_xbf_elems, (size_t)T * K)) return rc;
-    if (int rc = ensure_buf(g_xsc, g_xsc_elems, (size_t)T)) return rc;
-    uint8_t* code = nullptr;
+    code = nullptr;
     CK(hipMalloc(&code, dpack_bytes(src)));
     d.code = code;
-    hipError_t e = launch_dpack(src, code, g_stream);
-    if (e == hipSuccess) e = launch_x_to_f16(x, x_stride, K, T, g_xbf, g_xsc, g_stream);
+    const hipError_t e = launch_dpack(src, code, g_stream);
+    if (e != hipSuccess) { hipFree(code); code = nullptr; return done(e); }
+    return MLXR_OK;
+}
+
+int mlxr_k_qgemm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int gated, int T, const float* x, int x_stride,
+                       float* y, int y_stride) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (int rc = ensure_stream()) return rc;
+    int rows = 0;
+    for (int i = 0; i < nparts && parts; i++) rows += parts[i].O;
+    const int out_cols = gated ? (parts ? parts[0].O : 0) : rows;
+    if (T < 1 || !x || !y || x_stride < K || y_stride < out_cols || x_stride % 4) return set_error(MLXR_E_INVALID_ARG, "T / strides");
+    MvPhaseDesc d; uint8_t* code;
+    if (int rc = tiles_pack(parts, nparts, K, gs, gated, d, code)) return rc;
+    if (int rc = ensure_buf(g_xbf, g_xbf_elems, (size_t)T * K)) { hipFree(code); return rc; }
+    if (int rc = ensure_buf(g_xsc, g_xsc_elems, (size_t)T)) { hipFree(code); return rc; }
+    hipError_t e = launch_x_to_f16(x, x_stride, K, T, g_xbf, g_xsc, g_stream);
     if (e == hipSuccess) e = launch_tile_gemm(d, g_xbf, g_xsc, T, y, y_stride, g_stream);
+    const hipError_t e2 = hipStreamSynchronize(g_stream);
+    hipFree(code);
+    if (e == hipSuccess) e = e2;
+    return done(e);
+}
+
+int mlxr_k_qmv_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode, const float* x, const float* norm_w, float eps,
+                     float* y, int reps) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (int rc = ensure_stream()) return rc;
+    if (mode < 0 || mode > 2 || !x || !y || reps < 1) return set_error(MLXR_E_INVALID_ARG, "mode / pointers / reps");
+    MvPhaseDesc d; uint8_t* code;
+    if (int rc = tiles_pack(parts, nparts, K, gs, mode == 2, d, code)) return rc;
+    if (!dpack_mv_supported(d)) { hipFree(code); return set_error(MLXR_E_UNSUPPORTED, "matvec over repacked tiles: K too large"); }
+    hipError_t e = hipSuccess;
+    for (int r = 0; r < reps && e == hipSuccess; r++) e = launch_dpack_mv(d, x, norm_w, eps, y, mode, g_stream);
     const hipError_t e2 = hipStreamSynchronize(g_stream);
     hipFree(code);
     if (e == hipSuccess) e = e2;

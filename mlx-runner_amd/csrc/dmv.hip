@@ -1,0 +1,134 @@
+// Standalone batch-1 matvec over the repacked weight tiles: one launch per projection of the
+// kernel-per-op decode step. Kept in its own translation unit, apart from the persistent decode
+// kernel: sharing that kernel's code object slowed it by ~70% (measured), so each gets its own.
+#include <algorithm>
+#include "mv.h"
+
+namespace mlxr {
+
+constexpr int DMV_MAX_K = 32768;     // input length of the standalone matvec (max)
+constexpr int DMV_MAX_LDS = 160 * 1024;
+
+// One projection of the kernel-per-op decode step (the path for steps the persistent kernel does
+// not take: sparse attention, models outside its limits, decode mode 0) over the same repacked
+// tiles: y = W x (+ bias), y += W x, or y = SiLU(W_g x) * (W_u x), x optionally RMSNorm(x) * w.
+// Every workgroup issues its first scale group of weights, then packs x straight from global
+// memory (one pass for the norm statistics and max |x|, one to pack), so large inputs (K up to
+// 32768) fit in LDS without an f32 copy.
+template <int FB, int MODE>
+__global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, const float* __restrict__ x,
+                                                              const float* __restrict__ nw, float eps, float* __restrict__ y, int tpw) {
+    constexpr int GSH = FB == 4 ? 5 : 6;
+    extern __shared__ float lds[];
+    const int K = p.K;
+    MvLds L;
+    L.xf = nullptr; L.hown = nullptr;
+    L.xh = lds;
+    L.gsum = L.xh + (K >> 5) * XH_STRIDE;
+    L.zero16 = L.gsum + 2 * (K >> GSH);
+    L.part = L.zero16 + 4;
+    float* red = L.part + tpw * MK_WAVES * 16;
+    const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    Ring<FB> ring;
+    mv_prefetch<FB>(p, wg, nwg, wave, lane, ring);
+    // statistics: sum of squares of x, max |x w| (max |x| without a norm)
+    float ss = 0.0f, mx = 0.0f;
+    for (int i = threadIdx.x * 4; i < K; i += MK_THREADS * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(x + i);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        float4 a = v;
+        if (nw) {
+            const float4 w = *reinterpret_cast<const float4*>(nw + i);
+            a.x *= w.x; a.y *= w.y; a.z *= w.z; a.w *= w.w;
+        }
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    }
+    ss = wave_sum(ss); mx = wave_max(mx);
+    if (lane == 0) { red[wave] = ss; red[8 + wave] = mx; }
+    __syncthreads();
+    float tot = 0.0f, gmax = 0.0f;
+    for (int i = 0; i < MK_WAVES; i++) { tot += red[i]; gmax = fmaxf(gmax, red[8 + i]); }
+    const float inv = nw ? 1.0f / sqrtf(tot / (float)K + eps) : 1.0f;
+    float unscale;
+    if (nw) {
+        auto ld = [x, nw, inv](int t, float4& lo, float4& hi) {
+            lo = *reinterpret_cast<const float4*>(x + 8 * t); hi = *reinterpret_cast<const float4*>(x + 8 * t + 4);
+            const float4 wl = *reinterpret_cast<const float4*>(nw + 8 * t), wh = *reinterpret_cast<const float4*>(nw + 8 * t + 4);
+            lo.x = lo.x * inv * wl.x; lo.y = lo.y * inv * wl.y; lo.z = lo.z * inv * wl.z; lo.w = lo.w * inv * wl.w;
+            hi.x = hi.x * inv * wh.x; hi.y = hi.y * inv * wh.y; hi.z = hi.z * inv * wh.z; hi.w = hi.w * inv * wh.w;
+        };
+        unscale = pack_x16_from(ld, K, gmax * inv, L, GSH);
+    } else {
+        auto ld = [x](int t, float4& lo, float4& hi) {
+            lo = *reinterpret_cast<const float4*>(x + 8 * t); hi = *reinterpret_cast<const float4*>(x + 8 * t + 4);
+        };
+        unscale = pack_x16_from(ld, K, gmax, L, GSH);
+    }
+    mv_run<FB>(p, L.xh, L.gsum, L.zero16, wg, nwg, wave, lane, ring, L.part);
+    __syncthreads();
+    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
+    const int nfw = g.nt * g.NF;
+    if (MODE == OUT_GATED) {
+        for (int i = threadIdx.x; i < g.nt * 8; i += MK_THREADS) {
+            const int tl = i >> 3, j = i & 7, o = 8 * (g.t0 + tl) + j;
+            if (o < p.o1) {
+                const float gv = tile_row(L.part, tl, j, nfw, g.NF) * unscale;
+                const float uv = tile_row(L.part, tl, j + 8, nfw, g.NF) * unscale;
+                y[o] = (gv / (1.0f + expf(-gv))) * uv;
+            }
+        }
+        return;
+    }
+    for (int i = threadIdx.x; i < g.nt * 16; i += MK_THREADS) {
+        const int row = 16 * g.t0 + i;
+        if (row >= p.rows) break;
+        const float v = tile_row(L.part, i >> 4, i & 15, nfw, g.NF) * unscale + row_bias(p, row);
+        if (MODE == OUT_ADD) y[row] += v;
+        else y[row] = v;
+    }
+}
+
+template <int FB, int MODE>
+static hipError_t dmv_launch(const MvPhaseDesc& p, const float* x, const float* nw, float eps, float* y, int nwg, int tpw,
+                             size_t lds, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute((const void*)dpack_mv_kernel<FB, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 DMV_MAX_LDS);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((dpack_mv_kernel<FB, MODE>), dim3(nwg), dim3(MK_THREADS), lds, s, p, x, nw, eps, y, tpw);
+    return hipGetLastError();
+}
+
+bool dpack_mv_supported(const MvPhaseDesc& p) {
+    return (p.gs == 32 || p.gs == 64) && p.K % 128 == 0 && p.K <= DMV_MAX_K && p.tiles > 0 && p.code;
+}
+
+hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* norm_w, float eps, float* y, int mode,
+                           hipStream_t s) {
+    if (!dpack_mv_supported(p) || mode < 0 || mode > 2) return hipErrorInvalidValue;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return hipErrorInvalidDevice;
+    }
+    const int nwg = std::min(p.tiles, 4 * cus);
+    const int tpw = (p.tiles + nwg - 1) / nwg;
+    if (tpw > MK_TPW) return hipErrorInvalidValue;
+    const size_t lds = sizeof(float) * ((size_t)(p.K >> 5) * XH_STRIDE + 2 * (p.K / p.gs) + 4 + (size_t)tpw * MK_WAVES * 16 + 16);
+    if (lds > DMV_MAX_LDS) return hipErrorInvalidValue;
+    const bool fb4 = p.gs == 32;
+    switch (mode) {
+        case OUT_STORE: return fb4 ? dmv_launch<4, OUT_STORE>(p, x, norm_w, eps, y, nwg, tpw, lds, s)
+                                   : dmv_launch<8, OUT_STORE>(p, x, norm_w, eps, y, nwg, tpw, lds, s);
+        case OUT_ADD: return fb4 ? dmv_launch<4, OUT_ADD>(p, x, norm_w, eps, y, nwg, tpw, lds, s)
+                                 : dmv_launch<8, OUT_ADD>(p, x, norm_w, eps, y, nwg, tpw, lds, s);
+        default: return fb4 ? dmv_launch<4, OUT_GATED>(p, x, norm_w, eps, y, nwg, tpw, lds, s)
+                            : dmv_launch<8, OUT_GATED>(p, x, norm_w, eps, y, nwg, tpw, lds, s);
+    }
+}
+
+}  // namespace mlxr

@@ -1,0 +1,260 @@
+// Matvec building blocks over the repacked weight tiles (DPack), shared by the persistent decode
+// step (decode.hip) and the standalone per-projection matvec (dmv.hip).
+#pragma once
+#include "decode.h"
+
+namespace mlxr {
+
+constexpr int MK_THREADS = 512;
+constexpr int MK_WAVES = MK_THREADS / 64;
+constexpr int MK_TPW = 64;           // 16-row tiles of one workgroup in a matvec phase (max)
+
+// ------------------------------------------------------------------------------- matvec phase
+// Weights of the persistent step are a repacked copy (DPack, built once at load by dpack_kernel).
+// A matrix is cut into tiles of 16 rows; a tile is a sequence of scale groups, each covering 16
+// quantization groups (FB = gs / 8 code blocks of 128 codes) and stored as FB + 1 blocks of 1 KB
+// (one 16-byte slice per lane):
+//   block 0      (scale | bias << 16) of rows 4 (l >> 4) + i (i = slot dword), group 16 f + (l & 15):
+//                the accumulator layout of v_mfma_f32_16x16x32_f16;
+//   blocks 1..FB code block k: row 16 t + (l & 15), code dwords 16 kb + 4 j + (l >> 4) (j = slot
+//                dword, one per MFMA), kb = FB f + k - 1: the A-operand layout.
+// Gated phases put gate rows 8t..8t+7 in tile rows 0-7 and the matching up rows in rows 8-15.
+// A wave streams whole scale groups, so its loads walk one contiguous range and every ring slot
+// has a fixed role (slot 0: scales, slot k: code block k - 1).
+//
+// MFMA formulation: a nibble masked into the mantissa of the f16 1024.0 is the half 1024 + q (the
+// nibble at bits 4..7 gives 1024 + 16 q, met by x / 16 in the operand), so A is built with one
+// AND-OR per two codes. B is the chunk's x (f16) in the column of the chunk's group and zero in the
+// other 15, so the accumulator holds per-(row, group) sums sum (1024 + q) x = 1024 X'_g + sum q x
+// for 16 groups at once; the scale and bias are applied once per scale group:
+//   y_row += s_rg (D_rg - Cs_g) + b_rg Xs_g,   Cs_g = 1024 * sum of the group's stored halves.
+// Products of halves are exact and accumulate in fp32.
+typedef MvPhaseDesc MvPhase;
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+// Global-address-space pointers: loads through them are global (not flat) loads, which count on
+// the memory counter only; a flat load also counts on the LDS counter, so every wait for an LDS
+// read would wait for it too.
+typedef const __attribute__((address_space(1))) uint8_t* gptr8;
+typedef const __attribute__((address_space(1))) u32x4_t* gptr128;
+// 16-byte streaming load (data read once: the nontemporal hint keeps it from displacing activations)
+__device__ __forceinline__ uint4 ld_stream16(gptr8 p) {
+    const u32x4_t v = __builtin_nontemporal_load((gptr128)p);
+    return uint4{v.x, v.y, v.z, v.w};
+}
+
+// One scale group in flight per lane (FB + 1 slices of 16 bytes), kept exactly as loaded: no
+// instruction touches a slot before it is consumed, so the memory-counter wait for a slot never
+// drains the loads after it.
+template <int FB>
+struct Ring { uint4 u[FB + 1]; };
+
+// Geometry of a phase for this workgroup / wave.
+template <int FB>
+struct MvGeom {
+    int KBT, NF;            // code blocks and scale groups per tile
+    int t0, nt;             // this workgroup's tiles [t0, t0 + nt)
+    int f0, f1;             // this wave's scale groups [f0, f1) in the workgroup's tile-major order
+};
+template <int FB>
+__device__ __forceinline__ MvGeom<FB> mv_geom(const MvPhase& p, int wg, int nwg, int wave) {
+    MvGeom<FB> g;
+    g.KBT = p.K >> 7; g.NF = (g.KBT + FB - 1) / FB;
+    g.t0 = (int)((int64_t)p.tiles * wg / nwg);
+    g.nt = (int)((int64_t)p.tiles * (wg + 1) / nwg) - g.t0;
+    const int nfw = g.nt * g.NF;
+    g.f0 = nfw * wave / MK_WAVES; g.f1 = nfw * (wave + 1) / MK_WAVES;
+    return g;
+}
+// This lane's slice of the wave's first scale group.
+template <int FB>
+__device__ __forceinline__ gptr8 mv_base(const MvPhase& p, const MvGeom<FB>& g, int lane) {
+    return (gptr8)p.code + ((int64_t)g.t0 * g.NF + g.f0) * ((FB + 1) * 1024) + lane * 16;
+}
+
+template <int FB>
+__device__ __forceinline__ void mv_prefetch(const MvPhase p, int wg, int nwg, int wave, int lane, Ring<FB>& ring) {
+    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, wave);
+    if (g.f1 <= g.f0) {   // every path defines the ring, so no earlier value stays live across phases
+#pragma unroll
+        for (int d = 0; d <= FB; d++) ring.u[d] = uint4{0u, 0u, 0u, 0u};
+        return;
+    }
+    const gptr8 b = mv_base<FB>(p, g, lane);
+#pragma unroll
+    for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
+}
+
+// Constants of the A-operand build, made opaque to constant folding (ORed with a per-lane register
+// that is 0 at run time) so that (w & m) | c becomes one v_and_or_b32 with the constants in registers rather
+// than an AND and an OR with literals. No inline assembly here: the compiler must see every VGPR
+// write that feeds an MFMA operand to insert the wait states the matrix core requires.
+struct DotConsts { uint32_t m_lo, m_hi, magic; };   // magic: two halves of 1024.0
+__device__ __forceinline__ DotConsts dot_consts(int zero) {
+    const uint32_t z = (uint32_t)zero;
+    return DotConsts{0x000F000Fu | z, 0x00F000F0u | z, 0x64006400u | z};
+}
+// A operand of one code dword: halves (n0, n4, 16 n1, 16 n5, n2, n6, 16 n3, 16 n7) + 1024.
+__device__ __forceinline__ f16x8_t a_operand(uint32_t w, const DotConsts& k) {
+    const uint32_t w8 = w >> 8;
+    const u32x4_t v = {(w & k.m_lo) | k.magic, (w & k.m_hi) | k.magic, (w8 & k.m_lo) | k.magic, (w8 & k.m_hi) | k.magic};
+    return __builtin_bit_cast(f16x8_t, v);
+}
+
+// LDS layout of the matvec input (f16): chunk c of 32 values at xh + 20 * c (80 bytes), code dword i
+// of the chunk (codes 8i..8i+7, nibble j at bits 4j) matched by the 16-byte slot i holding
+//   (x0, x4), (x1 / 16, x5 / 16), (x2, x6), (x3 / 16, x7 / 16)      (x of codes 8i..8i+7)
+// after a power-of-two scaling of the whole vector; then the chunk's (Cs, Xs) at byte 64. gsum[g]
+// holds (Cs, Xs) of quantization group g; zero16 is 16 bytes of zeros (the masked B operand).
+constexpr int XH_STRIDE = 20;          // floats per chunk
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+// Packs x[0..K) (f32, read through the loader; every value already final, max |x| reduced by the
+// caller into gmax) into the f16 layout above and the group sums for group size 2^gsh. Scale 2^e
+// maps max |x| below 2^14, so every stored half is finite and (for all but values 2^28 below the
+// maximum) normal. Returns 2^-e.
+// LDS of a matvec phase (the attention phase reuses the same memory, so every phase rebuilds it).
+struct MvLds { float* xf; float* xh; float* gsum; float* zero16; float* hown; float* part; };
+
+// LD(t, lo, hi) yields values 8t..8t+7 of x.
+template <typename LD>
+__device__ __forceinline__ float pack_x16_from(const LD& ld, int K, float gmax, const MvLds& L, int gsh) {
+    float* xh = L.xh; float* gsum = L.gsum;
+    if (threadIdx.x < 4) L.zero16[threadIdx.x] = 0.0f;
+    int ex = 0;
+    if (gmax > 0.0f && gmax <= 3.0e38f) frexpf(gmax, &ex);
+    const int e = min(max(14 - ex, -100), 100);
+    const float up = ldexpf(1.0f, e);
+    for (int t = threadIdx.x; t < (K >> 3); t += MK_THREADS) {   // t: 8 values; 4 consecutive t per chunk
+        float4 lo, hi;
+        ld(t, lo, hi);
+        const _Float16 h0 = (_Float16)(lo.x * up), h4 = (_Float16)(hi.x * up);
+        const _Float16 h1 = (_Float16)(lo.y * up * 0.0625f), h5 = (_Float16)(hi.y * up * 0.0625f);
+        const _Float16 h2 = (_Float16)(lo.z * up), h6 = (_Float16)(hi.z * up);
+        const _Float16 h3 = (_Float16)(lo.w * up * 0.0625f), h7 = (_Float16)(hi.w * up * 0.0625f);
+        uint4 o;
+        o.x = __builtin_bit_cast(uint32_t, h2_t{h0, h4});
+        o.y = __builtin_bit_cast(uint32_t, h2_t{h1, h5});
+        o.z = __builtin_bit_cast(uint32_t, h2_t{h2, h6});
+        o.w = __builtin_bit_cast(uint32_t, h2_t{h3, h7});
+        const int c = t >> 2;
+        *reinterpret_cast<uint4*>(xh + c * XH_STRIDE + (t & 3) * 4) = o;
+        const float ev = (float)h0 + (float)h4 + (float)h2 + (float)h6;
+        const float od = (float)h1 + (float)h5 + (float)h3 + (float)h7;
+        float cs = ev + od, xsum = ev + 16.0f * od;
+        cs += __shfl_xor(cs, 1, 64); cs += __shfl_xor(cs, 2, 64);
+        xsum += __shfl_xor(xsum, 1, 64); xsum += __shfl_xor(xsum, 2, 64);
+        if ((t & 3) == 0) *reinterpret_cast<float2*>(xh + c * XH_STRIDE + 16) = float2{1024.0f * cs, xsum};
+    }
+    __syncthreads();
+    const int cpg = 1 << (gsh - 5);   // chunks per group
+    for (int g = threadIdx.x; g < (K >> gsh); g += MK_THREADS) {
+        float2 s = {0.0f, 0.0f};
+        for (int c = g * cpg; c < (g + 1) * cpg; c++) {
+            const float2 v = *reinterpret_cast<const float2*>(xh + c * XH_STRIDE + 16);
+            s.x += v.x; s.y += v.y;
+        }
+        *reinterpret_cast<float2*>(gsum + 2 * g) = s;
+    }
+    __syncthreads();
+    return 1.0f / up;
+}
+__device__ __forceinline__ float pack_x16(const float* xf, int K, float gmax, const MvLds& L, int gsh) {
+    auto ld = [xf](int t, float4& lo, float4& hi) {
+        lo = *reinterpret_cast<const float4*>(xf + 8 * t);
+        hi = *reinterpret_cast<const float4*>(xf + 8 * t + 4);
+    };
+    return pack_x16_from(ld, K, gmax, L, gsh);
+}
+
+
+// Streams the wave's scale groups (the first already in the ring), leaving per-tile partial row
+// sums in part[(tile * MK_WAVES + wave) * 16 + row] (LDS) for mv_finish.
+template <int FB>
+__device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const float* gsum, const float* zero16, int wg, int nwg,
+                                       int wave, int lane, Ring<FB>& ring, float* part) {
+    constexpr int GSH = FB == 4 ? 5 : 6;          // log2 of the group size
+    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, wave);
+    const int nfb = g.f1 - g.f0;
+    if (nfb <= 0) return;
+    const int gpr = p.K >> GSH;                   // groups per row
+    const gptr8 base = mv_base<FB>(p, g, lane);
+    const DotConsts kc = dot_consts(__float_as_int(zero16[lane & 3]));   // a zero the compiler cannot fold
+    const int col = lane & 15;
+    f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f};
+    int tile = g.f0 / g.NF, f = g.f0 - tile * g.NF;   // scale group within the tile
+    for (int i = 0; i < nfb; i++) {
+        const gptr8 nxt = base + (int64_t)min(i + 1, nfb - 1) * ((FB + 1) * 1024);   // the last reloads itself
+        const uint4 sbr = ring.u[0];
+        ring.u[0] = ld_stream16(nxt);
+        const float* xb = xh + (lane >> 4) * 4 + f * (4 * FB) * XH_STRIDE;   // this lane's slot of the group's first chunk
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < FB; k++) {
+            const uint4 unit = ring.u[k + 1];
+            const uint32_t wd[4] = {unit.x, unit.y, unit.z, unit.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                constexpr int CPG = 1 << (GSH - 5);                       // chunks per group
+                const int gcol = (4 * k + j) / CPG;                        // the chunk's group column
+                const float* bp = col == gcol ? xb + (4 * k + j) * XH_STRIDE : zero16;
+                const f16x8_t b = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(bp));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b, acc, 0, 0, 0);
+            }
+            ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
+        }
+        // scales of the 16 groups (groups past the row's last are zero-scaled; their sums may be junk)
+        const int gi = 16 * f + col;
+        const bool real = gi < gpr;
+        const float2 gs2 = *reinterpret_cast<const float2*>(gsum + 2 * (real ? gi : 0));
+        const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float sc = __uint_as_float(sv[r] << 16), bb = __uint_as_float(sv[r] & 0xffff0000u);
+            const float t = sc * (acc[r] - gs2.x) + bb * gs2.y;
+            run[r] += real ? t : 0.0f;
+        }
+        if (f == g.NF - 1 || i == nfb - 1) {     // tile done (or the wave's range): row sums to LDS
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float v = row16_sum(run[r]);
+                if (col == 0) part[(tile * MK_WAVES + wave) * 16 + 4 * (lane >> 4) + r] = v;
+            }
+            run = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (++f == g.NF) { f = 0; tile++; }
+    }
+}
+
+enum MvOut { OUT_STORE = 0, OUT_ADD = 1, OUT_GATED = 2, OUT_ARGMAX = 3 };
+
+struct MvResult { float best; int best_idx; };
+
+// Branch-free (part, row) of a concatenated row (bias lookup).
+__device__ __forceinline__ void mv_locate(const MvPhase& p, int vr, int& part, int& row) {
+    const int a = vr >= p.o1 ? 1 : 0, b = vr >= p.o1 + p.o2 ? 1 : 0;
+    part = a + b; row = vr - (a ? p.o1 : 0) - (b ? p.o2 : 0);
+}
+__device__ __forceinline__ float row_bias(const MvPhase& p, int vr) {
+    if (!p.bias[0]) return 0.0f;
+    int part, row; mv_locate(p, vr, part, row);
+    const uint16_t* b = part == 0 ? p.bias[0] : part == 1 ? p.bias[1] : p.bias[2];
+    return bf16_to_f32(b[row]);
+}
+
+// Row r of tile tl of this workgroup: the partial sums of the waves whose ranges meet the tile, in
+// wave order.
+__device__ __forceinline__ float tile_row(const float* part, int tl, int r, int nfw, int NF) {
+    float s = 0.0f;
+    for (int w = 0; w < MK_WAVES; w++) {
+        const int a = nfw * w / MK_WAVES, b = nfw * (w + 1) / MK_WAVES;
+        if (a < b && a < (tl + 1) * NF && b > tl * NF) s += part[(tl * MK_WAVES + w) * 16 + r];   // non-empty, meets the tile
+    }
+    return s;
+}
+
+
+}  // namespace mlxr

@@ -192,6 +192,72 @@ def test_qgemm_tiles_gated(gpu, gs):
         assert max_rel_err(got, ref) < TOL, T
 
 
+def qmv_tiles(mlxr, fxs, x, mode=0, norm_w=None, eps=1e-6, y0=None):
+    qm = (mlxr.QMat * len(fxs))(*[f.device(mlxr) for f in fxs])
+    O = fxs[0].O if mode == 2 else sum(f.O for f in fxs)
+    dx = mlxr.DeviceArray.from_numpy(np.asarray(x, np.float32))
+    dy = mlxr.DeviceArray.from_numpy(np.full(O, np.nan, np.float32) if y0 is None else np.asarray(y0, np.float32))
+    dn = mlxr.DeviceArray.from_numpy(np.asarray(norm_w, np.float32)) if norm_w is not None else None
+    mlxr.check(mlxr.lib.mlxr_k_qmv_tiles(qm, len(fxs), fxs[0].K, fxs[0].gs, mode, dx.ptr, dn.ptr if dn else None, eps,
+                                         dy.ptr, 1))
+    mlxr.synchronize()
+    return dy.numpy()
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_qmv_tiles_epilogues(gpu, gs):
+    """The kernel-per-op decode projection over the repacked tiles (qmv with its fused RMSNorm input,
+    accumulate and SiLU-gated epilogues; Kernels.swift:60-113, 2004-2013) against the oracle's
+    fp64 product: fused q|k|v parts with bias and ragged row counts, K from one scale group to the
+    32B MLP's 27648, and an input of large magnitude (the power-of-two scaling).
+    Declared precision (the prefill GEMM's tests treat their f16 operands the same way): x is
+    rounded to f16 after a power-of-two scaling, the codes, scales and biases enter exactly and
+    products accumulate in fp32. The fp32 sums carry (1024 + q) x terms (the code's offset is
+    removed once per group), so their slack is a small multiple of 2^-24 * 1024 sum_k |s_k x_k|
+    (s_k: the scale of k's group); 2^-20 of it is allowed. Checked: |got - matmul_x16| (the
+    oracle's fp64 product of the rounded x) within that slack, and |got - exact| <= 2^-11
+    sum_k |w_k x_k| + slack."""
+    rng = np.random.default_rng(gs)
+
+    def check(got, ref, fxs, x, K):
+        x64 = np.abs(x.astype(np.float64))
+        ref16 = np.concatenate([f.oracle(oracle).matmul_x16(x)[0] for f in fxs])
+        srep = np.concatenate([np.repeat(np.abs(f.scales.astype(np.float64)), f.gs, axis=1) for f in fxs])
+        slack = 2.0 ** -20 * 1024 * (srep @ x64) + 1e-6 * (1 + np.abs(ref))
+        assert np.all(np.abs(got - ref16) <= slack), K
+        dense = np.concatenate([f.dense() for f in fxs]).astype(np.float64)
+        assert np.all(np.abs(got - ref) <= 2.0 ** -11 * (np.abs(dense) @ x64) + slack), K
+
+    for K, Os in ((128, (40,)), (1024, (264, 40, 88)), (5120, (72,)), (27648, (24,))):
+        fxs = [QuantFixture(O, K, 4, gs, seed=O + K, with_bias=len(Os) > 1, fast=True) for O in Os]
+        h = rng.normal(0, 1, K).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, K).astype(np.float32)
+        xn = oracle.rms_norm(h[None], w, 1e-6)[0]
+        ref = np.concatenate([f.oracle(oracle).matmul_f64(xn)[0] for f in fxs])
+        check(qmv_tiles(gpu, fxs, h, norm_w=w), ref, fxs, xn, K)
+        big = (h * 3e4).astype(np.float32)
+        ref_big = np.concatenate([f.oracle(oracle).matmul_f64(big)[0] for f in fxs])
+        check(qmv_tiles(gpu, fxs, big), ref_big, fxs, big, K)
+        y0 = rng.normal(0, 1, ref.size).astype(np.float32)
+        check(qmv_tiles(gpu, fxs, xn, mode=1, y0=y0) - y0, ref, fxs, xn, K)
+    K, I = 2048, 200
+    g, u = (QuantFixture(I, K, 4, gs, seed=s, fast=True) for s in (5, 6))
+    h = rng.normal(0, 1, K).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    xn = oracle.rms_norm(h[None], w, 1e-6)[0]
+    gr, ur = g.oracle(oracle).matmul_x16(xn)[0], u.oracle(oracle).matmul_x16(xn)[0]
+    gated16 = np.array([oracle.lib.orc_silu_mul(float(a), float(b)) for a, b in zip(gr, ur)], np.float32)
+    got = qmv_tiles(gpu, [g, u], h, mode=2, norm_w=w)
+    # each part's slack (as above) carried through silu(g) * u: |d silu / dg| <= 1.1
+    x64 = np.abs(xn.astype(np.float64))
+    sl = [2.0 ** -20 * 1024 * (np.repeat(np.abs(f.scales.astype(np.float64)), gs, axis=1) @ x64) for f in (g, u)]
+    silu = gr / (1.0 + np.exp(-gr.astype(np.float64)))
+    bound = 1.1 * np.abs(ur) * sl[0] + np.abs(silu) * sl[1] + 1e-6 * (1 + np.abs(gated16))
+    assert np.all(np.abs(got - gated16) <= bound)
+    zero = qmv_tiles(gpu, [g, u], np.zeros(K, np.float32), mode=2)
+    assert np.all(zero == 0.0)
+
+
 def test_qgemm_batch_invariant(gpu):
     """prefillTilesAgreeBitwise (KernelTests.swift:168-184): a token's output does not depend on T."""
     O, K = 2050, 1024
