@@ -58,7 +58,8 @@ struct MegaArgs {
     float eps, scale;
     const int* pt;
     int* hist; int* status; int* dpos;
-    float *logits, *part;
+    float *logits, *part;             // attention partials: max [nH * nsplit], sum [..], acc [..][128]
+    uint2* part_ready;                // per (KV head, range): tagged once the range's partials are stored
     // Tagged exchange vectors: element i is (value bits, tag) written by one 8-byte store; a reader
     // polls until the tag of the phase that produces it appears (no grid barrier between phases).
     // hA: h after down (and the embedding), hB: h after o_proj; q|k|v; attention output; SiLU(g)*u.

@@ -34,6 +34,7 @@ namespace mlxr {
 
 constexpr int MK_MAXG = 8;
 constexpr int MK_HOWN = 1024;        // residual rows of one workgroup in an accumulate phase (max)
+constexpr int MK_MERGE_B = 32;       // partials one merging thread has in flight
 
 // ------------------------------------------------------------------------------- coherence
 // Data one workgroup writes and another reads within the launch (h, q|k|v, attention partials and
@@ -180,12 +181,25 @@ __device__ __forceinline__ float2 fetch_to_lds(const uint2* src, int K, unsigned
             const int i2 = min(base + j * MK_THREADS + (int)threadIdx.x, K2 - 1);
             v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, i2 * 16, 0, 16);
         }
+        // poll the batch: every round reissues all loads still missing their tag together
+        for (unsigned spins = 0;;) {
+            bool ready = true;
+#pragma unroll
+            for (int j = 0; j < MK_LDB; j++) {
+                const int i2 = base + j * MK_THREADS + (int)threadIdx.x;
+                ready &= i2 >= K2 || (v[j].y == tag && v[j].w == tag);
+            }
+            if (ready || !tag_spin(tw, spins)) break;
+#pragma unroll
+            for (int j = 0; j < MK_LDB; j++) {
+                const int i2 = base + j * MK_THREADS + (int)threadIdx.x;
+                if (i2 < K2 && (v[j].y != tag || v[j].w != tag)) v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, i2 * 16, 0, 16);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < MK_LDB; j++) {
             const int i2 = base + j * MK_THREADS + (int)threadIdx.x;
             if (i2 < K2) {
-                unsigned spins = 0;
-                while ((v[j].y != tag || v[j].w != tag) && tag_spin(tw, spins)) v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, i2 * 16, 0, 16);
                 const float x0 = __uint_as_float(v[j].x), x1 = __uint_as_float(v[j].z);
                 *reinterpret_cast<float2*>(xf + i2 * 2) = float2{x0, x1};
                 ss += x0 * x0 + x1 * x1;
@@ -402,7 +416,6 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
         const int nk = n1 - n0;
         const int prow = (kvh * G) * nsplit;             // partial rows: (head, split)
-        float* pm = a.part; float* pl = a.part + nH * nsplit; float* pa = a.part + 2 * nH * nsplit;
         uint16_t* qb = reinterpret_cast<uint16_t*>(lds); // [2][16][128] bf16: q hi / lo
         uint16_t* kn16 = qb + 2 * 16 * 128;              // new key, bf16 [128]
         uint16_t* vn16 = kn16 + 128;                     // new value, bf16 [128]
@@ -558,6 +571,10 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 }
             }
             __syncthreads();
+            // partials: plain agent-scope stores, then (once they are complete) this range's ready tag
+            const unsigned atag = tag_of(3 + 5 * li);
+            const int P = nH * nsplit;
+            float* pm = a.part; float* pl = a.part + P; float* pa = a.part + 2 * P;
             for (int idx = tid; idx < G * 128; idx += MK_THREADS) {
                 const int g = idx >> 7, d = idx & 127;
                 float v = 0.0f;
@@ -566,51 +583,49 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 st_ag(pa + (int64_t)r * 128 + d, nk > 0 ? v : 0.0f);
                 if (d == 0) { st_ag(pm + r, nk > 0 ? mls[g] : -1e30f); st_ag(pl + r, nk > 0 ? mls[16 + g] : 0.0f); }
             }
-            prof_mark(a.prof, 512 + 8 * li + 3);
-            // the last range of this KV head to finish merges the partials in range order
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (tid == 0) {
-                const unsigned done = add_ag(&a.kv_done[kvh * 32], 1u);
-                flag = done == (unsigned)nsplit - 1;
-                if (flag) __hip_atomic_store(&a.kv_done[kvh * 32], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __syncthreads();
-            if (flag) {
-                // merge: weights f_s = exp(m_s - M) and 1 / sum_s l_s f_s per head (m, l staged in LDS),
-                // then every (head, dim) sums its nsplit partials, loaded 32 at a time
-                const int P = nH * nsplit;
-                float* wts = wacc;                                  // [G][nsplit] weights
+            if (tid == 0) st_tag(a.part_ready + kvh * nsplit + split, 0.0f, atag);
+            prof_mark(a.prof, 512 + 8 * li + 3);
+            if (split == nsplit - 1) {
+                // the last range (the fewest keys) merges the KV head's partials in range order once
+                // every range's ready tag is up: all loads of the merge in one round trip, the weights
+                // exp(m_s - M) computed by every (head, dim) thread from the staged maxima
+                if (tid < nsplit) ld_tag1(a.part_ready, kvh * nsplit + tid, nKV * nsplit, atag, tw);
+                __syncthreads();
+                float* wts = wacc;                                  // [G][nsplit] maxima
                 float* lsv = wacc + MK_MAXG * 64;                   // [G][nsplit] sums
                 for (int idx = tid; idx < G * nsplit; idx += MK_THREADS) {
                     wts[idx] = ld_coh1(pm, prow + idx, P);
                     lsv[idx] = ld_coh1(pl, prow + idx, P);
                 }
-                __syncthreads();
-                if (tid < G) {
-                    float M = -1e30f;
-                    for (int s = 0; s < nsplit; s++) M = fmaxf(M, wts[tid * nsplit + s]);
-                    float Ls = 0.0f;
-                    for (int s = 0; s < nsplit; s++) {
-                        const float f = expf(wts[tid * nsplit + s] - M);
-                        wts[tid * nsplit + s] = f;
-                        Ls += lsv[tid * nsplit + s] * f;
-                    }
-                    mrow[tid] = 1.0f / Ls;
-                }
-                __syncthreads();
-                for (int idx = tid; idx < G * 128; idx += MK_THREADS) {
-                    const int g = idx >> 7, d = idx & 127;
+                for (int idx0 = 0; idx0 < G * 128; idx0 += MK_THREADS) {
+                    const int idx = idx0 + tid;
+                    const int g = min(idx >> 7, G - 1), d = idx & 127;
                     const int rb = prow + g * nsplit;
-                    float o = 0.0f;
-                    for (int s0 = 0; s0 < nsplit; s0 += 32) {
-                        float v[32];
+                    float v[MK_MERGE_B];
 #pragma unroll
-                        for (int q = 0; q < 32; q++) v[q] = ld_coh1(pa, (rb + min(s0 + q, nsplit - 1)) * 128 + d, P * 128);
+                    for (int q = 0; q < MK_MERGE_B; q++) v[q] = ld_coh1(pa, (rb + min(q, nsplit - 1)) * 128 + d, P * 128);
+                    __syncthreads();                                // the maxima and sums are staged
+                    float M = -1e30f;
+                    for (int s = 0; s < nsplit; s++) M = fmaxf(M, wts[g * nsplit + s]);
+                    float o = 0.0f, Ls = 0.0f;
+                    for (int s0 = 0; s0 < nsplit; s0 += MK_MERGE_B) {
+                        if (s0 > 0) {
 #pragma unroll
-                        for (int q = 0; q < 32; q++) if (s0 + q < nsplit) o += v[q] * wts[g * nsplit + s0 + q];
+                            for (int q = 0; q < MK_MERGE_B; q++) v[q] = ld_coh1(pa, (rb + min(s0 + q, nsplit - 1)) * 128 + d, P * 128);
+                        }
+#pragma unroll
+                        for (int q = 0; q < MK_MERGE_B; q++) {
+                            const int s = s0 + q;
+                            if (s < nsplit) {
+                                const float f = expf(wts[g * nsplit + s] - M);
+                                o += v[q] * f;
+                                Ls += lsv[g * nsplit + s] * f;
+                            }
+                        }
                     }
-                    st_tag(a.attnT + (kvh * G + g) * 128 + d, o * mrow[g], tag_of(3 + 5 * li));
+                    if (idx < G * 128) st_tag(a.attnT + (kvh * G + g) * 128 + d, o * (1.0f / Ls), atag);
                 }
             }
         }

@@ -427,10 +427,12 @@ static int mega_setup(Model* m) {
         HIPCHECK(hipMemset(a.attnT, 0, sizeof(uint2) * c.nH * c.D));
         HIPCHECK(hipMemset(a.mlpT, 0, sizeof(uint2) * c.I));
     }
-    if ((rc = dalloc(m, &a.part, (size_t)c.nH * nsplit * (c.D + 2))) || (rc = dalloc(m, &a.wg_best, nwg)) ||
+    if ((rc = dalloc(m, &a.part, (size_t)c.nH * nsplit * (c.D + 2))) || (rc = dalloc(m, &a.part_ready, (size_t)c.nKV * nsplit)) ||
+        (rc = dalloc(m, &a.wg_best, nwg)) ||
         (rc = dalloc(m, &a.wg_idx, nwg)) || (rc = dalloc(m, &a.kv_done, 64 * 32)) || (rc = dalloc(m, &a.head_done, 64)) ||
         (rc = dalloc(m, &a.sync, 1)))
         return rc;
+    HIPCHECK(hipMemset(a.part_ready, 0, sizeof(uint2) * c.nKV * nsplit));
     HIPCHECK(hipMemset(a.kv_done, 0, 64 * 32 * 4));
     HIPCHECK(hipMemset(a.head_done, 0, 64 * 4));
     HIPCHECK(hipMemset(a.sync, 0, sizeof(MegaSync)));
