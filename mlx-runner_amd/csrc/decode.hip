@@ -496,7 +496,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     sv[r] = ok ? sacc[r] : -INFINITY;
                     mloc = fmaxf(mloc, sv[r]);
                 }
-                mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64)); mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+                mloc = xor32_max(xor16_max(mloc));
                 if (lane < 16) wred[lane * MK_WAVES + wave] = mloc;
                 __syncthreads();
                 // new running max per head; probabilities of this lane's keys
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     lsum += p;
                     if (hh < MAXG) pp[hh * 128 + 16 * wave + 4 * (lane >> 4) + r] = hh < G ? p : 0.0f;
                 }
-                lsum += __shfl_xor(lsum, 16, 64); lsum += __shfl_xor(lsum, 32, 64);
+                lsum = xor32_sum(xor16_sum(lsum));
                 if (lane < 16) wred[MK_WAVES * 16 + lane * MK_WAVES + wave] = lsum;
                 float alpha[MAXG];
 #pragma unroll
@@ -524,8 +524,12 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 __syncthreads();
                 // running sums (one thread per head), then P.V with the rescaled accumulators
                 if (tid < G) {
-                    float mn = mls[tid], ls = 0.0f;
-                    for (int w = 0; w < MK_WAVES; w++) { mn = fmaxf(mn, wred[tid * MK_WAVES + w]); ls += wred[MK_WAVES * 16 + tid * MK_WAVES + w]; }
+                    const float4 ma = *reinterpret_cast<const float4*>(wred + tid * MK_WAVES);
+                    const float4 mb = *reinterpret_cast<const float4*>(wred + tid * MK_WAVES + 4);
+                    const float4 la = *reinterpret_cast<const float4*>(wred + MK_WAVES * 16 + tid * MK_WAVES);
+                    const float4 lb = *reinterpret_cast<const float4*>(wred + MK_WAVES * 16 + tid * MK_WAVES + 4);
+                    const float mn = fmaxf(mls[tid], fmaxf(fmaxf(fmaxf(ma.x, ma.y), fmaxf(ma.z, ma.w)), fmaxf(fmaxf(mb.x, mb.y), fmaxf(mb.z, mb.w))));
+                    const float ls = ((((((la.x + la.y) + la.z) + la.w) + lb.x) + lb.y) + lb.z) + lb.w;
                     mls[16 + tid] = mls[16 + tid] * alpha[tid] + ls;
                     mls[tid] = mn;
                 }
@@ -564,8 +568,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 if (g < G) {
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        float v = acc[g][e];
-                        v += __shfl_xor(v, 32, 64);
+                        const float v = xor32_sum(acc[g][e]);
                         if (lane < 32) wacc[(wave * MAXG + g) * 128 + lane * 4 + e] = v;
                     }
                 }
