@@ -69,6 +69,7 @@ struct MegaArgs {
     MegaSync* sync;
     int* abort_host;                  // host-mapped copy of sync->abort (read by the host after a step)
     int select;                       // 1: greedy token selection fused (writes hist / ring, advances *dpos)
+    int kv_stage;                     // 1: a range's second chunk of keys is staged in LDS (cache byte offsets < 2^31)
     int* ring_tok; int* ring_status; int ring_mask;
     unsigned long long* prof;         // optional: per workgroup, wall-clock at every phase start / end
 };

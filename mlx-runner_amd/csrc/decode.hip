@@ -269,6 +269,10 @@ __device__ __forceinline__ void att_range(int L, int nsplit, int split, int& n0,
 // Loads chunk c of keys [n0, nf) (nf: the first key not yet final in the cache; keys past it are
 // clamped to a final row and replaced or masked by the caller).
 // Every path defines the registers, so no earlier value stays live across phases.
+__device__ __forceinline__ void att_load_k(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
+                                           KVPrefetch& pf);
+__device__ __forceinline__ void att_load_v(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
+                                           KVPrefetch& pf);
 __device__ __forceinline__ void att_prefetch_k(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int nf, int c, KVPrefetch& pf) {
     if (nf <= n0) {
 #pragma unroll
@@ -279,6 +283,12 @@ __device__ __forceinline__ void att_prefetch_k(const MegaArgs& a, const LayerDev
     const int kb = n0 + 128 * c + 16 * wave;            // the wave's 16 keys span at most two pages
     const int jf = min(kb, nf - 1), jl = min(kb + 15, nf - 1);
     const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = a.pt[pg0], e1 = a.pt[jl >> MLXR_PAGE_SHIFT];
+    att_load_k(a, ly, kvh, kb, nf, pg0, e0, e1, pf);
+}
+// K rows of the wave's 16 keys from kb, with the page entries of the first and last already loaded.
+__device__ __forceinline__ void att_load_k(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
+                                           KVPrefetch& pf) {
+    const int lane = threadIdx.x & 63;
     const int jk = min(kb + (lane & 15), nf - 1);
     const int64_t rk = ((int64_t)(((jk >> MLXR_PAGE_SHIFT) == pg0 ? e0 : e1) * a.nKV + kvh) * MLXR_PAGE + (jk & (MLXR_PAGE - 1))) * 128 +
                        8 * (lane >> 4);
@@ -295,6 +305,12 @@ __device__ __forceinline__ void att_prefetch_v(const MegaArgs& a, const LayerDev
     const int kb = n0 + 128 * c + 8 * (t >> 5);          // the thread's 8 keys span at most two pages
     const int jf = min(kb, nf - 1), jl = min(kb + 7, nf - 1);
     const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = a.pt[pg0], e1 = a.pt[jl >> MLXR_PAGE_SHIFT];
+    att_load_v(a, ly, kvh, kb, nf, pg0, e0, e1, pf);
+}
+// V slices of the thread's 8 keys from kb, with the page entries of the first and last already loaded.
+__device__ __forceinline__ void att_load_v(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
+                                           KVPrefetch& pf) {
+    const int t = threadIdx.x;
 #pragma unroll
     for (int r = 0; r < 8; r++) {
         const int jv = min(kb + r, nf - 1);
@@ -304,9 +320,47 @@ __device__ __forceinline__ void att_prefetch_v(const MegaArgs& a, const LayerDev
         pf.v[r] = uint2{(uint32_t)v, (uint32_t)(v >> 32)};
     }
 }
-__device__ __forceinline__ void att_prefetch(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int nf, int c, KVPrefetch& pf) {
-    att_prefetch_k(a, ly, kvh, n0, nf, c, pf);
-    att_prefetch_v(a, ly, kvh, n0, nf, c, pf);
+// Chunk 1 (keys n0 + 128 .. n0 + 255) of a range longer than 128 keys, copied by buffer->LDS DMA into
+// kvl right after the q|k|v matvec: K rows [128][256 B], then V rows. Keys at or past nf are clamped
+// to a final row (replaced or masked by the caller, as for the register chunks). Each wave moves its
+// 16 keys' K and V rows, 4 rows (1 KiB) per instruction. Byte offsets fit 32 bits (checked at setup).
+typedef __attribute__((address_space(3))) void* att_lptr;
+constexpr int ATT_KVL_OFF = 53248;     // byte offset of the staged chunk in the workgroup's LDS
+constexpr int ATT_KVL_BYTES = 65536;
+__device__ __forceinline__ void att_stage1(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
+                                           uint8_t* kvl) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(ly.kc, 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(ly.vc, 0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int j = min(kb + 4 * i + (lane >> 4), nf - 1);
+        const uint32_t off = (uint32_t)((((j >> MLXR_PAGE_SHIFT) == pg0 ? e0 : e1) * a.nKV + kvh) * MLXR_PAGE + (j & (MLXR_PAGE - 1))) * 256u +
+                             16u * (lane & 15);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (att_lptr)(kvl + (16 * wave + 4 * i) * 256), 16, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (att_lptr)(kvl + 32768 + (16 * wave + 4 * i) * 256), 16, off, 0, 0, 0);
+    }
+}
+// Start of the attention phase: chunk 0's K / V into registers and, for a staged range, chunk 1 into
+// LDS; every page entry these need is loaded first, together (one round trip before the data loads).
+__device__ __forceinline__ void att_begin(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int nf, bool staged, uint8_t* kvl,
+                                          KVPrefetch& pf) {
+    if (nf <= n0) {
+#pragma unroll
+        for (int db = 0; db < 4; db++) pf.k[db] = uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int r = 0; r < 8; r++) pf.v[r] = uint2{0u, 0u};
+        return;
+    }
+    const int t = threadIdx.x, wave = t >> 6;
+    const int kk = n0 + 16 * wave, kv = n0 + 8 * (t >> 5), ks = n0 + 128 + 16 * wave;
+    const int pk = min(kk, nf - 1) >> MLXR_PAGE_SHIFT, pv = min(kv, nf - 1) >> MLXR_PAGE_SHIFT, ps = min(ks, nf - 1) >> MLXR_PAGE_SHIFT;
+    const int ek0 = a.pt[pk], ek1 = a.pt[min(kk + 15, nf - 1) >> MLXR_PAGE_SHIFT];
+    const int ev0 = a.pt[pv], ev1 = a.pt[min(kv + 7, nf - 1) >> MLXR_PAGE_SHIFT];
+    const int es0 = a.pt[ps], es1 = a.pt[min(ks + 15, nf - 1) >> MLXR_PAGE_SHIFT];
+    att_load_k(a, ly, kvh, kk, nf, pk, ek0, ek1, pf);
+    att_load_v(a, ly, kvh, kv, nf, pv, ev0, ev1, pf);
+    if (staged) att_stage1(a, ly, kvh, ks, nf, ps, es0, es1, kvl);
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4 v, float* o) {
@@ -358,13 +412,15 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
     const int pos = *a.dpos, L = pos + 1;
     const int H = a.H, D = 128, nH = a.nH, nKV = a.nKV, G = nH / nKV;
     const int Kmax = std::max(H, std::max(a.I, nH * D));
+    // matvec LDS: what mv_finish reads (partials, residual rows) lies below ATT_KVL_OFF, so the
+    // attention phase's staging DMA may start as soon as a workgroup leaves the q|k|v matvec
     MvLds ml;
-    ml.xf = lds;                                  // matvec input, f32 staging (Kmax floats)
+    ml.part = lds;                                // per-tile partial row sums [MK_TPW][waves][16]
+    ml.hown = ml.part + MK_TPW * MK_WAVES * 16;   // this workgroup's residual rows (up to MK_HOWN)
+    ml.xf = ml.hown + MK_HOWN;                    // matvec input, f32 staging (Kmax floats)
     ml.xh = ml.xf + Kmax;                         // matvec input, f16 layout (Kmax / 32 chunks)
     ml.gsum = ml.xh + (Kmax >> 5) * XH_STRIDE;    // per-group sums (Kmax / 32 float2 at most)
     ml.zero16 = ml.gsum + (Kmax >> 5) * 2;        // 16 bytes of zeros
-    ml.hown = ml.zero16 + 4;                      // this workgroup's residual rows (up to MK_HOWN)
-    ml.part = ml.hown + MK_HOWN;                  // per-tile partial row sums [MK_TPW][waves][16]
     __shared__ int redi[MK_WAVES];
     Ring<FB> ring;
     KVPrefetch kvpf;
@@ -407,7 +463,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         const int item = wg;                       // nwg == nKV * nsplit
         const int kvh = item / nsplit, split = item % nsplit;
         int n0, n1; att_range(L, nsplit, split, n0, n1);
-        att_prefetch(a, ly, kvh, n0, min(n1, pos), 0, kvpf);
+        uint8_t* kvl = reinterpret_cast<uint8_t*>(lds) + ATT_KVL_OFF;
+        const bool staged = a.kv_stage && n1 - n0 > 128;   // chunk 1 joins chunk 0's pass from LDS
+        att_begin(a, ly, kvh, n0, min(n1, pos), staged, kvl, kvpf);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- B: attention for (kvh, split): scores on the matrix cores (K rows from the bf16 cache as
@@ -422,8 +480,8 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         float* buf = reinterpret_cast<float*>(vn16 + 128);   // 4 x 128 rope scratch
         float* wred = buf + 4 * 128;                     // [2][waves][16] per-wave max, sum
         float* mls = wred + 2 * MK_WAVES * 16;           // [2][16] running max, sum per head
-        float* pp = mls + 32;                            // [MAXG][128] chunk probabilities
-        float* wacc = pp + MAXG * 128;                   // [waves][MAXG][128] P.V partials; merge scratch
+        float* pp = mls + 32;                            // [MAXG][256] probabilities of the pass's keys
+        float* wacc = pp + MAXG * 256;                   // [waves][MAXG][128] P.V partials; merge scratch
         float* mrow = wacc + MK_WAVES * MAXG * 128;      // [MAXG] merge scale
         {
             const bool owns_new = pos >= n0 && pos < n1;
@@ -472,16 +530,19 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const int hh = lane & 15, d4 = tid & 31, slice = tid >> 5;
             const int nchunks = (nk + 127) >> 7;
             const int nf = min(n1, pos);
-            for (int c = 0; c < nchunks; c++) {
+            for (int c = 0; c < nchunks;) {
                 asm volatile("" ::: "memory");   // keeps the q reads in the loop (no registers held across chunks)
-                // scores S[key][head] of the wave's 16 keys
+                // a staged range takes chunks 0 and 1 in one pass (chunk 1 from LDS)
+                const bool pair = staged && c == 0;
+                const int cn = c + (pair ? 2 : 1);
+                // scores S[key][head] of the wave's 16 keys (and its 16 keys of chunk 1)
                 const int kbase = n0 + 128 * c + 16 * wave;
                 uint4* kq = kvpf.k;
                 if (owns_new && kbase + (lane & 15) == pos) {   // only the owner wrote kn16 / vn16
 #pragma unroll
                     for (int db = 0; db < 4; db++) kq[db] = *reinterpret_cast<const uint4*>(kn16 + 32 * db + 8 * (lane >> 4));
                 }
-                f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+                f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f}, sacc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int db = 0; db < 4; db++)
 #pragma unroll
@@ -489,12 +550,31 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                         const uint4 bq = *reinterpret_cast<const uint4*>(qb + hl * 2048 + hh * 128 + 32 * db + 8 * (lane >> 4));
                         sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kq[db]), __builtin_bit_cast(bf16x8_t, bq), sacc, 0, 0, 0);
                     }
-                float sv[4], mloc = -INFINITY;
+                if (pair) {
+                    __builtin_amdgcn_s_waitcnt(0x0070);    // this wave's DMA (vmcnt 0), then every wave's
+                    __builtin_amdgcn_s_barrier();
+                    const bool newk = owns_new && kbase + 128 + (lane & 15) == pos;
+#pragma unroll
+                    for (int db = 0; db < 4; db++) {
+                        const uint16_t* src = newk ? kn16 + 32 * db + 8 * (lane >> 4)
+                                                   : reinterpret_cast<const uint16_t*>(kvl + (16 * wave + (lane & 15)) * 256) + 32 * db + 8 * (lane >> 4);
+                        const uint4 k1 = *reinterpret_cast<const uint4*>(src);
+#pragma unroll
+                        for (int hl = 0; hl < 2; hl++) {
+                            const uint4 bq = *reinterpret_cast<const uint4*>(qb + hl * 2048 + hh * 128 + 32 * db + 8 * (lane >> 4));
+                            sacc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, k1), __builtin_bit_cast(bf16x8_t, bq), sacc1, 0, 0, 0);
+                        }
+                    }
+                }
+                float sv[4], sv1[4], mloc = -INFINITY;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const bool ok = kbase + 4 * (lane >> 4) + r < n1;
                     sv[r] = ok ? sacc[r] : -INFINITY;
                     mloc = fmaxf(mloc, sv[r]);
+                    const bool ok1 = pair && kbase + 128 + 4 * (lane >> 4) + r < n1;
+                    sv1[r] = ok1 ? sacc1[r] : -INFINITY;
+                    mloc = fmaxf(mloc, sv1[r]);
                 }
                 mloc = xor32_max(xor16_max(mloc));
                 if (lane < 16) wred[lane * MK_WAVES + wave] = mloc;
@@ -508,7 +588,15 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 for (int r = 0; r < 4; r++) {
                     const float p = expf(sv[r] - mnew_h);
                     lsum += p;
-                    if (hh < MAXG) pp[hh * 128 + 16 * wave + 4 * (lane >> 4) + r] = hh < G ? p : 0.0f;
+                    if (hh < MAXG) pp[hh * 256 + 16 * wave + 4 * (lane >> 4) + r] = hh < G ? p : 0.0f;
+                }
+                if (pair) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float p = expf(sv1[r] - mnew_h);
+                        lsum += p;
+                        if (hh < MAXG) pp[hh * 256 + 128 + 16 * wave + 4 * (lane >> 4) + r] = hh < G ? p : 0.0f;
+                    }
                 }
                 lsum = xor32_sum(xor16_sum(lsum));
                 if (lane < 16) wred[MK_WAVES * 16 + lane * MK_WAVES + wave] = lsum;
@@ -520,7 +608,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     const float mn = fmaxf(mls[g], fmaxf(fmaxf(fmaxf(ga.x, ga.y), fmaxf(ga.z, ga.w)), fmaxf(fmaxf(gb.x, gb.y), fmaxf(gb.z, gb.w))));
                     alpha[g] = expf(mls[g] - mn);
                 }
-                if (c + 1 < nchunks) att_prefetch_k(a, ly, kvh, n0, nf, c + 1, kvpf);   // while softmax and P.V run
+                if (cn < nchunks) att_prefetch_k(a, ly, kvh, n0, nf, cn, kvpf);   // while softmax and P.V run
                 __syncthreads();
                 // running sums (one thread per head), then P.V with the rescaled accumulators
                 if (tid < G) {
@@ -542,7 +630,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     // keys 8 slice + 4 half .. +4 of the chunk (probabilities of masked keys are 0)
                     float4 pr[MAXG];
 #pragma unroll
-                    for (int g = 0; g < MAXG; g++) pr[g] = *reinterpret_cast<const float4*>(pp + g * 128 + 8 * slice + 4 * half);
+                    for (int g = 0; g < MAXG; g++) pr[g] = *reinterpret_cast<const float4*>(pp + g * 256 + 8 * slice + 4 * half);
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         const int r = 4 * half + q, j = n0 + 128 * c + 8 * slice + r;
@@ -558,7 +646,31 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                         }
                     }
                 }
-                if (c + 1 < nchunks) att_prefetch_v(a, ly, kvh, n0, nf, c + 1, kvpf);
+                if (pair) {
+#pragma unroll
+                    for (int half = 0; half < 2; half++) {
+                        float4 pr[MAXG];
+#pragma unroll
+                        for (int g = 0; g < MAXG; g++) pr[g] = *reinterpret_cast<const float4*>(pp + g * 256 + 128 + 8 * slice + 4 * half);
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const int r = 4 * half + q, j = n0 + 128 + 8 * slice + r;
+                            const uint16_t* src = owns_new && j == pos ? vn16 + 4 * d4
+                                                                       : reinterpret_cast<const uint16_t*>(kvl + 32768 + (8 * slice + r) * 256) + 4 * d4;
+                            const uint2 vv = *reinterpret_cast<const uint2*>(src);
+                            const float vf[4] = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
+                                                 __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
+#pragma unroll
+                            for (int g = 0; g < MAXG; g++) {
+                                const float pg = q == 0 ? pr[g].x : q == 1 ? pr[g].y : q == 2 ? pr[g].z : pr[g].w;
+#pragma unroll
+                                for (int e = 0; e < 4; e++) acc[g][e] = fmaf(pg, vf[e], acc[g][e]);
+                            }
+                        }
+                    }
+                }
+                if (cn < nchunks) att_prefetch_v(a, ly, kvh, n0, nf, cn, kvpf);
+                c = cn;
             }
             prof_mark(a.prof, 512 + 8 * li + 1);
             prof_mark(a.prof, 512 + 8 * li + 2);
@@ -775,8 +887,10 @@ size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split) {
     const size_t kmax = (size_t)std::max(a.H, std::max(a.I, a.nH * 128));
     size_t mv = (kmax + kmax / 32 * (XH_STRIDE + 2) + 4 + MK_HOWN + MK_TPW * MK_WAVES * 16) * 4;
     // attention: q hi/lo image, new k/v, rope scratch, exchanges, probabilities, P.V partials, merge scale
-    size_t att = 2 * 16 * 128 * 2 + 2 * 128 * 2 + (size_t)(4 * 128 + 2 * MK_WAVES * 16 + 32 + MK_MAXG * 128 +
+    size_t att = 2 * 16 * 128 * 2 + 2 * 128 * 2 + (size_t)(4 * 128 + 2 * MK_WAVES * 16 + 32 + MK_MAXG * 256 +
                  MK_WAVES * MK_MAXG * 128 + MK_MAXG) * 4;
+    if (att > (size_t)ATT_KVL_OFF || (size_t)(MK_TPW * MK_WAVES * 16 + MK_HOWN) * 4 > (size_t)ATT_KVL_OFF) return (size_t)-1;
+    if (a.kv_stage) att = ATT_KVL_OFF + ATT_KVL_BYTES;   // the staged second chunk of keys
     (void)max_keys_per_split; (void)G;
     return std::max(mv, att);
 }

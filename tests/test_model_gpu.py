@@ -116,6 +116,26 @@ def test_persistent_decode_matches_kernel_per_op(gpu, models, name):
             assert abs(logits[a[i]] - logits[b[i]]) < LOGIT_TOL
 
 
+def test_persistent_decode_long_ranges(gpu, models):
+    """Key ranges longer than one and two 128-key chunks per workgroup (the tiny model's two KV
+    heads give 128 ranges each: ~156 keys at 20000 tokens, ~265 at 34000): the persistent step's
+    greedy tokens against the kernel-per-op step's; where they part, the two tokens' logits (full
+    prefill of the shared prefix) are within the 2e-2 gate."""
+    d = models["qwen3"]
+    with mlxr.Transformer(d, context_length=34100) as m:
+        assert m.persistent_decode
+        for n in (20000, 34000):
+            toks = prompt(n, 1000, seed=n % 97)
+            m.set_decode_mode(1)
+            a = m.generate(toks, 6, GREEDY)
+            m.set_decode_mode(0)
+            b = m.generate(toks, 6, GREEDY)
+            if a != b:
+                i = next(k for k in range(len(a)) if a[k] != b[k])
+                logits = m.forward(np.concatenate([toks, np.array(a[:i], np.int32)]), 0)
+                assert abs(logits[a[i]] - logits[b[i]]) < LOGIT_TOL, (n, i)
+
+
 @pytest.mark.parametrize("name", ["qwen3", "qwen2", "llama"])
 def test_decode_tiles_match_mlx_layout(gpu, models, name):
     """Single-token steps of the kernel-per-op path: the matvecs over the repacked tiles (decode mode
