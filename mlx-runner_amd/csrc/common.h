@@ -69,6 +69,17 @@ __device__ __forceinline__ float xor32_max(float v) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float wave_sum(float v) { return xor32_sum(xor16_sum(row16_sum(v))); }
+
+// Workgroup barrier for LDS traffic only. __syncthreads() also waits for every global load and store
+// the wave has in flight (vmcnt 0: a weight prefetch, tagged write-backs); this waits for the wave's
+// LDS (and scalar) accesses alone, so those stay in flight across it. The asm statements keep the
+// compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // lgkmcnt(0); vmcnt and expcnt at their maxima (no wait)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 __device__ __forceinline__ float wave_max(float v) { return xor32_max(xor16_max(row16_max(v))); }
 
 // KV cache addressing: layer cache [n_pages][nKV][PAGE][D] bf16; pt maps logical page -> physical.

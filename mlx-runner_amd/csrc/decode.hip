@@ -123,7 +123,7 @@ __device__ __forceinline__ void prof_mark(unsigned long long* prof, int ev) {
 template <int MODE, int FB>
 __device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, int wg, int nwg, const float* part, uint2* out,
                                               unsigned tag, float* logits, const float* hown, float* red, int* redi) {
-    __syncthreads();
+    lds_barrier();
     const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
     const int nfw = g.nt * g.NF;
     MvResult res{-INFINITY, 0x7fffffff};
@@ -158,7 +158,7 @@ __device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, i
             if (m2 > m || (m2 == m && i2 < idx)) { m = m2; idx = i2; }
         }
         if ((threadIdx.x & 63) == 0) { red[threadIdx.x >> 6] = m; redi[threadIdx.x >> 6] = idx; }
-        __syncthreads();
+        lds_barrier();
         res.best = -INFINITY; res.best_idx = 0x7fffffff;
         for (int w = 0; w < MK_WAVES; w++)
             if (red[w] > res.best || (red[w] == res.best && redi[w] < res.best_idx)) { res.best = red[w]; res.best_idx = redi[w]; }
@@ -214,7 +214,7 @@ __device__ __forceinline__ float2 fetch_to_lds(const uint2* src, int K, unsigned
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
     if ((threadIdx.x & 63) == 0) red[8 + (threadIdx.x >> 6)] = v;
-    __syncthreads();
+    lds_barrier();
     float m = 0.0f;
     for (int i = 0; i < MK_WAVES; i++) m = fmaxf(m, red[8 + i]);
     return m;
@@ -227,7 +227,7 @@ __device__ __forceinline__ float norm_to_lds(const uint2* src, unsigned tag, con
                                             const MvLds& L, int gsh, float* red) {
     const float ss = wave_sum(fetch_to_lds(src, K, tag, tw, L.xf).x);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
+    lds_barrier();
     float tot = 0.0f;
     for (int i = 0; i < MK_WAVES; i++) tot += red[i];
     const float inv = 1.0f / sqrtf(tot / (float)K + eps);
@@ -377,14 +377,14 @@ __device__ __forceinline__ float head_norm_rope(float v, int i, const float* nw,
     if (nw) {
         float ss = wave_sum(v * v);
         if ((i & 63) == 0) red[grp * 2 + (i >> 6)] = ss;
-        __syncthreads();
+        lds_barrier();
         const float tot = red[grp * 2] + red[grp * 2 + 1];
         v = v * (1.0f / sqrtf(tot / 128.0f + eps)) * nw[i];
     } else {
-        __syncthreads();
+        lds_barrier();
     }
     buf[i] = v;
-    __syncthreads();
+    lds_barrier();
     float out = v;
     if (i < rot_dim) {
         const int half = rot_dim / 2;
@@ -395,7 +395,7 @@ __device__ __forceinline__ float head_norm_rope(float v, int i, const float* nw,
         const float c = cosf(ang), sn = sinf(ang);
         out = first ? v * c - buf[partner] * sn : v * c + buf[partner] * sn;
     }
-    __syncthreads();
+    lds_barrier();
     return out;
 }
 
@@ -519,7 +519,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     ly.kc[row] = kb; ly.vc[row] = vb;
                 }
             }
-            __syncthreads();
+            lds_barrier();
             prof_mark(a.prof, 512 + 8 * li + 7);
 
             float acc[MAXG][4];
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 }
                 mloc = xor32_max(xor16_max(mloc));
                 if (lane < 16) wred[lane * MK_WAVES + wave] = mloc;
-                __syncthreads();
+                lds_barrier();
                 // new running max per head; probabilities of this lane's keys
                 const float4 wa = *reinterpret_cast<const float4*>(wred + hh * MK_WAVES);
                 const float4 wb = *reinterpret_cast<const float4*>(wred + hh * MK_WAVES + 4);
@@ -609,7 +609,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     alpha[g] = expf(mls[g] - mn);
                 }
                 if (cn < nchunks) att_prefetch_k(a, ly, kvh, n0, nf, cn, kvpf);   // while softmax and P.V run
-                __syncthreads();
+                lds_barrier();
                 // running sums (one thread per head), then P.V with the rescaled accumulators
                 if (tid < G) {
                     const float4 ma = *reinterpret_cast<const float4*>(wred + tid * MK_WAVES);
@@ -685,7 +685,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     }
                 }
             }
-            __syncthreads();
+            lds_barrier();
             // partials: plain agent-scope stores, then (once they are complete) this range's ready tag
             const unsigned atag = tag_of(3 + 5 * li);
             const int P = nH * nsplit;
@@ -699,7 +699,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 if (d == 0) { st_ag(pm + r, nk > 0 ? mls[g] : -1e30f); st_ag(pl + r, nk > 0 ? mls[16 + g] : 0.0f); }
             }
             __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
+            lds_barrier();
             if (tid == 0) st_tag(a.part_ready + kvh * nsplit + split, 0.0f, atag);
             prof_mark(a.prof, 512 + 8 * li + 3);
             if (split == nsplit - 1) {
@@ -707,7 +707,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 // every range's ready tag is up: all loads of the merge in one round trip, the weights
                 // exp(m_s - M) computed by every (head, dim) thread from the staged maxima
                 if (tid < nsplit) ld_tag1(a.part_ready, kvh * nsplit + tid, nKV * nsplit, atag, tw);
-                __syncthreads();
+                lds_barrier();
                 float* wts = wacc;                                  // [G][nsplit] maxima
                 float* lsv = wacc + MK_MAXG * 64;                   // [G][nsplit] sums
                 for (int idx = tid; idx < G * nsplit; idx += MK_THREADS) {
@@ -721,7 +721,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     float v[MK_MERGE_B];
 #pragma unroll
                     for (int q = 0; q < MK_MERGE_B; q++) v[q] = ld_coh1(pa, (rb + min(q, nsplit - 1)) * 128 + d, P * 128);
-                    __syncthreads();                                // the maxima and sums are staged
+                    lds_barrier();                                // the maxima and sums are staged
                     float M = -1e30f;
                     for (int s = 0; s < nsplit; s++) M = fmaxf(M, wts[g * nsplit + s]);
                     float o = 0.0f, Ls = 0.0f;

@@ -45,7 +45,7 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
     }
     ss = wave_sum(ss); mx = wave_max(mx);
     if (lane == 0) { red[wave] = ss; red[8 + wave] = mx; }
-    __syncthreads();
+    lds_barrier();
     float tot = 0.0f, gmax = 0.0f;
     for (int i = 0; i < MK_WAVES; i++) { tot += red[i]; gmax = fmaxf(gmax, red[8 + i]); }
     const float inv = nw ? 1.0f / sqrtf(tot / (float)K + eps) : 1.0f;
@@ -65,7 +65,7 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
         unscale = pack_x16_from(ld, K, gmax, L, GSH);
     }
     mv_run<FB>(p, L.xh, L.gsum, L.zero16, wg, nwg, wave, lane, ring, L.part);
-    __syncthreads();
+    lds_barrier();
     const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
     const int nfw = g.nt * g.NF;
     if (MODE == OUT_GATED) {

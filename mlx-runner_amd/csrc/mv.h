@@ -62,16 +62,18 @@ template <int FB>
 __device__ __forceinline__ MvGeom<FB> mv_geom(const MvPhase& p, int wg, int nwg, int wave) {
     MvGeom<FB> g;
     g.KBT = p.K >> 7; g.NF = (g.KBT + FB - 1) / FB;
-    g.t0 = (int)((int64_t)p.tiles * wg / nwg);
-    g.nt = (int)((int64_t)p.tiles * (wg + 1) / nwg) - g.t0;
+    // 32-bit: tiles * workgroups stays far below 2^31 (tiles <= 2^16, checked at setup)
+    g.t0 = (int)((unsigned)(p.tiles * wg) / (unsigned)nwg);
+    g.nt = (int)((unsigned)(p.tiles * (wg + 1)) / (unsigned)nwg) - g.t0;
     const int nfw = g.nt * g.NF;
-    g.f0 = nfw * wave / MK_WAVES; g.f1 = nfw * (wave + 1) / MK_WAVES;
+    g.f0 = (nfw * wave) >> 3; g.f1 = (nfw * (wave + 1)) >> 3;   // MK_WAVES == 8
+    static_assert(MK_WAVES == 8, "wave split");
     return g;
 }
 // This lane's slice of the wave's first scale group.
 template <int FB>
 __device__ __forceinline__ gptr8 mv_base(const MvPhase& p, const MvGeom<FB>& g, int lane) {
-    return (gptr8)p.code + ((int64_t)g.t0 * g.NF + g.f0) * ((FB + 1) * 1024) + lane * 16;
+    return (gptr8)p.code + (size_t)(unsigned)(g.t0 * g.NF + g.f0) * ((FB + 1) * 1024) + lane * 16;
 }
 
 template <int FB>
@@ -149,7 +151,7 @@ __device__ __forceinline__ float pack_x16_from(const LD& ld, int K, float gmax, 
         xsum += __shfl_xor(xsum, 1, 64); xsum += __shfl_xor(xsum, 2, 64);
         if ((t & 3) == 0) *reinterpret_cast<float2*>(xh + c * XH_STRIDE + 16) = float2{1024.0f * cs, xsum};
     }
-    __syncthreads();
+    lds_barrier();
     const int cpg = 1 << (gsh - 5);   // chunks per group
     for (int g = threadIdx.x; g < (K >> gsh); g += MK_THREADS) {
         float2 s = {0.0f, 0.0f};
@@ -159,7 +161,7 @@ __device__ __forceinline__ float pack_x16_from(const LD& ld, int K, float gmax, 
         }
         *reinterpret_cast<float2*>(gsum + 2 * g) = s;
     }
-    __syncthreads();
+    lds_barrier();
     return 1.0f / up;
 }
 __device__ __forceinline__ float pack_x16(const float* xf, int K, float gmax, const MvLds& L, int gsh) {
@@ -187,9 +189,11 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
     f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f};
     int tile = g.f0 / g.NF, f = g.f0 - tile * g.NF;   // scale group within the tile
     for (int i = 0; i < nfb; i++) {
-        const gptr8 nxt = base + (int64_t)min(i + 1, nfb - 1) * ((FB + 1) * 1024);   // the last reloads itself
+        // the next scale group streams in behind this one (none after the last: no load is left in flight)
+        const bool more = i + 1 < nfb;
+        const gptr8 nxt = base + (int64_t)(i + 1) * ((FB + 1) * 1024);
         const uint4 sbr = ring.u[0];
-        ring.u[0] = ld_stream16(nxt);
+        if (more) ring.u[0] = ld_stream16(nxt);
         const float* xb = xh + (lane >> 4) * 4 + f * (4 * FB) * XH_STRIDE;   // this lane's slot of the group's first chunk
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -204,7 +208,7 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
                 const f16x8_t b = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(bp));
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b, acc, 0, 0, 0);
             }
-            ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
+            if (more) ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
         }
         // scales of the 16 groups (groups past the row's last are zero-scaled; their sums may be junk)
         const int gi = 16 * f + col;

@@ -34,6 +34,8 @@ def models():
         "llama": configs.tiny("llama", tie=False, theta=500000.0),
         "qwen3_g128_8bit": configs.tiny("qwen3", bits=8, gs=128, layers=1),
         "qwen3_3bit": configs.tiny("qwen3", bits=3, gs=32, layers=1),
+        # hidden 1024 at gs 32: wider rows (two scale groups per 16-row tile)
+        "qwen3_h1024": configs.tiny("qwen3", hidden=1024, inter=1024, gs=32),
     }.items():
         d = os.path.join(tmp, name)
         mlxr.synth_write(cfg, seed=1234, directory=d)
@@ -96,7 +98,7 @@ def test_graph_and_eager_decode_agree(gpu, models):
     assert a == b
 
 
-@pytest.mark.parametrize("name", ["qwen3", "qwen2", "llama"])
+@pytest.mark.parametrize("name", ["qwen3", "qwen2", "llama", "qwen3_h1024"])
 def test_persistent_decode_matches_kernel_per_op(gpu, models, name):
     """The persistent decode step (one launch per token) against the kernel-per-op step: same greedy
     tokens (teacher-forced against the oracle where they part), logits within the 2e-2 gate."""
