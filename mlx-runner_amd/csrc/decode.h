@@ -70,12 +70,14 @@ struct MegaArgs {
     int* abort_host;                  // host-mapped copy of sync->abort (read by the host after a step)
     int select;                       // 1: greedy token selection fused (writes hist / ring, advances *dpos)
     int kv_stage;                     // 1: a range's second chunk of keys is staged in LDS (cache byte offsets < 2^31)
+    int desc_lds_off;                 // byte offset of the layers' descriptors in the workgroup's LDS
     int* ring_tok; int* ring_status; int ring_mask;
     unsigned long long* prof;         // optional: per workgroup, wall-clock at every phase start / end
 };
 constexpr int MEGA_PROF_EVENTS = 1024;
 
-size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split);
+size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split);   // a.L, a.kv_stage and the shape set
+size_t mega_desc_offset(const MegaArgs& a);
 hipError_t launch_decode_step(const MegaArgs& a, int nwg, size_t lds, hipStream_t s);
 hipError_t mega_set_lds_limit(size_t lds);
 int mega_threads();

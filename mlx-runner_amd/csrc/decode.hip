@@ -112,6 +112,11 @@ __device__ __forceinline__ float ld_tag1(const uint2* base, int i, int n, unsign
     return __uint_as_float(v.x);
 }
 
+// Every layer's descriptors are copied into LDS at the start of a launch and read from there: a
+// global load of a descriptor field would make its wait also wait for every global load and store
+// the wave has in flight (that counter completes in order), such as the next phase's weight
+// prefetch or the tagged results just stored, at every phase boundary.
+
 // Profile marks (optional): wall clock of phase boundaries, per workgroup.
 __device__ __forceinline__ void prof_mark(unsigned long long* prof, int ev) {
     if (prof && threadIdx.x == 0 && ev < MEGA_PROF_EVENTS) prof[(size_t)blockIdx.x * MEGA_PROF_EVENTS + ev] = wall_clock64();
@@ -442,15 +447,25 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             for (int j = 0; j < 8; j++) st_tag(a.hA + c * 8 + j, (float)((w >> (4 * j)) & 15u) * s + b, tag_of(1));
         }
     }
+    // the layers' descriptors into LDS (read at every phase; see above)
+    LayerDev* ldesc = reinterpret_cast<LayerDev*>(reinterpret_cast<uint8_t*>(lds) + a.desc_lds_off);
+    {
+        static_assert(sizeof(LayerDev) % 16 == 0, "descriptor copy in 16-byte units");
+        const uint4* src = reinterpret_cast<const uint4*>(a.layers);
+        uint4* dst = reinterpret_cast<uint4*>(ldesc);
+        const int n = a.L * (int)(sizeof(LayerDev) / 16);
+        for (int i = tid; i < n; i += MK_THREADS) dst[i] = src[i];
+    }
+    lds_barrier();
     unsigned epoch = 0;                                   // phase boundaries of this launch (profile marks)
     prof_mark(a.prof, 0);
     prof_mark(a.prof, 2 * epoch); ++epoch;
-    mv_prefetch<FB>(a.layers[0].qkv, wg, nwg, wave, lane, ring);
+    mv_prefetch<FB>(ldesc[0].qkv, wg, nwg, wave, lane, ring);
     prof_mark(a.prof, 2 * epoch - 1);
 
     const int nsplit = nwg / nKV;
     for (int li = 0; li < a.L; li++) {
-        const LayerDev& ly = a.layers[li];
+        const LayerDev& ly = ldesc[li];
         // ---- A: q|k|v
         {
             const float us = norm_to_lds(a.hA, tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), tw, ly.in_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
@@ -782,7 +797,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.hA, tag_of(6 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
-        if (li + 1 < a.L) mv_prefetch<FB>(a.layers[li + 1].qkv, wg, nwg, wave, lane, ring);
+        if (li + 1 < a.L) mv_prefetch<FB>(ldesc[li + 1].qkv, wg, nwg, wave, lane, ring);
         else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
     }
@@ -892,8 +907,10 @@ size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split) {
     if (att > (size_t)ATT_KVL_OFF || (size_t)(MK_TPW * MK_WAVES * 16 + MK_HOWN) * 4 > (size_t)ATT_KVL_OFF) return (size_t)-1;
     if (a.kv_stage) att = ATT_KVL_OFF + ATT_KVL_BYTES;   // the staged second chunk of keys
     (void)max_keys_per_split; (void)G;
-    return std::max(mv, att);
+    // then every layer's descriptors (copied in at the start of the launch)
+    return (std::max(mv, att) + 15) / 16 * 16 + (size_t)a.L * sizeof(LayerDev);
 }
+size_t mega_desc_offset(const MegaArgs& a) { return mega_lds_bytes(a, 0) - (size_t)a.L * sizeof(LayerDev); }
 
 // Every layer's matrices share the group size (checked at setup); a.head.gs selects the variant.
 hipError_t launch_decode_step(const MegaArgs& a, int nwg, size_t lds, hipStream_t s) {
