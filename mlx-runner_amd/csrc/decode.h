@@ -71,6 +71,7 @@ struct MegaArgs {
     int select;                       // 1: greedy token selection fused (writes hist / ring, advances *dpos)
     int kv_stage;                     // 1: a range's second chunk of keys is staged in LDS (cache byte offsets < 2^31)
     int desc_lds_off;                 // byte offset of the layers' descriptors in the workgroup's LDS
+    int n_pages, pt_lds_off;          // page table entries, byte offset of their LDS copy
     int* ring_tok; int* ring_status; int ring_mask;
     unsigned long long* prof;         // optional: per workgroup, wall-clock at every phase start / end
 };

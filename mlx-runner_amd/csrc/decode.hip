@@ -278,7 +278,7 @@ __device__ __forceinline__ void att_load_k(const MegaArgs& a, const LayerDev& ly
                                            KVPrefetch& pf);
 __device__ __forceinline__ void att_load_v(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
                                            KVPrefetch& pf);
-__device__ __forceinline__ void att_prefetch_k(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int nf, int c, KVPrefetch& pf) {
+__device__ __forceinline__ void att_prefetch_k(const MegaArgs& a, const int* pt, const LayerDev& ly, int kvh, int n0, int nf, int c, KVPrefetch& pf) {
     if (nf <= n0) {
 #pragma unroll
         for (int db = 0; db < 4; db++) pf.k[db] = uint4{0u, 0u, 0u, 0u};
@@ -287,7 +287,7 @@ __device__ __forceinline__ void att_prefetch_k(const MegaArgs& a, const LayerDev
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int kb = n0 + 128 * c + 16 * wave;            // the wave's 16 keys span at most two pages
     const int jf = min(kb, nf - 1), jl = min(kb + 15, nf - 1);
-    const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = a.pt[pg0], e1 = a.pt[jl >> MLXR_PAGE_SHIFT];
+    const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = pt[pg0], e1 = pt[jl >> MLXR_PAGE_SHIFT];
     att_load_k(a, ly, kvh, kb, nf, pg0, e0, e1, pf);
 }
 // K rows of the wave's 16 keys from kb, with the page entries of the first and last already loaded.
@@ -300,7 +300,7 @@ __device__ __forceinline__ void att_load_k(const MegaArgs& a, const LayerDev& ly
 #pragma unroll
     for (int db = 0; db < 4; db++) pf.k[db] = ld_stream16((gptr8)(ly.kc + rk + 32 * db));
 }
-__device__ __forceinline__ void att_prefetch_v(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int nf, int c, KVPrefetch& pf) {
+__device__ __forceinline__ void att_prefetch_v(const MegaArgs& a, const int* pt, const LayerDev& ly, int kvh, int n0, int nf, int c, KVPrefetch& pf) {
     if (nf <= n0) {
 #pragma unroll
         for (int r = 0; r < 8; r++) pf.v[r] = uint2{0u, 0u};
@@ -309,7 +309,7 @@ __device__ __forceinline__ void att_prefetch_v(const MegaArgs& a, const LayerDev
     const int t = threadIdx.x;
     const int kb = n0 + 128 * c + 8 * (t >> 5);          // the thread's 8 keys span at most two pages
     const int jf = min(kb, nf - 1), jl = min(kb + 7, nf - 1);
-    const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = a.pt[pg0], e1 = a.pt[jl >> MLXR_PAGE_SHIFT];
+    const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = pt[pg0], e1 = pt[jl >> MLXR_PAGE_SHIFT];
     att_load_v(a, ly, kvh, kb, nf, pg0, e0, e1, pf);
 }
 // V slices of the thread's 8 keys from kb, with the page entries of the first and last already loaded.
@@ -348,8 +348,8 @@ __device__ __forceinline__ void att_stage1(const MegaArgs& a, const LayerDev& ly
 }
 // Start of the attention phase: chunk 0's K / V into registers and, for a staged range, chunk 1 into
 // LDS; every page entry these need is loaded first, together (one round trip before the data loads).
-__device__ __forceinline__ void att_begin(const MegaArgs& a, const LayerDev& ly, int kvh, int n0, int nf, bool staged, uint8_t* kvl,
-                                          KVPrefetch& pf) {
+__device__ __forceinline__ void att_begin(const MegaArgs& a, const int* pt, const LayerDev& ly, int kvh, int n0, int nf, bool staged,
+                                          uint8_t* kvl, KVPrefetch& pf) {
     if (nf <= n0) {
 #pragma unroll
         for (int db = 0; db < 4; db++) pf.k[db] = uint4{0u, 0u, 0u, 0u};
@@ -360,9 +360,9 @@ __device__ __forceinline__ void att_begin(const MegaArgs& a, const LayerDev& ly,
     const int t = threadIdx.x, wave = t >> 6;
     const int kk = n0 + 16 * wave, kv = n0 + 8 * (t >> 5), ks = n0 + 128 + 16 * wave;
     const int pk = min(kk, nf - 1) >> MLXR_PAGE_SHIFT, pv = min(kv, nf - 1) >> MLXR_PAGE_SHIFT, ps = min(ks, nf - 1) >> MLXR_PAGE_SHIFT;
-    const int ek0 = a.pt[pk], ek1 = a.pt[min(kk + 15, nf - 1) >> MLXR_PAGE_SHIFT];
-    const int ev0 = a.pt[pv], ev1 = a.pt[min(kv + 7, nf - 1) >> MLXR_PAGE_SHIFT];
-    const int es0 = a.pt[ps], es1 = a.pt[min(ks + 15, nf - 1) >> MLXR_PAGE_SHIFT];
+    const int ek0 = pt[pk], ek1 = pt[min(kk + 15, nf - 1) >> MLXR_PAGE_SHIFT];
+    const int ev0 = pt[pv], ev1 = pt[min(kv + 7, nf - 1) >> MLXR_PAGE_SHIFT];
+    const int es0 = pt[ps], es1 = pt[min(ks + 15, nf - 1) >> MLXR_PAGE_SHIFT];
     att_load_k(a, ly, kvh, kk, nf, pk, ek0, ek1, pf);
     att_load_v(a, ly, kvh, kv, nf, pv, ev0, ev1, pf);
     if (staged) att_stage1(a, ly, kvh, ks, nf, ps, es0, es1, kvl);
@@ -456,6 +456,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         const int n = a.L * (int)(sizeof(LayerDev) / 16);
         for (int i = tid; i < n; i += MK_THREADS) dst[i] = src[i];
     }
+    // the page table too (the attention phase's row lookups must not wait on global traffic either)
+    int* lpt = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(lds) + a.pt_lds_off);
+    for (int i = tid; i < a.n_pages; i += MK_THREADS) lpt[i] = a.pt[i];
     lds_barrier();
     unsigned epoch = 0;                                   // phase boundaries of this launch (profile marks)
     prof_mark(a.prof, 0);
@@ -480,7 +483,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         int n0, n1; att_range(L, nsplit, split, n0, n1);
         uint8_t* kvl = reinterpret_cast<uint8_t*>(lds) + ATT_KVL_OFF;
         const bool staged = a.kv_stage && n1 - n0 > 128;   // chunk 1 joins chunk 0's pass from LDS
-        att_begin(a, ly, kvh, n0, min(n1, pos), staged, kvl, kvpf);
+        att_begin(a, lpt, ly, kvh, n0, min(n1, pos), staged, kvl, kvpf);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- B: attention for (kvh, split): scores on the matrix cores (K rows from the bf16 cache as
@@ -530,7 +533,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 if (tid < 128) {
                     const uint16_t kb = f32_to_bf16(ko), vb = f32_to_bf16(vraw);
                     kn16[i] = kb; vn16[i] = vb;
-                    const int64_t row = kv_row(a.pt, nKV, kvh, pos) * 128 + i;
+                    const int64_t row = kv_row(lpt, nKV, kvh, pos) * 128 + i;
                     ly.kc[row] = kb; ly.vc[row] = vb;
                 }
             }
@@ -623,7 +626,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     const float mn = fmaxf(mls[g], fmaxf(fmaxf(fmaxf(ga.x, ga.y), fmaxf(ga.z, ga.w)), fmaxf(fmaxf(gb.x, gb.y), fmaxf(gb.z, gb.w))));
                     alpha[g] = expf(mls[g] - mn);
                 }
-                if (cn < nchunks) att_prefetch_k(a, ly, kvh, n0, nf, cn, kvpf);   // while softmax and P.V run
+                if (cn < nchunks) att_prefetch_k(a, lpt, ly, kvh, n0, nf, cn, kvpf);   // while softmax and P.V run
                 lds_barrier();
                 // running sums (one thread per head), then P.V with the rescaled accumulators
                 if (tid < G) {
@@ -684,7 +687,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                         }
                     }
                 }
-                if (cn < nchunks) att_prefetch_v(a, ly, kvh, n0, nf, cn, kvpf);
+                if (cn < nchunks) att_prefetch_v(a, lpt, ly, kvh, n0, nf, cn, kvpf);
                 c = cn;
             }
             prof_mark(a.prof, 512 + 8 * li + 1);
@@ -907,10 +910,12 @@ size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split) {
     if (att > (size_t)ATT_KVL_OFF || (size_t)(MK_TPW * MK_WAVES * 16 + MK_HOWN) * 4 > (size_t)ATT_KVL_OFF) return (size_t)-1;
     if (a.kv_stage) att = ATT_KVL_OFF + ATT_KVL_BYTES;   // the staged second chunk of keys
     (void)max_keys_per_split; (void)G;
-    // then every layer's descriptors (copied in at the start of the launch)
-    return (std::max(mv, att) + 15) / 16 * 16 + (size_t)a.L * sizeof(LayerDev);
+    // then every layer's descriptors and the page table (copied in at the start of the launch)
+    return (std::max(mv, att) + 15) / 16 * 16 + (size_t)a.L * sizeof(LayerDev) + ((size_t)a.n_pages * 4 + 15) / 16 * 16;
 }
-size_t mega_desc_offset(const MegaArgs& a) { return mega_lds_bytes(a, 0) - (size_t)a.L * sizeof(LayerDev); }
+size_t mega_desc_offset(const MegaArgs& a) {
+    return mega_lds_bytes(a, 0) - (size_t)a.L * sizeof(LayerDev) - ((size_t)a.n_pages * 4 + 15) / 16 * 16;
+}
 
 // Every layer's matrices share the group size (checked at setup); a.head.gs selects the variant.
 hipError_t launch_decode_step(const MegaArgs& a, int nwg, size_t lds, hipStream_t s) {

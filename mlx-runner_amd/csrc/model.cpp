@@ -403,9 +403,10 @@ static int mega_setup(Model* m) {
     a.H = c.H; a.nH = c.nH; a.nKV = c.nKV; a.I = c.I; a.rot_dim = c.rot_dim; a.traditional = c.traditional;
     // a layer's K (or V) cache in bytes: the LDS-staged chunk addresses it with 32-bit offsets
     a.kv_stage = (double)m->n_pages * c.nKV * MLXR_PAGE * c.D * 2 < 2147483648.0 ? 1 : 0;
-    a.L = c.L;
+    a.L = c.L; a.n_pages = m->n_pages;
     const size_t lds = mega_lds_bytes(a, max_keys);
     a.desc_lds_off = (int)mega_desc_offset(a);
+    a.pt_lds_off = a.desc_lds_off + (int)(sizeof(LayerDev) * c.L);
     if (lds > 150 * 1024) return no("LDS need " + std::to_string(lds >> 10) + " KiB");
     if (mega_set_lds_limit(lds) != hipSuccess) return no("LDS attribute");
     if (nwg > MEGA_MAX_WG) return no("too many workgroups");
