@@ -195,7 +195,8 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
         const uint4 sbr = ring.u[0];
         if (more) ring.u[0] = ld_stream16(nxt);
         const float* xb = xh + (lane >> 4) * 4 + f * (4 * FB) * XH_STRIDE;   // this lane's slot of the group's first chunk
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        // two accumulators (even / odd chunks): half the dependent MFMA chain
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int k = 0; k < FB; k++) {
             const uint4 unit = ring.u[k + 1];
@@ -206,7 +207,8 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
                 const int gcol = (4 * k + j) / CPG;                        // the chunk's group column
                 const float* bp = col == gcol ? xb + (4 * k + j) * XH_STRIDE : zero16;
                 const f16x8_t b = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(bp));
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b, acc, 0, 0, 0);
+                if (j & 1) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b, acc2, 0, 0, 0);
+                else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b, acc, 0, 0, 0);
             }
             if (more) ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
         }
@@ -214,6 +216,7 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
         const int gi = 16 * f + col;
         const bool real = gi < gpr;
         const float2 gs2 = *reinterpret_cast<const float2*>(gsum + 2 * (real ? gi : 0));
+        acc += acc2;
         const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -252,10 +255,14 @@ __device__ __forceinline__ float row_bias(const MvPhase& p, int vr) {
 // Row r of tile tl of this workgroup: the partial sums of the waves whose ranges meet the tile, in
 // wave order.
 __device__ __forceinline__ float tile_row(const float* part, int tl, int r, int nfw, int NF) {
+    float v[MK_WAVES];
+#pragma unroll
+    for (int w = 0; w < MK_WAVES; w++) v[w] = part[(tl * MK_WAVES + w) * 16 + r];   // all read at once, then masked
     float s = 0.0f;
+#pragma unroll
     for (int w = 0; w < MK_WAVES; w++) {
-        const int a = nfw * w / MK_WAVES, b = nfw * (w + 1) / MK_WAVES;
-        if (a < b && a < (tl + 1) * NF && b > tl * NF) s += part[(tl * MK_WAVES + w) * 16 + r];   // non-empty, meets the tile
+        const int a = (nfw * w) >> 3, b = (nfw * (w + 1)) >> 3;
+        if (a < b && a < (tl + 1) * NF && b > tl * NF) s += v[w];   // non-empty, meets the tile
     }
     return s;
 }
