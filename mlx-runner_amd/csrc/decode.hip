@@ -376,15 +376,17 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4 v, float* o) {
 }
 
 // head vector (128, in LDS buf) -> per-head RMSNorm (optional) -> RoPE, 128 threads of one group
-__device__ __forceinline__ float head_norm_rope(float v, int i, const float* nw, float eps, const float* invf, int pos,
+// nwi: the norm weight of dimension i (loaded by the caller); rope: cos / sin of pos * inv_freq[f]
+// for f < rot_dim / 2 (LDS, computed once per launch).
+__device__ __forceinline__ float head_norm_rope(float v, int i, bool norm, float nwi, float eps, const float2* rope,
                                                 int rot_dim, int traditional, float* buf, float* red, int grp) {
     // grp: which 128-thread group (0..3) of the workgroup; red has 2 floats per group
-    if (nw) {
+    if (norm) {
         float ss = wave_sum(v * v);
         if ((i & 63) == 0) red[grp * 2 + (i >> 6)] = ss;
         lds_barrier();
         const float tot = red[grp * 2] + red[grp * 2 + 1];
-        v = v * (1.0f / sqrtf(tot / 128.0f + eps)) * nw[i];
+        v = v * (1.0f / sqrtf(tot / 128.0f + eps)) * nwi;
     } else {
         lds_barrier();
     }
@@ -396,9 +398,8 @@ __device__ __forceinline__ float head_norm_rope(float v, int i, const float* nw,
         int fi, partner; bool first;
         if (traditional) { fi = i / 2; partner = i ^ 1; first = (i & 1) == 0; }
         else { fi = i % half; first = i < half; partner = first ? i + half : i - half; }
-        const float ang = (float)pos * invf[fi];
-        const float c = cosf(ang), sn = sinf(ang);
-        out = first ? v * c - buf[partner] * sn : v * c + buf[partner] * sn;
+        const float2 cs = rope[fi];
+        out = first ? v * cs.x - buf[partner] * cs.y : v * cs.x + buf[partner] * cs.y;
     }
     lds_barrier();
     return out;
@@ -459,6 +460,12 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
     // the page table too (the attention phase's row lookups must not wait on global traffic either)
     int* lpt = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(lds) + a.pt_lds_off);
     for (int i = tid; i < a.n_pages; i += MK_THREADS) lpt[i] = a.pt[i];
+    // RoPE cos / sin of this step's position (the angle of every layer's q and k)
+    float2* rope = reinterpret_cast<float2*>(lpt + (a.n_pages + 3) / 4 * 4);
+    if (tid < a.rot_dim / 2) {
+        const float ang = (float)pos * a.inv_freq[tid];
+        rope[tid] = float2{cosf(ang), sinf(ang)};
+    }
     lds_barrier();
     unsigned epoch = 0;                                   // phase boundaries of this launch (profile marks)
     prof_mark(a.prof, 0);
@@ -483,6 +490,10 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         int n0, n1; att_range(L, nsplit, split, n0, n1);
         uint8_t* kvl = reinterpret_cast<uint8_t*>(lds) + ATT_KVL_OFF;
         const bool staged = a.kv_stage && n1 - n0 > 128;   // chunk 1 joins chunk 0's pass from LDS
+        // the q / k norm weights, loaded before the K / V loads (the memory counter completes in
+        // order: a load issued after them could only be used once they are in)
+        const int QKV = (nH + 2 * nKV) * D;
+        const float qnw = ly.q_norm ? ly.q_norm[tid & 127] : 1.0f, knw = ly.k_norm ? ly.k_norm[tid & 127] : 1.0f;
         att_begin(a, lpt, ly, kvh, n0, min(n1, pos), staged, kvl, kvpf);
         prof_mark(a.prof, 2 * epoch - 1);
 
@@ -505,7 +516,6 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const bool owns_new = pos >= n0 && pos < n1;
             // q heads (4 per pass of 512 threads), then the new k and v if this range holds pos
             const int grp = tid >> 7, i = tid & 127;
-            const int QKV = (nH + 2 * nKV) * D;
             // every value this workgroup needs from q|k|v, loaded at once
             const unsigned qtag = tag_of(2 + 5 * li);
             const float qv0 = ld_tag1(a.qkvT, (kvh * G + min(grp, G - 1)) * D + i, QKV, qtag, tw);
@@ -515,7 +525,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             for (int base = 0; base < G; base += 4) {
                 const int g = base + grp;
                 const float v = g < G ? (base == 0 ? qv0 : qv1) : 0.0f;
-                const float o = head_norm_rope(v, i, ly.q_norm, a.eps, a.inv_freq, pos, a.rot_dim, a.traditional, buf + grp * 128, red, grp);
+                const float o = head_norm_rope(v, i, ly.q_norm != nullptr, qnw, a.eps, rope, a.rot_dim, a.traditional, buf + grp * 128, red, grp);
                 if (g < G) {
                     const float q = o * a.scale;
                     const uint16_t hi = f32_to_bf16(q);
@@ -529,7 +539,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             }
             if (tid < 32) mls[tid] = tid < 16 ? -1e30f : 0.0f;
             if (owns_new) {
-                const float ko = head_norm_rope(tid < 128 ? kraw : 0.0f, i, ly.k_norm, a.eps, a.inv_freq, pos, a.rot_dim, a.traditional, buf + grp * 128, red, grp);
+                const float ko = head_norm_rope(tid < 128 ? kraw : 0.0f, i, ly.k_norm != nullptr, knw, a.eps, rope, a.rot_dim, a.traditional, buf + grp * 128, red, grp);
                 if (tid < 128) {
                     const uint16_t kb = f32_to_bf16(ko), vb = f32_to_bf16(vraw);
                     kn16[i] = kb; vn16[i] = vb;
@@ -911,10 +921,11 @@ size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split) {
     if (a.kv_stage) att = ATT_KVL_OFF + ATT_KVL_BYTES;   // the staged second chunk of keys
     (void)max_keys_per_split; (void)G;
     // then every layer's descriptors and the page table (copied in at the start of the launch)
-    return (std::max(mv, att) + 15) / 16 * 16 + (size_t)a.L * sizeof(LayerDev) + ((size_t)a.n_pages * 4 + 15) / 16 * 16;
+    // (and the RoPE table: 64 cos / sin pairs at most)
+    return (std::max(mv, att) + 15) / 16 * 16 + (size_t)a.L * sizeof(LayerDev) + ((size_t)a.n_pages * 4 + 15) / 16 * 16 + 64 * 8;
 }
 size_t mega_desc_offset(const MegaArgs& a) {
-    return mega_lds_bytes(a, 0) - (size_t)a.L * sizeof(LayerDev) - ((size_t)a.n_pages * 4 + 15) / 16 * 16;
+    return mega_lds_bytes(a, 0) - (size_t)a.L * sizeof(LayerDev) - ((size_t)a.n_pages * 4 + 15) / 16 * 16 - 64 * 8;
 }
 
 // Every layer's matrices share the group size (checked at setup); a.head.gs selects the variant.
