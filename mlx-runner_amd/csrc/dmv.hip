@@ -19,7 +19,7 @@ template <int FB, int MODE>
 __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, const float* __restrict__ x,
                                                               const float* __restrict__ nw, float eps, float* __restrict__ y, int tpw) {
     constexpr int GSH = FB == 4 ? 5 : 6;
-    extern __shared__ float lds[];
+    extern __shared__ __attribute__((aligned(16))) float lds[];
     const int K = p.K;
     MvLds L;
     L.xf = nullptr; L.hown = nullptr;
@@ -31,17 +31,27 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
     const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     Ring<FB> ring;
     mv_prefetch<FB>(p, wg, nwg, wave, lane, ring);
-    // statistics: sum of squares of x, max |x w| (max |x| without a norm)
+    // statistics: sum of squares of x, max |x w| (max |x| without a norm); four 16-byte loads per
+    // thread in flight (global address space: they cannot alias the LDS writes)
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    typedef const __attribute__((address_space(1))) f4v* gf4p;
+    auto gf4 = [](const float* p) { const f4v v = *(gf4p)p; return float4{v.x, v.y, v.z, v.w}; };
     float ss = 0.0f, mx = 0.0f;
-    for (int i = threadIdx.x * 4; i < K; i += MK_THREADS * 4) {
-        const float4 v = *reinterpret_cast<const float4*>(x + i);
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        float4 a = v;
-        if (nw) {
-            const float4 w = *reinterpret_cast<const float4*>(nw + i);
-            a.x *= w.x; a.y *= w.y; a.z *= w.z; a.w *= w.w;
+    for (int base = threadIdx.x * 4; base < K; base += MK_THREADS * 16) {
+        float4 v[4], w[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = base + u * MK_THREADS * 4;
+            v[u] = float4{0.0f, 0.0f, 0.0f, 0.0f}; w[u] = float4{1.0f, 1.0f, 1.0f, 1.0f};
+            if (i < K) v[u] = gf4(x + i);
+            if (nw && i < K) w[u] = gf4(nw + i);
         }
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
+            const float4 a = float4{v[u].x * w[u].x, v[u].y * w[u].y, v[u].z * w[u].z, v[u].w * w[u].w};
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        }
     }
     ss = wave_sum(ss); mx = wave_max(mx);
     if (lane == 0) { red[wave] = ss; red[8 + wave] = mx; }
@@ -51,17 +61,15 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
     const float inv = nw ? 1.0f / sqrtf(tot / (float)K + eps) : 1.0f;
     float unscale;
     if (nw) {
-        auto ld = [x, nw, inv](int t, float4& lo, float4& hi) {
-            lo = *reinterpret_cast<const float4*>(x + 8 * t); hi = *reinterpret_cast<const float4*>(x + 8 * t + 4);
-            const float4 wl = *reinterpret_cast<const float4*>(nw + 8 * t), wh = *reinterpret_cast<const float4*>(nw + 8 * t + 4);
+        auto ld = [x, nw, inv, gf4](int t, float4& lo, float4& hi) {
+            lo = gf4(x + 8 * t); hi = gf4(x + 8 * t + 4);
+            const float4 wl = gf4(nw + 8 * t), wh = gf4(nw + 8 * t + 4);
             lo.x = lo.x * inv * wl.x; lo.y = lo.y * inv * wl.y; lo.z = lo.z * inv * wl.z; lo.w = lo.w * inv * wl.w;
             hi.x = hi.x * inv * wh.x; hi.y = hi.y * inv * wh.y; hi.z = hi.z * inv * wh.z; hi.w = hi.w * inv * wh.w;
         };
         unscale = pack_x16_from(ld, K, gmax * inv, L, GSH);
     } else {
-        auto ld = [x](int t, float4& lo, float4& hi) {
-            lo = *reinterpret_cast<const float4*>(x + 8 * t); hi = *reinterpret_cast<const float4*>(x + 8 * t + 4);
-        };
+        auto ld = [x, gf4](int t, float4& lo, float4& hi) { lo = gf4(x + 8 * t); hi = gf4(x + 8 * t + 4); };
         unscale = pack_x16_from(ld, K, gmax, L, GSH);
     }
     mv_run<FB>(p, L.xh, L.gsum, L.zero16, wg, nwg, wave, lane, ring, L.part);
