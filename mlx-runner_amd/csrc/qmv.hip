@@ -86,7 +86,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f 
 // XNORM: x is normalised into LDS by the workgroup (K floats).
 template <int BITS, int ST, bool XNORM>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
-    extern __shared__ float xs_lds[];
+    extern __shared__ __attribute__((aligned(16))) float xs_lds[];
     __shared__ float red[QMV_WAVES];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int K = a.K;
