@@ -195,6 +195,8 @@ def long_main(a):
     cfg = configs.CONFIGS[a.config]
     d = model_dir(a.config, a.seed)
     model = mlxr.Transformer(d, context_length=a.context, sparse=mlxr.SparseAttention(min_context=5128))
+    if a.no_graphs:
+        model.set_graphs(False)
     total = model.max_seq - a.steps - a.warmup - 8      # the prompt leaves room for the decoded tokens
     first_turn = min(30000, total - 8)
     greedy = mlxr.SamplingParameters.greedy()
@@ -291,6 +293,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=360)
     ap.add_argument("--step-iters", type=int, default=64)
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="launch the kernel-per-op decode step kernel by kernel (profiling) instead of as a hipGraph")
     ap.add_argument("--decode-mode", type=int, default=1, choices=[0, 1, 2],
                     help="1: persistent decode step, 0: kernel per op (repacked tiles), 2: kernel per op (MLX layout)")
     ap.add_argument("--mode", default="decode", choices=["decode", "prefill", "sweep", "long"],
@@ -344,6 +348,8 @@ def main():
     model = mlxr.Transformer(d, context_length=need)
     log(f"[bench] model loaded in {time.time() - t:.1f}s ({model.weight_bytes / 1e9:.2f} GB of weights, {model.quant_description})")
     model.set_decode_mode(a.decode_mode)
+    if a.no_graphs:
+        model.set_graphs(False)
     greedy = mlxr.SamplingParameters.greedy()
     prompt = np.random.default_rng(a.seed).integers(0, model.vocab_size, a.context).astype(np.int32)
 
