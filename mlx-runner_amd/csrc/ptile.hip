@@ -16,8 +16,9 @@
 // the tiles 4 wq + 2 kc, + 1 against all 128 tokens (8 X fragments x 2 W fragments = 16 MFMAs per
 // 32-k step); two waves share each SIMD, so one issues MFMAs while the other waits on memory or
 // dequantizes. The X block (128 tokens x 128 k, f16, 16-byte chunks XOR-swizzled by (row & 15),
-// read by all eight waves) and the 16 code blocks are copied buffer -> LDS (two stages); the scale
-// blocks of a scale group (16 groups) once per group (two buffers). Gated phases (gate rows in tile rows 0-7, up rows in 8-15) finish with
+// read by all eight waves), the 16 code blocks and the block's scale words are copied buffer -> LDS
+// into three stages, two blocks ahead of the one being computed (one block ahead left about a third
+// of the waves' time waiting for the copies). Gated phases (gate rows in tile rows 0-7, up rows in 8-15) finish with
 // SiLU(gate) * up in the epilogue, so the MLP activation is written directly.
 #include "decode.h"
 
@@ -34,10 +35,11 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 constexpr int PT_M = 128, PT_TILES = 16, PT_KB = 128;
 constexpr int PT_XB = PT_M * 256;                   // X block
 constexpr int PT_CB = PT_TILES * 1024;              // code blocks
-constexpr int PT_STAGE = PT_XB + PT_CB;
-constexpr int PT_NST = 2;
-constexpr int PT_SC = PT_TILES * 1024;              // scale blocks of one scale group
-constexpr int PT_LDS = PT_NST * PT_STAGE + 2 * PT_SC;
+constexpr int PT_SB = PT_TILES * 256;               // the scale words of one block's groups
+constexpr int PT_STAGE = PT_XB + PT_CB + PT_SB;
+constexpr int PT_NST = 3;                           // stages: copies run two blocks ahead
+constexpr int PT_LDS = PT_NST * PT_STAGE;
+constexpr int PT_WAIT_ONE_AHEAD = 0x0F77;           // s_waitcnt vmcnt(7): one block's copies still in flight
 constexpr int PT_RSRC_W3 = 0x00020000;              // raw buffer, 32-bit data format
 
 struct TileGemmArgs {
@@ -78,8 +80,10 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
 #pragma unroll
         for (int u = 0; u < 2; u++) acc[i][u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // this wave's copies of block blk: X rows 16 w .. 16 w + 15 (4 x 1 KB), the code blocks of
-    // workgroup tiles 2 w, 2 w + 1, and at a scale group's first block their scale blocks
+    // this wave's copies of block blk (7 per wave): X rows 16 w .. 16 w + 15 (4 x 1 KB), the code
+    // blocks of workgroup tiles 2 w, 2 w + 1, and their scale words of the block's 128 / gs groups
+    // (lanes 0-31: tile 2 w + (lane >> 4), 16-byte chunk (rows 4 rq .. 4 rq + 3, group gl) with
+    // lane & 15 = 4 rq + gl; chunks past the block's groups are loaded and never read)
     auto issue = [&](int blk) {
         uint8_t* st = pt_lds + (blk % PT_NST) * PT_STAGE;
 #pragma unroll
@@ -88,15 +92,18 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
             const uint32_t off = (uint32_t)(m0 + r) * (uint32_t)K * 2u + blk * 256 + 16 * (r16 ^ (r & 15));
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr_t)(st + qq * 1024), 16, off, 0, 0, 0);
         }
-        const int f = blk / FB, pos = blk - f * FB + 1;
+        const int f = blk / FB, bl = blk - f * FB;
 #pragma unroll
         for (int c = 0; c < 2; c++) {
             const int tw = 2 * wave + c;
             const uint32_t base = (uint32_t)(t0 + tw) * tile_bytes + (uint32_t)f * (FB + 1) * 1024 + lane * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(st + PT_XB + tw * 1024), 16, base + pos * 1024, 0, 0, 0);
-            if (pos == 1)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(pt_lds + PT_NST * PT_STAGE + (f & 1) * PT_SC + tw * 1024),
-                                                         16, base, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(st + PT_XB + tw * 1024), 16, base + (bl + 1) * 1024, 0, 0, 0);
+        }
+        if (lane < 32) {
+            const int tw = 2 * wave + (lane >> 4), l = lane & 15;
+            const uint32_t off = (uint32_t)(t0 + tw) * tile_bytes + (uint32_t)f * (FB + 1) * 1024 +
+                                 ((l >> 2) * 16 + bl * (PT_KB / a.p.gs) + (l & 3)) * 16;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(st + PT_XB + PT_CB + 2 * wave * 256), 16, off, 0, 0, 0);
         }
     };
 
@@ -105,19 +112,18 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
     // dequantized W are produced while step j's MFMAs run.
     auto compute = [&](int blk, int pf) {
         const uint8_t* st = pt_lds + (blk % PT_NST) * PT_STAGE;
-        const int f = blk / FB, bl = blk - f * FB;
-        const uint8_t* sc = pt_lds + PT_NST * PT_STAGE + (f & 1) * PT_SC;
+        const uint8_t* sc = st + PT_XB + PT_CB;
         q4u4_t cw[2];
 #pragma unroll
         for (int u = 0; u < 2; u++) cw[u] = *reinterpret_cast<const q4u4_t*>(st + PT_XB + (4 * wq + 2 * kc + u) * 1024 + lane * 16);
         half2_t s2[4][2], b2[4][2];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int gl = ((bl * PT_KB + 32 * j) >> 3) / FB;   // (k within the scale group) / gs
-            const int so = ((r16 >> 2) * 16 + gl) * 16 + (r16 & 3) * 4;
+            const int gl = (32 * j) / a.p.gs;                      // group within the block
+            const int so = ((r16 >> 2) * 4 + gl) * 16 + (r16 & 3) * 4;
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(sc + (4 * wq + 2 * kc + u) * 1024 + so);
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(sc + (4 * wq + 2 * kc + u) * 256 + so);
                 s2[j][u] = bf16_half2(w & 0xFFFFu);
                 b2[j][u] = bf16_half2(w >> 16);
             }
@@ -168,13 +174,15 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
     };
 
     issue(0);
+    if (nb > 1) issue(1);
     for (int blk = 0; blk < nb; blk++) {
-        // this wave's copies of block blk have landed (nothing newer is in flight) ...
-        __builtin_amdgcn_s_waitcnt(0);
-        // ... and every wave's; block blk - 1's stage is no longer read. A bare s_barrier:
-        // __syncthreads' fence adds nothing here.
+        // this wave's copies of block blk have landed (block blk + 1's may still be in flight) ...
+        if (blk + 1 < nb) __builtin_amdgcn_s_waitcnt(PT_WAIT_ONE_AHEAD);
+        else __builtin_amdgcn_s_waitcnt(0);
+        // ... and every wave's; block blk - 1's stage, which block blk + 2 overwrites, is no longer
+        // read. A bare s_barrier: __syncthreads' fence adds nothing here.
         __builtin_amdgcn_s_barrier();
-        compute(blk, blk + 1 < nb ? blk + 1 : -1);
+        compute(blk, blk + 2 < nb ? blk + 2 : -1);
     }
     // lane holds, for token m0 + 16 i + r16, rows 4 kq .. 4 kq + 3 of tile t0 + 4 wq + 2 kc + u
 #pragma unroll
