@@ -9,12 +9,40 @@ namespace mlxr {
 constexpr int DMV_MAX_K = 32768;     // input length of the standalone matvec (max)
 constexpr int DMV_MAX_LDS = 160 * 1024;
 
+// The matvec over the packed input and the epilogue (y = v, y += v, or SiLU(gate) * up).
+template <int FB, int MODE>
+__device__ __forceinline__ void dmv_finish(const MvPhaseDesc& p, const MvLds& L, int wg, int nwg, int wave, int lane,
+                                           Ring<FB>& ring, float unscale, float* __restrict__ y) {
+    mv_run<FB>(p, L.xh, L.gsum, L.zero16, wg, nwg, wave, lane, ring, L.part);
+    lds_barrier();
+    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
+    const int nfw = g.nt * g.NF;
+    if (MODE == OUT_GATED) {
+        for (int i = threadIdx.x; i < g.nt * 8; i += MK_THREADS) {
+            const int tl = i >> 3, j = i & 7, o = 8 * (g.t0 + tl) + j;
+            if (o < p.o1) {
+                const float gv = tile_row(L.part, tl, j, nfw, g.NF) * unscale;
+                const float uv = tile_row(L.part, tl, j + 8, nfw, g.NF) * unscale;
+                y[o] = (gv / (1.0f + expf(-gv))) * uv;
+            }
+        }
+        return;
+    }
+    for (int i = threadIdx.x; i < g.nt * 16; i += MK_THREADS) {
+        const int row = 16 * g.t0 + i;
+        if (row >= p.rows) break;
+        const float v = tile_row(L.part, i >> 4, i & 15, nfw, g.NF) * unscale + row_bias(p, row);
+        if (MODE == OUT_ADD) y[row] += v;
+        else y[row] = v;
+    }
+}
+
 // One projection of the kernel-per-op decode step (the path for steps the persistent kernel does
 // not take: sparse attention, models outside its limits, decode mode 0) over the same repacked
 // tiles: y = W x (+ bias), y += W x, or y = SiLU(W_g x) * (W_u x), x optionally RMSNorm(x) * w.
-// Every workgroup issues its first scale group of weights, then packs x straight from global
-// memory (one pass for the norm statistics and max |x|, one to pack), so large inputs (K up to
-// 32768) fit in LDS without an f32 copy.
+// Every workgroup issues its first scale group of weights (after x when x is held in registers)
+// and packs x straight from global memory (the norm statistics and max |x| first, then the
+// packing), so large inputs (K up to 32768) fit in LDS without an f32 copy.
 template <int FB, int MODE>
 __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, const float* __restrict__ x,
                                                               const float* __restrict__ nw, float eps, float* __restrict__ y, int tpw) {
@@ -30,13 +58,70 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
     float* red = L.part + tpw * MK_WAVES * 16;
     const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     Ring<FB> ring;
-    mv_prefetch<FB>(p, wg, nwg, wave, lane, ring);
-    // statistics: sum of squares of x, max |x w| (max |x| without a norm); four 16-byte loads per
-    // thread in flight (global address space: they cannot alias the LDS writes)
+    // statistics: sum of squares of x, max |x w| (max |x| without a norm). Inputs of up to
+    // 8 * XR * MK_THREADS values are read once, 8-group t = tid + MK_THREADS i into registers, and
+    // packed from there; longer ones are read again to pack, four 16-byte loads per thread in flight
+    // (global address space: they cannot alias the LDS writes).
     typedef float f4v __attribute__((ext_vector_type(4)));
     typedef const __attribute__((address_space(1))) f4v* gf4p;
     auto gf4 = [](const float* p) { const f4v v = *(gf4p)p; return float4{v.x, v.y, v.z, v.w}; };
+    constexpr int XR = 4;
+    const bool inreg = K <= 8 * XR * MK_THREADS;
+    float4 xv[XR][2];
     float ss = 0.0f, mx = 0.0f;
+    if (inreg) {
+        float4 wv[XR][2];
+#pragma unroll
+        for (int i = 0; i < XR; i++) {
+            const int t = threadIdx.x + i * MK_THREADS;
+#pragma unroll
+            for (int c = 0; c < 2; c++) { xv[i][c] = float4{0.0f, 0.0f, 0.0f, 0.0f}; wv[i][c] = float4{1.0f, 1.0f, 1.0f, 1.0f}; }
+            if (8 * t < K) {
+                xv[i][0] = gf4(x + 8 * t); xv[i][1] = gf4(x + 8 * t + 4);
+                if (nw) { wv[i][0] = gf4(nw + 8 * t); wv[i][1] = gf4(nw + 8 * t + 4); }
+            }
+        }
+        // the weights' first scale group after x: the memory counter completes in order, so the
+        // statistics wait for x alone while the weights stream in behind
+        mv_prefetch<FB>(p, wg, nwg, wave, lane, ring);
+#pragma unroll
+        for (int i = 0; i < XR; i++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const float4 v = xv[i][c], w = wv[i][c];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                const float4 a = float4{v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w};
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+            }
+        ss = wave_sum(ss); mx = wave_max(mx);
+        if (lane == 0) { red[wave] = ss; red[8 + wave] = mx; }
+        lds_barrier();
+        float tot = 0.0f, gmax = 0.0f;
+        for (int i = 0; i < MK_WAVES; i++) { tot += red[i]; gmax = fmaxf(gmax, red[8 + i]); }
+        const float inv = nw ? 1.0f / sqrtf(tot / (float)K + eps) : 1.0f;
+        if (nw) {
+#pragma unroll
+            for (int i = 0; i < XR; i++)
+#pragma unroll
+                for (int c = 0; c < 2; c++) {
+                    float4& v = xv[i][c];
+                    const float4 w = wv[i][c];
+                    v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
+                }
+        }
+        // pack_x16_from visits t = tid + MK_THREADS i in order of i
+        auto ld = [&](int t, float4& lo, float4& hi) {
+            const int i = (t - (int)threadIdx.x) / MK_THREADS;
+            lo = xv[0][0]; hi = xv[0][1];
+#pragma unroll
+            for (int k = 1; k < XR; k++)
+                if (i == k) { lo = xv[k][0]; hi = xv[k][1]; }
+        };
+        const float unscale = pack_x16_from(ld, K, gmax * inv, L, GSH);
+        dmv_finish<FB, MODE>(p, L, wg, nwg, wave, lane, ring, unscale, y);
+        return;
+    }
+    mv_prefetch<FB>(p, wg, nwg, wave, lane, ring);
     for (int base = threadIdx.x * 4; base < K; base += MK_THREADS * 16) {
         float4 v[4], w[4];
 #pragma unroll
@@ -72,28 +157,7 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
         auto ld = [x, gf4](int t, float4& lo, float4& hi) { lo = gf4(x + 8 * t); hi = gf4(x + 8 * t + 4); };
         unscale = pack_x16_from(ld, K, gmax, L, GSH);
     }
-    mv_run<FB>(p, L.xh, L.gsum, L.zero16, wg, nwg, wave, lane, ring, L.part);
-    lds_barrier();
-    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
-    const int nfw = g.nt * g.NF;
-    if (MODE == OUT_GATED) {
-        for (int i = threadIdx.x; i < g.nt * 8; i += MK_THREADS) {
-            const int tl = i >> 3, j = i & 7, o = 8 * (g.t0 + tl) + j;
-            if (o < p.o1) {
-                const float gv = tile_row(L.part, tl, j, nfw, g.NF) * unscale;
-                const float uv = tile_row(L.part, tl, j + 8, nfw, g.NF) * unscale;
-                y[o] = (gv / (1.0f + expf(-gv))) * uv;
-            }
-        }
-        return;
-    }
-    for (int i = threadIdx.x; i < g.nt * 16; i += MK_THREADS) {
-        const int row = 16 * g.t0 + i;
-        if (row >= p.rows) break;
-        const float v = tile_row(L.part, i >> 4, i & 15, nfw, g.NF) * unscale + row_bias(p, row);
-        if (MODE == OUT_ADD) y[row] += v;
-        else y[row] = v;
-    }
+    dmv_finish<FB, MODE>(p, L, wg, nwg, wave, lane, ring, unscale, y);
 }
 
 template <int FB, int MODE>

@@ -412,6 +412,7 @@ __global__ __launch_bounds__(512, 1) void qgemm4_kernel(QGemm4Dev a) {
 
 hipError_t launch_x_to_f16(const float* x, int xs, int K, int T, uint16_t* out, float* inv, hipStream_t s) {
     if (K % 8 || xs % 4 || T < 1) return hipErrorInvalidValue;
+    if (launch_row_f16(x, xs, K, T, out, inv, s)) return hipGetLastError();
     hipLaunchKernelGGL(x_to_f16_kernel, dim3(T), dim3(256), 0, s, x, xs, K, out, inv);
     return hipGetLastError();
 }

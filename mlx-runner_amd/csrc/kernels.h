@@ -54,6 +54,8 @@ struct QGemmArgs {
 hipError_t launch_qgemm(const QGemmArgs& a, hipStream_t s);
 // The 4-bit GEMM pre-pass: row t of x scaled by the power of two that puts max|x| in [2^13, 2^14),
 // rounded to f16 (each 8-group stored as 0,4,1,5,2,6,3,7), inv[t] = the inverse scale.
+// launch_x_to_f16's single-pass kernel (misc.hip) for K <= 32768; false (nothing launched) above.
+bool launch_row_f16(const float* x, int xs, int K, int T, uint16_t* out, float* inv, hipStream_t s);
 hipError_t launch_x_to_f16(const float* x, int xs, int K, int T, uint16_t* out, float* inv, hipStream_t s);
 
 // Embedding: out[t][k] = dequant(row ids[t]) (ids read from hist + *dpos + t0).

@@ -139,9 +139,121 @@ __global__ __launch_bounds__(256) void rms_norm_f16_kernel(const float* x, const
     }
 }
 
+// Single-pass form of the f16-operand producers above (x_to_f16_kernel in gemm.hip, and
+// rms_norm_f16_kernel with or without the residual add) for rows of up to 2048 NG values: each
+// thread loads its 8-groups g = tid + 256 i (i < NG) once, all loads in flight together, and keeps
+// them in registers through the reductions; the arithmetic per value is the same as those kernels'.
+// MODE 0: y = x; 1: y = RMSNorm(x) * w; 2: h += r, then y = RMSNorm(h) * w.
+template <int NG, int MODE>
+__global__ __launch_bounds__(256) void row_f16_kernel(const float* x, int row_stride, const float* w, int dim, float eps,
+                                                      float* h, const float* r, uint16_t* xh, float* invs) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, ng = dim >> 3, tid = threadIdx.x;
+    const float* xr = (MODE == 2 ? h : x) + (int64_t)row * row_stride;
+    float4 v[NG][2], u[MODE == 2 ? NG : 1][2];
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const int g = tid + 256 * i;
+        v[i][0] = v[i][1] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (g < ng) {
+            v[i][0] = *reinterpret_cast<const float4*>(xr + 8 * g);
+            v[i][1] = *reinterpret_cast<const float4*>(xr + 8 * g + 4);
+            if constexpr (MODE == 2) {
+                const float* rr = r + (int64_t)row * row_stride + 8 * g;
+                u[i][0] = *reinterpret_cast<const float4*>(rr);
+                u[i][1] = *reinterpret_cast<const float4*>(rr + 4);
+            }
+        }
+    }
+    if constexpr (MODE == 2) {
+#pragma unroll
+        for (int i = 0; i < NG; i++) {
+            const int g = tid + 256 * i;
+            if (g >= ng) continue;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                v[i][c].x += u[i][c].x; v[i][c].y += u[i][c].y; v[i][c].z += u[i][c].z; v[i][c].w += u[i][c].w;
+            }
+            float* hr = h + (int64_t)row * row_stride + 8 * g;
+            *reinterpret_cast<float4*>(hr) = v[i][0];
+            *reinterpret_cast<float4*>(hr + 4) = v[i][1];
+        }
+    }
+    if constexpr (MODE != 0) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NG; i++) {
+            const float4 a = v[i][0], b = v[i][1];
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
+        }
+        ss = block_sum_256(ss, red);
+        const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+        for (int i = 0; i < NG; i++) {
+            const int g = tid + 256 * i;
+            if (g >= ng) continue;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const float4 ww = *reinterpret_cast<const float4*>(w + 8 * g + 4 * c);
+                float4& a = v[i][c];
+                a.x = a.x * inv * ww.x; a.y = a.y * inv * ww.y; a.z = a.z * inv * ww.z; a.w = a.w * inv * ww.w;
+            }
+        }
+        __syncthreads();   // red is reused
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NG; i++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const float4 a = v[i][c];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        }
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e2 = 0;
+    if (mx > 0.0f && mx <= 3.0e38f) { frexpf(mx, &e2); e2 = 14 - e2; e2 = e2 < -126 ? -126 : (e2 > 126 ? 126 : e2); }
+    const float sc = ldexpf(1.0f, e2);
+    if (tid == 0) invs[row] = ldexpf(1.0f, -e2);
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const int g = tid + 256 * i;
+        if (g >= ng) continue;
+        const float4 a = v[i][0], b = v[i][1];
+        uint4 q;
+        q.x = (uint32_t)f32_to_f16(a.x * sc) | ((uint32_t)f32_to_f16(b.x * sc) << 16);
+        q.y = (uint32_t)f32_to_f16(a.y * sc) | ((uint32_t)f32_to_f16(b.y * sc) << 16);
+        q.z = (uint32_t)f32_to_f16(a.z * sc) | ((uint32_t)f32_to_f16(b.z * sc) << 16);
+        q.w = (uint32_t)f32_to_f16(a.w * sc) | ((uint32_t)f32_to_f16(b.w * sc) << 16);
+        reinterpret_cast<uint4*>(xh + (int64_t)row * dim)[g] = q;
+    }
+}
+
+template <int MODE>
+static bool row_f16_launch(const float* x, int row_stride, const float* w, int dim, int rows, float eps, float* h,
+                           const float* r, uint16_t* xh, float* inv, hipStream_t s) {
+    const int per = (dim / 8 + 255) / 256;
+#define MLXR_ROW_F16(NG)                                                                                         \
+    hipLaunchKernelGGL((row_f16_kernel<NG, MODE>), dim3(rows), dim3(256), 0, s, x, row_stride, w, dim, eps, h, r, xh, inv)
+    if (per <= 2) MLXR_ROW_F16(2);
+    else if (per <= 4) MLXR_ROW_F16(4);
+    else if (per <= 8) MLXR_ROW_F16(8);
+    else if (per <= 16) MLXR_ROW_F16(16);
+    else return false;
+#undef MLXR_ROW_F16
+    return true;
+}
+
+bool launch_row_f16(const float* x, int xs, int K, int T, uint16_t* out, float* inv, hipStream_t s) {
+    return row_f16_launch<0>(x, xs, nullptr, K, T, 0.0f, nullptr, nullptr, out, inv, s);
+}
+
 hipError_t launch_rms_norm_f16(const float* x, const float* w, int dim, int rows, int row_stride, float eps, uint16_t* xh,
                                float* inv, hipStream_t s) {
     if (dim % 8 || row_stride % 4) return hipErrorInvalidValue;
+    if (row_f16_launch<1>(x, row_stride, w, dim, rows, eps, nullptr, nullptr, xh, inv, s)) return hipGetLastError();
     hipLaunchKernelGGL(rms_norm_f16_kernel, dim3(rows), dim3(256), 0, s, x, w, dim, row_stride, eps, 0, (float*)nullptr,
                        (const float*)nullptr, xh, inv);
     return hipGetLastError();
@@ -149,6 +261,7 @@ hipError_t launch_rms_norm_f16(const float* x, const float* w, int dim, int rows
 hipError_t launch_add_rms_norm_f16(float* h, const float* r, const float* w, int dim, int rows, float eps, uint16_t* xh,
                                    float* inv, hipStream_t s) {
     if (dim % 8) return hipErrorInvalidValue;
+    if (row_f16_launch<2>(h, dim, w, dim, rows, eps, h, r, xh, inv, s)) return hipGetLastError();
     hipLaunchKernelGGL(rms_norm_f16_kernel, dim3(rows), dim3(256), 0, s, (const float*)h, w, dim, dim, eps, 1, h, r, xh, inv);
     return hipGetLastError();
 }

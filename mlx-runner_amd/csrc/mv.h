@@ -108,7 +108,7 @@ __device__ __forceinline__ f16x8_t a_operand(uint32_t w, const DotConsts& k) {
 // LDS layout of the matvec input (f16): chunk c of 32 values at xh + 20 * c (80 bytes), code dword i
 // of the chunk (codes 8i..8i+7, nibble j at bits 4j) matched by the 16-byte slot i holding
 //   (x0, x4), (x1 / 16, x5 / 16), (x2, x6), (x3 / 16, x7 / 16)      (x of codes 8i..8i+7)
-// after a power-of-two scaling of the whole vector; then the chunk's (Cs, Xs) at byte 64. gsum[g]
+// after a power-of-two scaling of the whole vector (bytes 64..79 of a chunk are padding). gsum[g]
 // holds (Cs, Xs) of quantization group g; zero16 is 16 bytes of zeros (the masked B operand).
 constexpr int XH_STRIDE = 20;          // floats per chunk
 
@@ -144,22 +144,15 @@ __device__ __forceinline__ float pack_x16_from(const LD& ld, int K, float gmax, 
         o.w = __builtin_bit_cast(uint32_t, h2_t{h3, h7});
         const int c = t >> 2;
         *reinterpret_cast<uint4*>(xh + c * XH_STRIDE + (t & 3) * 4) = o;
+        // (Cs, Xs) of the quantization group: the 4 (gs 32) or 8 (gs 64) t of a group sit in
+        // consecutive lanes of one wave (K is a multiple of 128, so whole groups are active)
         const float ev = (float)h0 + (float)h4 + (float)h2 + (float)h6;
         const float od = (float)h1 + (float)h5 + (float)h3 + (float)h7;
         float cs = ev + od, xsum = ev + 16.0f * od;
         cs += __shfl_xor(cs, 1, 64); cs += __shfl_xor(cs, 2, 64);
         xsum += __shfl_xor(xsum, 1, 64); xsum += __shfl_xor(xsum, 2, 64);
-        if ((t & 3) == 0) *reinterpret_cast<float2*>(xh + c * XH_STRIDE + 16) = float2{1024.0f * cs, xsum};
-    }
-    lds_barrier();
-    const int cpg = 1 << (gsh - 5);   // chunks per group
-    for (int g = threadIdx.x; g < (K >> gsh); g += MK_THREADS) {
-        float2 s = {0.0f, 0.0f};
-        for (int c = g * cpg; c < (g + 1) * cpg; c++) {
-            const float2 v = *reinterpret_cast<const float2*>(xh + c * XH_STRIDE + 16);
-            s.x += v.x; s.y += v.y;
-        }
-        *reinterpret_cast<float2*>(gsum + 2 * g) = s;
+        if (gsh == 6) { cs += __shfl_xor(cs, 4, 64); xsum += __shfl_xor(xsum, 4, 64); }
+        if ((t & ((1 << (gsh - 3)) - 1)) == 0) *reinterpret_cast<float2*>(gsum + 2 * (t >> (gsh - 3))) = float2{1024.0f * cs, xsum};
     }
     lds_barrier();
     return 1.0f / up;
