@@ -326,11 +326,14 @@ __device__ __forceinline__ void att_load_v(const MegaArgs& a, const LayerDev& ly
     }
 }
 // Chunk 1 (keys n0 + 128 .. n0 + 255) of a range longer than 128 keys, copied by buffer->LDS DMA into
-// kvl right after the q|k|v matvec: K rows [128][256 B], then V rows. Keys at or past nf are clamped
+// kvl right after the q|k|v matvec: K rows [128][256 B] (16-byte piece j of row r stored at piece
+// j ^ (r & 15), so the 16 rows a wave's A-operand load reads together fall in different LDS banks),
+// then V rows. Keys at or past nf are clamped
 // to a final row (replaced or masked by the caller, as for the register chunks). Each wave moves its
 // 16 keys' K and V rows, 4 rows (1 KiB) per instruction. Byte offsets fit 32 bits (checked at setup).
 typedef __attribute__((address_space(3))) void* att_lptr;
-constexpr int ATT_KVL_OFF = 53248;     // byte offset of the staged chunk in the workgroup's LDS
+constexpr int ATT_KVL_OFF = 53248;
+constexpr int ATT_PPS = 260;           // row stride (floats) of the attention phase's probabilities     // byte offset of the staged chunk in the workgroup's LDS
 constexpr int ATT_KVL_BYTES = 65536;
 __device__ __forceinline__ void att_stage1(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
                                            uint8_t* kvl) {
@@ -340,10 +343,10 @@ __device__ __forceinline__ void att_stage1(const MegaArgs& a, const LayerDev& ly
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int j = min(kb + 4 * i + (lane >> 4), nf - 1);
-        const uint32_t off = (uint32_t)((((j >> MLXR_PAGE_SHIFT) == pg0 ? e0 : e1) * a.nKV + kvh) * MLXR_PAGE + (j & (MLXR_PAGE - 1))) * 256u +
-                             16u * (lane & 15);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (att_lptr)(kvl + (16 * wave + 4 * i) * 256), 16, off, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (att_lptr)(kvl + 32768 + (16 * wave + 4 * i) * 256), 16, off, 0, 0, 0);
+        const uint32_t row = (uint32_t)((((j >> MLXR_PAGE_SHIFT) == pg0 ? e0 : e1) * a.nKV + kvh) * MLXR_PAGE + (j & (MLXR_PAGE - 1))) * 256u;
+        const uint32_t pk = (uint32_t)((lane & 15) ^ ((4 * i + (lane >> 4)) & 15));   // LDS row 16 wave + 4 i + (lane >> 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (att_lptr)(kvl + (16 * wave + 4 * i) * 256), 16, row + 16u * pk, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (att_lptr)(kvl + 32768 + (16 * wave + 4 * i) * 256), 16, row + 16u * (lane & 15), 0, 0, 0);
     }
 }
 // Start of the attention phase: chunk 0's K / V into registers and, for a staged range, chunk 1 into
@@ -503,14 +506,18 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
         const int nk = n1 - n0;
         const int prow = (kvh * G) * nsplit;             // partial rows: (head, split)
-        uint16_t* qb = reinterpret_cast<uint16_t*>(lds); // [2][16][128] bf16: q hi / lo
+        // [2][16][128] bf16: q hi / lo; the 16-byte piece j of head row g at piece j ^ g, so the
+        // 16 rows read together by a B-operand load fall in different LDS banks
+        uint16_t* qb = reinterpret_cast<uint16_t*>(lds);
         uint16_t* kn16 = qb + 2 * 16 * 128;              // new key, bf16 [128]
         uint16_t* vn16 = kn16 + 128;                     // new value, bf16 [128]
         float* buf = reinterpret_cast<float*>(vn16 + 128);   // 4 x 128 rope scratch
         float* wred = buf + 4 * 128;                     // [2][waves][16] per-wave max, sum
         float* mls = wred + 2 * MK_WAVES * 16;           // [2][16] running max, sum per head
-        float* pp = mls + 32;                            // [MAXG][256] probabilities of the pass's keys
-        float* wacc = pp + MAXG * 256;                   // [waves][MAXG][128] P.V partials; merge scratch
+        // [MAXG][ATT_PPS] probabilities of the pass's 256 keys (rows padded so that the 16 heads'
+        // 16-byte stores of one key quad fall in different LDS banks)
+        float* pp = mls + 32;
+        float* wacc = pp + MAXG * ATT_PPS;               // [waves][MAXG][128] P.V partials; merge scratch
         float* mrow = wacc + MK_WAVES * MAXG * 128;      // [MAXG] merge scale
         {
             const bool owns_new = pos >= n0 && pos < n1;
@@ -529,8 +536,9 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 if (g < G) {
                     const float q = o * a.scale;
                     const uint16_t hi = f32_to_bf16(q);
-                    qb[g * 128 + i] = hi;
-                    qb[2048 + g * 128 + i] = f32_to_bf16(q - bf16_to_f32(hi));
+                    const int si = g * 128 + (((i >> 3) ^ g) << 3) + (i & 7);
+                    qb[si] = hi;
+                    qb[2048 + si] = f32_to_bf16(q - bf16_to_f32(hi));
                 }
             }
             for (int e = tid; e < 2 * (16 - G) * 128; e += MK_THREADS) {   // unused head columns: zero
@@ -575,7 +583,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 for (int db = 0; db < 4; db++)
 #pragma unroll
                     for (int hl = 0; hl < 2; hl++) {
-                        const uint4 bq = *reinterpret_cast<const uint4*>(qb + hl * 2048 + hh * 128 + 32 * db + 8 * (lane >> 4));
+                        const uint4 bq = *reinterpret_cast<const uint4*>(qb + hl * 2048 + hh * 128 + 8 * ((4 * db + (lane >> 4)) ^ hh));
                         sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kq[db]), __builtin_bit_cast(bf16x8_t, bq), sacc, 0, 0, 0);
                     }
                 if (pair) {
@@ -585,11 +593,12 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
 #pragma unroll
                     for (int db = 0; db < 4; db++) {
                         const uint16_t* src = newk ? kn16 + 32 * db + 8 * (lane >> 4)
-                                                   : reinterpret_cast<const uint16_t*>(kvl + (16 * wave + (lane & 15)) * 256) + 32 * db + 8 * (lane >> 4);
+                                                   : reinterpret_cast<const uint16_t*>(kvl + (16 * wave + (lane & 15)) * 256) +
+                                                         8 * ((4 * db + (lane >> 4)) ^ (lane & 15));
                         const uint4 k1 = *reinterpret_cast<const uint4*>(src);
 #pragma unroll
                         for (int hl = 0; hl < 2; hl++) {
-                            const uint4 bq = *reinterpret_cast<const uint4*>(qb + hl * 2048 + hh * 128 + 32 * db + 8 * (lane >> 4));
+                            const uint4 bq = *reinterpret_cast<const uint4*>(qb + hl * 2048 + hh * 128 + 8 * ((4 * db + (lane >> 4)) ^ hh));
                             sacc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, k1), __builtin_bit_cast(bf16x8_t, bq), sacc1, 0, 0, 0);
                         }
                     }
@@ -612,19 +621,24 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 const float4 wb = *reinterpret_cast<const float4*>(wred + hh * MK_WAVES + 4);
                 const float mnew_h = fmaxf(mls[hh], fmaxf(fmaxf(fmaxf(wa.x, wa.y), fmaxf(wa.z, wa.w)), fmaxf(fmaxf(wb.x, wb.y), fmaxf(wb.z, wb.w))));
                 float lsum = 0.0f;
+                float pq[4];
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float p = expf(sv[r] - mnew_h);
-                    lsum += p;
-                    if (hh < MAXG) pp[hh * 256 + 16 * wave + 4 * (lane >> 4) + r] = hh < G ? p : 0.0f;
+                    pq[r] = expf(sv[r] - mnew_h);
+                    lsum += pq[r];
                 }
+                if (hh < MAXG)
+                    *reinterpret_cast<float4*>(pp + hh * ATT_PPS + 16 * wave + 4 * (lane >> 4)) =
+                        hh < G ? float4{pq[0], pq[1], pq[2], pq[3]} : float4{0.0f, 0.0f, 0.0f, 0.0f};
                 if (pair) {
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        const float p = expf(sv1[r] - mnew_h);
-                        lsum += p;
-                        if (hh < MAXG) pp[hh * 256 + 128 + 16 * wave + 4 * (lane >> 4) + r] = hh < G ? p : 0.0f;
+                        pq[r] = expf(sv1[r] - mnew_h);
+                        lsum += pq[r];
                     }
+                    if (hh < MAXG)
+                        *reinterpret_cast<float4*>(pp + hh * ATT_PPS + 128 + 16 * wave + 4 * (lane >> 4)) =
+                            hh < G ? float4{pq[0], pq[1], pq[2], pq[3]} : float4{0.0f, 0.0f, 0.0f, 0.0f};
                 }
                 lsum = xor32_sum(xor16_sum(lsum));
                 if (lane < 16) wred[MK_WAVES * 16 + lane * MK_WAVES + wave] = lsum;
@@ -658,7 +672,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     // keys 8 slice + 4 half .. +4 of the chunk (probabilities of masked keys are 0)
                     float4 pr[MAXG];
 #pragma unroll
-                    for (int g = 0; g < MAXG; g++) pr[g] = *reinterpret_cast<const float4*>(pp + g * 256 + 8 * slice + 4 * half);
+                    for (int g = 0; g < MAXG; g++) pr[g] = *reinterpret_cast<const float4*>(pp + g * ATT_PPS + 8 * slice + 4 * half);
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         const int r = 4 * half + q, j = n0 + 128 * c + 8 * slice + r;
@@ -679,7 +693,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     for (int half = 0; half < 2; half++) {
                         float4 pr[MAXG];
 #pragma unroll
-                        for (int g = 0; g < MAXG; g++) pr[g] = *reinterpret_cast<const float4*>(pp + g * 256 + 128 + 8 * slice + 4 * half);
+                        for (int g = 0; g < MAXG; g++) pr[g] = *reinterpret_cast<const float4*>(pp + g * ATT_PPS + 128 + 8 * slice + 4 * half);
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             const int r = 4 * half + q, j = n0 + 128 + 8 * slice + r;
@@ -915,7 +929,7 @@ size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split) {
     const size_t kmax = (size_t)std::max(a.H, std::max(a.I, a.nH * 128));
     size_t mv = (kmax + kmax / 32 * (XH_STRIDE + 2) + 4 + MK_HOWN + MK_TPW * MK_WAVES * 16) * 4;
     // attention: q hi/lo image, new k/v, rope scratch, exchanges, probabilities, P.V partials, merge scale
-    size_t att = 2 * 16 * 128 * 2 + 2 * 128 * 2 + (size_t)(4 * 128 + 2 * MK_WAVES * 16 + 32 + MK_MAXG * 256 +
+    size_t att = 2 * 16 * 128 * 2 + 2 * 128 * 2 + (size_t)(4 * 128 + 2 * MK_WAVES * 16 + 32 + MK_MAXG * ATT_PPS +
                  MK_WAVES * MK_MAXG * 128 + MK_MAXG) * 4;
     if (att > (size_t)ATT_KVL_OFF || (size_t)(MK_TPW * MK_WAVES * 16 + MK_HOWN) * 4 > (size_t)ATT_KVL_OFF) return (size_t)-1;
     if (a.kv_stage) att = ATT_KVL_OFF + ATT_KVL_BYTES;   // the staged second chunk of keys
