@@ -329,7 +329,8 @@ __device__ __forceinline__ void att_load_v(const MegaArgs& a, const LayerDev& ly
 // kvl right after the q|k|v matvec: K rows [128][256 B] (16-byte piece j of row r stored at piece
 // j ^ (r & 15), so the 16 rows a wave's A-operand load reads together fall in different LDS banks),
 // then V rows. Keys at or past nf are clamped
-// to a final row (replaced or masked by the caller, as for the register chunks). Each wave moves its
+// to a final row, and groups of 4 rows that start at or past nf are not copied (the caller replaces
+// the new key and reads no row past the range). Each wave moves its
 // 16 keys' K and V rows, 4 rows (1 KiB) per instruction. Byte offsets fit 32 bits (checked at setup).
 typedef __attribute__((address_space(3))) void* att_lptr;
 constexpr int ATT_KVL_OFF = 53248;
@@ -342,6 +343,7 @@ __device__ __forceinline__ void att_stage1(const MegaArgs& a, const LayerDev& ly
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(ly.vc, 0, 0x7fffffff, 0x00020000);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
+        if (kb + 4 * i >= nf) break;   // rows of keys past the cache's final ones are never read
         const int j = min(kb + 4 * i + (lane >> 4), nf - 1);
         const uint32_t row = (uint32_t)((((j >> MLXR_PAGE_SHIFT) == pg0 ? e0 : e1) * a.nKV + kvh) * MLXR_PAGE + (j & (MLXR_PAGE - 1))) * 256u;
         const uint32_t pk = (uint32_t)((lane & 15) ^ ((4 * i + (lane >> 4)) & 15));   // LDS row 16 wave + 4 i + (lane >> 4)
@@ -591,7 +593,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     __builtin_amdgcn_s_barrier();
                     const bool newk = owns_new && kbase + 128 + (lane & 15) == pos;
 #pragma unroll
-                    for (int db = 0; db < 4; db++) {
+                    for (int db = 0; db < 4 && kbase + 128 < n1; db++) {   // none of the wave's keys in range: masked anyway
                         const uint16_t* src = newk ? kn16 + 32 * db + 8 * (lane >> 4)
                                                    : reinterpret_cast<const uint16_t*>(kvl + (16 * wave + (lane & 15)) * 256) +
                                                          8 * ((4 * db + (lane >> 4)) ^ (lane & 15));
@@ -688,7 +690,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                         }
                     }
                 }
-                if (pair) {
+                if (pair && n0 + 128 + 16 * wave < n1) {   // the wave's 16 keys of chunk 1 (rows past n1 are not staged)
 #pragma unroll
                     for (int half = 0; half < 2; half++) {
                         float4 pr[MAXG];
@@ -697,6 +699,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             const int r = 4 * half + q, j = n0 + 128 + 8 * slice + r;
+                            if (j >= n1) continue;
                             const uint16_t* src = owns_new && j == pos ? vn16 + 4 * d4
                                                                        : reinterpret_cast<const uint16_t*>(kvl + 32768 + (8 * slice + r) * 256) + 4 * d4;
                             const uint2 vv = *reinterpret_cast<const uint2*>(src);
