@@ -18,6 +18,18 @@ __device__ __host__ __forceinline__ uint16_t f32_to_bf16(float f) {
     b += 0x7fffu + ((b >> 16) & 1u);
     return (uint16_t)(b >> 16);
 }
+// Global-memory access through a global-address-space pointer. A plain (generic) pointer makes a
+// flat access, which also counts in the LDS counter: every later wait for LDS traffic (each
+// barrier) would then wait for that memory round trip as well.
+template <typename T>
+__device__ __forceinline__ T gload(const T* p) { return *(const __attribute__((address_space(1))) T*)p; }
+template <typename T>
+__device__ __forceinline__ void gstore(T* p, T v) { *(__attribute__((address_space(1))) T*)p = v; }
+__device__ __forceinline__ float4 gload4(const float* p) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v v = gload(reinterpret_cast<const f4v*>(p));
+    return float4{v.x, v.y, v.z, v.w};
+}
 __device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 __device__ __forceinline__ float f16_to_f32(uint16_t u) {
     _Float16 h; __builtin_memcpy(&h, &u, 2); return (float)h;

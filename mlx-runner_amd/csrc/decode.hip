@@ -226,10 +226,26 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 }
 
 
+// A norm's weights as each thread uses them in norm_to_lds (float4 i = threadIdx.x + MK_THREADS j),
+// loaded into registers before the phase's weight prefetch: issued later, they would complete
+// behind it (the memory counter completes in order) and add a round trip after the input arrives.
+constexpr int MK_NWR = 2;             // float4 per thread (norms of up to 4096 values)
+struct NormW { float4 v[MK_NWR]; };
+__device__ __forceinline__ NormW norm_w_load(const float* w, int K) {
+    NormW r;
+#pragma unroll
+    for (int j = 0; j < MK_NWR; j++) {
+        const int i = 4 * (threadIdx.x + MK_THREADS * j);
+        r.v[j] = i < K ? gload4(w + i) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    return r;
+}
+
 // x := RMSNorm(src) * w, packed to the f16 matvec layout (every workgroup computes the same
-// values). Returns the unscale factor of the packing.
-__device__ __forceinline__ float norm_to_lds(const uint2* src, unsigned tag, const TagWait& tw, const float* w, int K, float eps,
-                                            const MvLds& L, int gsh, float* red) {
+// values). Returns the unscale factor of the packing. wr: norm_w_load(w, K) (K <= 4096); longer
+// norms load w here.
+__device__ __forceinline__ float norm_to_lds(const uint2* src, unsigned tag, const TagWait& tw, const float* w, const NormW& wr,
+                                            int K, float eps, const MvLds& L, int gsh, float* red) {
     const float ss = wave_sum(fetch_to_lds(src, K, tag, tw, L.xf).x);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     lds_barrier();
@@ -237,9 +253,13 @@ __device__ __forceinline__ float norm_to_lds(const uint2* src, unsigned tag, con
     for (int i = 0; i < MK_WAVES; i++) tot += red[i];
     const float inv = 1.0f / sqrtf(tot / (float)K + eps);
     float mx = 0.0f;
-    for (int i = threadIdx.x * 4; i < K; i += MK_THREADS * 4) {
+    for (int i = threadIdx.x * 4, j = 0; i < K; i += MK_THREADS * 4, j++) {
         float4 v = *reinterpret_cast<float4*>(L.xf + i);
-        const float4 ww = *reinterpret_cast<const float4*>(w + i);
+        float4 ww = wr.v[0];
+#pragma unroll
+        for (int q = 1; q < MK_NWR; q++)
+            if (j == q) ww = wr.v[q];
+        if (K > 4 * MK_THREADS * MK_NWR) ww = gload4(w + i);
         v.x = v.x * inv * ww.x; v.y = v.y * inv * ww.y; v.z = v.z * inv * ww.z; v.w = v.w * inv * ww.w;
         *reinterpret_cast<float4*>(L.xf + i) = v;
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -265,6 +285,15 @@ __device__ __forceinline__ float copy_to_lds(const uint2* src, unsigned tag, con
 // thread's P.V slice (dims 4 (tid & 31) .. +4 of key 8 (tid >> 5) + r).
 struct KVPrefetch { uint4 k[4]; uint2 v[8]; };
 
+// The thread index, opaque to the compiler: offsets derived from it in the attention phase are
+// recomputed where used instead of being hoisted out of the layer loop and held in scratch memory
+// (a reload from scratch waits, in order, for every load issued before it, such as the K / V rows).
+__device__ __forceinline__ int att_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // Key range of attention item (kvh, split): [n0, n1) of the L = pos + 1 keys.
 __device__ __forceinline__ void att_range(int L, int nsplit, int split, int& n0, int& n1) {
     const int c = (L + nsplit - 1) / nsplit;
@@ -284,7 +313,7 @@ __device__ __forceinline__ void att_prefetch_k(const MegaArgs& a, const int* pt,
         for (int db = 0; db < 4; db++) pf.k[db] = uint4{0u, 0u, 0u, 0u};
         return;
     }
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = att_tid(), lane = t & 63, wave = t >> 6;
     const int kb = n0 + 128 * c + 16 * wave;            // the wave's 16 keys span at most two pages
     const int jf = min(kb, nf - 1), jl = min(kb + 15, nf - 1);
     const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = pt[pg0], e1 = pt[jl >> MLXR_PAGE_SHIFT];
@@ -293,7 +322,7 @@ __device__ __forceinline__ void att_prefetch_k(const MegaArgs& a, const int* pt,
 // K rows of the wave's 16 keys from kb, with the page entries of the first and last already loaded.
 __device__ __forceinline__ void att_load_k(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
                                            KVPrefetch& pf) {
-    const int lane = threadIdx.x & 63;
+    const int lane = att_tid() & 63;
     const int jk = min(kb + (lane & 15), nf - 1);
     const int64_t rk = ((int64_t)(((jk >> MLXR_PAGE_SHIFT) == pg0 ? e0 : e1) * a.nKV + kvh) * MLXR_PAGE + (jk & (MLXR_PAGE - 1))) * 128 +
                        8 * (lane >> 4);
@@ -306,7 +335,7 @@ __device__ __forceinline__ void att_prefetch_v(const MegaArgs& a, const int* pt,
         for (int r = 0; r < 8; r++) pf.v[r] = uint2{0u, 0u};
         return;
     }
-    const int t = threadIdx.x;
+    const int t = att_tid();
     const int kb = n0 + 128 * c + 8 * (t >> 5);          // the thread's 8 keys span at most two pages
     const int jf = min(kb, nf - 1), jl = min(kb + 7, nf - 1);
     const int pg0 = jf >> MLXR_PAGE_SHIFT, e0 = pt[pg0], e1 = pt[jl >> MLXR_PAGE_SHIFT];
@@ -315,7 +344,7 @@ __device__ __forceinline__ void att_prefetch_v(const MegaArgs& a, const int* pt,
 // V slices of the thread's 8 keys from kb, with the page entries of the first and last already loaded.
 __device__ __forceinline__ void att_load_v(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
                                            KVPrefetch& pf) {
-    const int t = threadIdx.x;
+    const int t = att_tid();
 #pragma unroll
     for (int r = 0; r < 8; r++) {
         const int jv = min(kb + r, nf - 1);
@@ -338,7 +367,7 @@ constexpr int ATT_PPS = 260;           // row stride (floats) of the attention p
 constexpr int ATT_KVL_BYTES = 65536;
 __device__ __forceinline__ void att_stage1(const MegaArgs& a, const LayerDev& ly, int kvh, int kb, int nf, int pg0, int e0, int e1,
                                            uint8_t* kvl) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = att_tid() & 63, wave = att_tid() >> 6;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(ly.kc, 0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(ly.vc, 0, 0x7fffffff, 0x00020000);
 #pragma unroll
@@ -362,7 +391,7 @@ __device__ __forceinline__ void att_begin(const MegaArgs& a, const int* pt, cons
         for (int r = 0; r < 8; r++) pf.v[r] = uint2{0u, 0u};
         return;
     }
-    const int t = threadIdx.x, wave = t >> 6;
+    const int t = att_tid(), wave = t >> 6;
     const int kk = n0 + 16 * wave, kv = n0 + 8 * (t >> 5), ks = n0 + 128 + 16 * wave;
     const int pk = min(kk, nf - 1) >> MLXR_PAGE_SHIFT, pv = min(kv, nf - 1) >> MLXR_PAGE_SHIFT, ps = min(ks, nf - 1) >> MLXR_PAGE_SHIFT;
     const int ek0 = pt[pk], ek1 = pt[min(kk + 15, nf - 1) >> MLXR_PAGE_SHIFT];
@@ -457,33 +486,40 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
     LayerDev* ldesc = reinterpret_cast<LayerDev*>(reinterpret_cast<uint8_t*>(lds) + a.desc_lds_off);
     {
         static_assert(sizeof(LayerDev) % 16 == 0, "descriptor copy in 16-byte units");
-        const uint4* src = reinterpret_cast<const uint4*>(a.layers);
-        uint4* dst = reinterpret_cast<uint4*>(ldesc);
+        typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+        const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.layers);
+        u32x4_t* dst = reinterpret_cast<u32x4_t*>(ldesc);
         const int n = a.L * (int)(sizeof(LayerDev) / 16);
-        for (int i = tid; i < n; i += MK_THREADS) dst[i] = src[i];
+        for (int i = tid; i < n; i += MK_THREADS) dst[i] = gload(src + i);
     }
     // the page table too (the attention phase's row lookups must not wait on global traffic either)
     int* lpt = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(lds) + a.pt_lds_off);
-    for (int i = tid; i < a.n_pages; i += MK_THREADS) lpt[i] = a.pt[i];
+    for (int i = tid; i < a.n_pages; i += MK_THREADS) lpt[i] = gload(a.pt + i);
     // RoPE cos / sin of this step's position (the angle of every layer's q and k)
     float2* rope = reinterpret_cast<float2*>(lpt + (a.n_pages + 3) / 4 * 4);
     if (tid < a.rot_dim / 2) {
-        const float ang = (float)pos * a.inv_freq[tid];
+        const float ang = (float)pos * gload(a.inv_freq + tid);
         rope[tid] = float2{cosf(ang), sinf(ang)};
     }
     lds_barrier();
     unsigned epoch = 0;                                   // phase boundaries of this launch (profile marks)
     prof_mark(a.prof, 0);
     prof_mark(a.prof, 2 * epoch); ++epoch;
+    NormW nwr = norm_w_load(ldesc[0].in_norm, H);
     mv_prefetch<FB>(ldesc[0].qkv, wg, nwg, wave, lane, ring);
     prof_mark(a.prof, 2 * epoch - 1);
 
     const int nsplit = nwg / nKV;
     for (int li = 0; li < a.L; li++) {
+        // the step position, opaque per layer: what depends on it (the attention phase's key range,
+        // page and row lookups) is computed in each layer where it is used, not once before the
+        // loop and held (in scratch: there are not enough registers) across every phase
+        int pos_l = pos;
+        asm volatile("" : "+s"(pos_l));
         const LayerDev& ly = ldesc[li];
         // ---- A: q|k|v
         {
-            const float us = norm_to_lds(a.hA, tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), tw, ly.in_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
+            const float us = norm_to_lds(a.hA, tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), tw, ly.in_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 0);
             mv_run<FB>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkvT, tag_of(2 + 5 * li), nullptr, nullptr, red, redi);
@@ -492,14 +528,14 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         // prefetch this workgroup's K/V rows (positions < pos are final)
         const int item = wg;                       // nwg == nKV * nsplit
         const int kvh = item / nsplit, split = item % nsplit;
-        int n0, n1; att_range(L, nsplit, split, n0, n1);
+        int n0, n1; att_range(pos_l + 1, nsplit, split, n0, n1);
         uint8_t* kvl = reinterpret_cast<uint8_t*>(lds) + ATT_KVL_OFF;
         const bool staged = a.kv_stage && n1 - n0 > 128;   // chunk 1 joins chunk 0's pass from LDS
         // the q / k norm weights, loaded before the K / V loads (the memory counter completes in
         // order: a load issued after them could only be used once they are in)
         const int QKV = (nH + 2 * nKV) * D;
-        const float qnw = ly.q_norm ? ly.q_norm[tid & 127] : 1.0f, knw = ly.k_norm ? ly.k_norm[tid & 127] : 1.0f;
-        att_begin(a, lpt, ly, kvh, n0, min(n1, pos), staged, kvl, kvpf);
+        const float qnw = ly.q_norm ? gload(ly.q_norm + (tid & 127)) : 1.0f, knw = ly.k_norm ? gload(ly.k_norm + (tid & 127)) : 1.0f;
+        att_begin(a, lpt, ly, kvh, n0, min(n1, pos_l), staged, kvl, kvpf);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- B: attention for (kvh, split): scores on the matrix cores (K rows from the bf16 cache as
@@ -522,7 +558,8 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         float* wacc = pp + MAXG * ATT_PPS;               // [waves][MAXG][128] P.V partials; merge scratch
         float* mrow = wacc + MK_WAVES * MAXG * 128;      // [MAXG] merge scale
         {
-            const bool owns_new = pos >= n0 && pos < n1;
+            const int tid = att_tid(), lane = tid & 63;
+            const bool owns_new = pos_l >= n0 && pos_l < n1;
             // q heads (4 per pass of 512 threads), then the new k and v if this range holds pos
             const int grp = tid >> 7, i = tid & 127;
             // every value this workgroup needs from q|k|v, loaded at once
@@ -553,8 +590,8 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 if (tid < 128) {
                     const uint16_t kb = f32_to_bf16(ko), vb = f32_to_bf16(vraw);
                     kn16[i] = kb; vn16[i] = vb;
-                    const int64_t row = kv_row(lpt, nKV, kvh, pos) * 128 + i;
-                    ly.kc[row] = kb; ly.vc[row] = vb;
+                    const int64_t row = kv_row(lpt, nKV, kvh, pos_l) * 128 + i;
+                    gstore(ly.kc + row, kb); gstore(ly.vc + row, vb);
                 }
             }
             lds_barrier();
@@ -567,7 +604,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 for (int e = 0; e < 4; e++) acc[g][e] = 0.0f;
             const int hh = lane & 15, d4 = tid & 31, slice = tid >> 5;
             const int nchunks = (nk + 127) >> 7;
-            const int nf = min(n1, pos);
+            const int nf = min(n1, pos_l);
             for (int c = 0; c < nchunks;) {
                 asm volatile("" ::: "memory");   // keeps the q reads in the loop (no registers held across chunks)
                 // a staged range takes chunks 0 and 1 in one pass (chunk 1 from LDS)
@@ -576,7 +613,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 // scores S[key][head] of the wave's 16 keys (and its 16 keys of chunk 1)
                 const int kbase = n0 + 128 * c + 16 * wave;
                 uint4* kq = kvpf.k;
-                if (owns_new && kbase + (lane & 15) == pos) {   // only the owner wrote kn16 / vn16
+                if (owns_new && kbase + (lane & 15) == pos_l) {   // only the owner wrote kn16 / vn16
 #pragma unroll
                     for (int db = 0; db < 4; db++) kq[db] = *reinterpret_cast<const uint4*>(kn16 + 32 * db + 8 * (lane >> 4));
                 }
@@ -591,7 +628,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                 if (pair) {
                     __builtin_amdgcn_s_waitcnt(0x0070);    // this wave's DMA (vmcnt 0), then every wave's
                     __builtin_amdgcn_s_barrier();
-                    const bool newk = owns_new && kbase + 128 + (lane & 15) == pos;
+                    const bool newk = owns_new && kbase + 128 + (lane & 15) == pos_l;
 #pragma unroll
                     for (int db = 0; db < 4 && kbase + 128 < n1; db++) {   // none of the wave's keys in range: masked anyway
                         const uint16_t* src = newk ? kn16 + 32 * db + 8 * (lane >> 4)
@@ -679,7 +716,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     for (int q = 0; q < 4; q++) {
                         const int r = 4 * half + q, j = n0 + 128 * c + 8 * slice + r;
                         uint2 vv = kvpf.v[r];
-                        if (owns_new && j == pos) vv = *reinterpret_cast<const uint2*>(vn16 + 4 * d4);
+                        if (owns_new && j == pos_l) vv = *reinterpret_cast<const uint2*>(vn16 + 4 * d4);
                         const float vf[4] = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
                                              __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
 #pragma unroll
@@ -700,7 +737,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                         for (int q = 0; q < 4; q++) {
                             const int r = 4 * half + q, j = n0 + 128 + 8 * slice + r;
                             if (j >= n1) continue;
-                            const uint16_t* src = owns_new && j == pos ? vn16 + 4 * d4
+                            const uint16_t* src = owns_new && j == pos_l ? vn16 + 4 * d4
                                                                        : reinterpret_cast<const uint16_t*>(kvl + 32768 + (8 * slice + r) * 256) + 4 * d4;
                             const uint2 vv = *reinterpret_cast<const uint2*>(src);
                             const float vf[4] = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
@@ -803,12 +840,13 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.hB, tag_of(4 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
+        nwr = norm_w_load(ly.post_norm, H);
         mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- D: gate|up with SiLU
         {
-            const float us = norm_to_lds(a.hB, tag_of(4 + 5 * li), tw, ly.post_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
+            const float us = norm_to_lds(a.hB, tag_of(4 + 5 * li), tw, ly.post_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 5);
             mv_run<FB>(ly.gu, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_GATED, FB>(ly.gu, us, wg, nwg, ml.part, a.mlpT, tag_of(5 + 5 * li), nullptr, nullptr, red, redi);
@@ -827,13 +865,14 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.hA, tag_of(6 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
+        nwr = norm_w_load(li + 1 < a.L ? ldesc[li + 1].in_norm : a.final_norm, H);
         if (li + 1 < a.L) mv_prefetch<FB>(ldesc[li + 1].qkv, wg, nwg, wave, lane, ring);
         else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
     }
 
     // ---- lm_head with the final norm, logits and the greedy token
-    const float us = norm_to_lds(a.hA, tag_of(6 + 5 * (a.L - 1)), tw, a.final_norm, H, a.eps, ml, FB == 4 ? 5 : 6, red);
+    const float us = norm_to_lds(a.hA, tag_of(6 + 5 * (a.L - 1)), tw, a.final_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
     mv_run<FB>(a.head, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
     const MvResult best = mv_finish<OUT_ARGMAX, FB>(a.head, us, wg, nwg, ml.part, nullptr, 0u, a.logits, nullptr, red, redi);
     prof_mark(a.prof, 2 * epoch);

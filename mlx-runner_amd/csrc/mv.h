@@ -242,7 +242,7 @@ __device__ __forceinline__ float row_bias(const MvPhase& p, int vr) {
     if (!p.bias[0]) return 0.0f;
     int part, row; mv_locate(p, vr, part, row);
     const uint16_t* b = part == 0 ? p.bias[0] : part == 1 ? p.bias[1] : p.bias[2];
-    return bf16_to_f32(b[row]);
+    return bf16_to_f32(gload(b + row));
 }
 
 // Row r of tile tl of this workgroup: the partial sums of the waves whose ranges meet the tile, in
