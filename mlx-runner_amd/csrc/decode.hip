@@ -534,7 +534,11 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         // the q / k norm weights, loaded before the K / V loads (the memory counter completes in
         // order: a load issued after them could only be used once they are in)
         const int QKV = (nH + 2 * nKV) * D;
-        const float qnw = ly.q_norm ? gload(ly.q_norm + (tid & 127)) : 1.0f, knw = ly.k_norm ? gload(ly.k_norm + (tid & 127)) : 1.0f;
+        // (rot_dim 128: lane l's two dims, (l, l + 64) or (2 l, 2 l + 1) traditional; else dim tid & 127)
+        const bool wave_rope = a.rot_dim == 128;
+        const int nd0 = wave_rope ? (a.traditional ? 2 * (tid & 63) : (tid & 63)) : (tid & 127);
+        const int nd1 = a.traditional ? nd0 + 1 : nd0 + 64;
+        const float qnw = ly.q_norm && !wave_rope ? gload(ly.q_norm + nd0) : 1.0f, knw = ly.k_norm && !wave_rope ? gload(ly.k_norm + nd0) : 1.0f;
         att_begin(a, lpt, ly, kvh, n0, min(n1, pos_l), staged, kvl, kvpf);
         prof_mark(a.prof, 2 * epoch - 1);
 
@@ -560,10 +564,52 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         {
             const int tid = att_tid(), lane = tid & 63;
             const bool owns_new = pos_l >= n0 && pos_l < n1;
+            const unsigned qtag = tag_of(2 + 5 * li);
+            if (wave_rope) {
+                // wave w takes item w (q head w < G, the new key at item G if this range holds pos);
+                // a lane's two dims are each other's RoPE partners, so the norm is one wave sum and
+                // the rotation needs no exchange
+                const int wv = tid >> 6;
+                const float2 cs = rope[lane];
+                for (int it = wv; it < G + (owns_new ? 1 : 0); it += MK_WAVES) {
+                    const bool isk = it == G;
+                    const int col = isk ? (nH + kvh) * D : (kvh * G + it) * D;
+                    // the norm weights load with the q / k values: both complete behind this range's
+                    // K / V loads (issued first; the memory counter completes in order)
+                    const float* nwp = isk ? ly.k_norm : ly.q_norm;
+                    const float nw0 = nwp ? gload(nwp + nd0) : 1.0f, nw1 = nwp ? gload(nwp + nd1) : 1.0f;
+                    float v0 = ld_tag1(a.qkvT, col + nd0, QKV, qtag, tw), v1 = ld_tag1(a.qkvT, col + nd1, QKV, qtag, tw);
+                    if (nwp) {
+                        const float r = 1.0f / sqrtf(wave_sum(v0 * v0 + v1 * v1) / 128.0f + a.eps);
+                        v0 = v0 * r * nw0;
+                        v1 = v1 * r * nw1;
+                    }
+                    const float o0 = v0 * cs.x - v1 * cs.y, o1 = v1 * cs.x + v0 * cs.y;
+                    if (isk) {
+                        const int vc = (nH + nKV + kvh) * D;
+                        const uint16_t k0 = f32_to_bf16(o0), k1 = f32_to_bf16(o1);
+                        const uint16_t w0 = f32_to_bf16(ld_tag1(a.qkvT, vc + nd0, QKV, qtag, tw));
+                        const uint16_t w1 = f32_to_bf16(ld_tag1(a.qkvT, vc + nd1, QKV, qtag, tw));
+                        kn16[nd0] = k0; kn16[nd1] = k1; vn16[nd0] = w0; vn16[nd1] = w1;
+                        const int64_t row = kv_row(lpt, nKV, kvh, pos_l) * 128;
+                        gstore(ly.kc + row + nd0, k0); gstore(ly.kc + row + nd1, k1);
+                        gstore(ly.vc + row + nd0, w0); gstore(ly.vc + row + nd1, w1);
+                    } else {
+                        const float q[2] = {o0 * a.scale, o1 * a.scale};
+                        const int dd[2] = {nd0, nd1};
+#pragma unroll
+                        for (int e = 0; e < 2; e++) {
+                            const uint16_t hi = f32_to_bf16(q[e]);
+                            const int si = it * 128 + (((dd[e] >> 3) ^ it) << 3) + (dd[e] & 7);
+                            qb[si] = hi;
+                            qb[2048 + si] = f32_to_bf16(q[e] - bf16_to_f32(hi));
+                        }
+                    }
+                }
+            } else {
             // q heads (4 per pass of 512 threads), then the new k and v if this range holds pos
             const int grp = tid >> 7, i = tid & 127;
             // every value this workgroup needs from q|k|v, loaded at once
-            const unsigned qtag = tag_of(2 + 5 * li);
             const float qv0 = ld_tag1(a.qkvT, (kvh * G + min(grp, G - 1)) * D + i, QKV, qtag, tw);
             const float qv1 = ld_tag1(a.qkvT, (kvh * G + min(grp + 4, G - 1)) * D + i, QKV, qtag, tw);
             const float kraw = ld_tag1(a.qkvT, (nH + kvh) * D + i, QKV, qtag, tw);
@@ -580,11 +626,6 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     qb[2048 + si] = f32_to_bf16(q - bf16_to_f32(hi));
                 }
             }
-            for (int e = tid; e < 2 * (16 - G) * 128; e += MK_THREADS) {   // unused head columns: zero
-                const int hl = e / ((16 - G) * 128), r = e - hl * (16 - G) * 128;
-                qb[hl * 2048 + G * 128 + r] = 0;
-            }
-            if (tid < 32) mls[tid] = tid < 16 ? -1e30f : 0.0f;
             if (owns_new) {
                 const float ko = head_norm_rope(tid < 128 ? kraw : 0.0f, i, ly.k_norm != nullptr, knw, a.eps, rope, a.rot_dim, a.traditional, buf + grp * 128, red, grp);
                 if (tid < 128) {
@@ -594,6 +635,12 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     gstore(ly.kc + row, kb); gstore(ly.vc + row, vb);
                 }
             }
+            }
+            for (int e = tid; e < 2 * (16 - G) * 128; e += MK_THREADS) {   // unused head columns: zero
+                const int hl = e / ((16 - G) * 128), r = e - hl * (16 - G) * 128;
+                qb[hl * 2048 + G * 128 + r] = 0;
+            }
+            if (tid < 32) mls[tid] = tid < 16 ? -1e30f : 0.0f;
             lds_barrier();
             prof_mark(a.prof, 512 + 8 * li + 7);
 
