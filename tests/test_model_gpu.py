@@ -36,6 +36,9 @@ def models():
         "qwen3_3bit": configs.tiny("qwen3", bits=3, gs=32, layers=1),
         # hidden 1024 at gs 32: wider rows (two scale groups per 16-row tile)
         "qwen3_h1024": configs.tiny("qwen3", hidden=1024, inter=1024, gs=32),
+        # RoPE variants: interleaved pairs, and half the head dims rotated
+        "qwen3_rope_trad": dict(configs.tiny("qwen3"), rope_traditional=True),
+        "qwen3_rope_half": dict(configs.tiny("qwen3"), partial_rotary_factor=0.5),
     }.items():
         d = os.path.join(tmp, name)
         mlxr.synth_write(cfg, seed=1234, directory=d)
@@ -116,6 +119,25 @@ def test_persistent_decode_matches_kernel_per_op(gpu, models, name):
             i = next(k for k in range(len(a)) if a[k] != b[k])
             logits = ref.forward(np.concatenate([toks, np.array(a[:i], np.int32)]), 0)
             assert abs(logits[a[i]] - logits[b[i]]) < LOGIT_TOL
+
+
+@pytest.mark.parametrize("name", ["qwen3_rope_trad", "qwen3_rope_half"])
+def test_persistent_decode_rope_variants(gpu, models, name):
+    """Interleaved (traditional) RoPE and partial rotation (rot_dim 64) in the persistent step, whose
+    q/k norm + RoPE takes a different path for each, against the kernel-per-op step's qkv_post
+    (checked against the oracle's RoPE in test_qkv_post): same greedy tokens, or, where they part,
+    the two tokens' logits (full prefill of the shared prefix) within the 2e-2 gate."""
+    d = models[name]
+    toks = prompt(40, 1000, seed=21)
+    with mlxr.Transformer(d, context_length=512) as m:
+        assert m.persistent_decode
+        a = m.generate(toks, 16, GREEDY)
+        m.set_decode_mode(0)
+        b = m.generate(toks, 16, GREEDY)
+        if a != b:
+            i = next(k for k in range(len(a)) if a[k] != b[k])
+            logits = m.forward(np.concatenate([toks, np.array(a[:i], np.int32)]), 0)
+            assert abs(logits[a[i]] - logits[b[i]]) < LOGIT_TOL, (name, i)
 
 
 def test_persistent_decode_long_ranges(gpu, models):
