@@ -521,7 +521,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         {
             const float us = norm_to_lds(a.hA, tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), tw, ly.in_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 0);
-            mv_run<FB>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_run<FB, true>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkvT, tag_of(2 + 5 * li), nullptr, nullptr, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
@@ -883,7 +883,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const float us = copy_to_lds(a.attnT, tag_of(3 + 5 * li), tw, nH * D, ml, FB == 4 ? 5 : 6, a.hA,
                                          tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), H, 16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 4);
-            mv_run<FB>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_run<FB, true>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.hB, tag_of(4 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
@@ -895,7 +895,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         {
             const float us = norm_to_lds(a.hB, tag_of(4 + 5 * li), tw, ly.post_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 5);
-            mv_run<FB>(ly.gu, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_run<FB, true>(ly.gu, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_GATED, FB>(ly.gu, us, wg, nwg, ml.part, a.mlpT, tag_of(5 + 5 * li), nullptr, nullptr, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
@@ -908,7 +908,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const float us = copy_to_lds(a.mlpT, tag_of(5 + 5 * li), tw, a.I, ml, FB == 4 ? 5 : 6, a.hB, tag_of(4 + 5 * li), H,
                                          16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 6);
-            mv_run<FB>(ly.down, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_run<FB, true>(ly.down, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.hA, tag_of(6 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
@@ -920,7 +920,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
 
     // ---- lm_head with the final norm, logits and the greedy token
     const float us = norm_to_lds(a.hA, tag_of(6 + 5 * (a.L - 1)), tw, a.final_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
-    mv_run<FB>(a.head, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+    mv_run<FB, true>(a.head, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
     const MvResult best = mv_finish<OUT_ARGMAX, FB>(a.head, us, wg, nwg, ml.part, nullptr, 0u, a.logits, nullptr, red, redi);
     prof_mark(a.prof, 2 * epoch);
     __shared__ float bv[MK_WAVES];

@@ -1,6 +1,7 @@
 // Matvec building blocks over the repacked weight tiles (DPack), shared by the persistent decode
 // step (decode.hip) and the standalone per-projection matvec (dmv.hip).
 #pragma once
+#include <type_traits>
 #include "decode.h"
 
 namespace mlxr {
@@ -168,7 +169,7 @@ __device__ __forceinline__ float pack_x16(const float* xf, int K, float gmax, co
 
 // Streams the wave's scale groups (the first already in the ring), leaving per-tile partial row
 // sums in part[(tile * MK_WAVES + wave) * 16 + row] (LDS) for mv_finish.
-template <int FB>
+template <int FB, bool STRAIGHT = false>
 __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const float* gsum, const float* zero16, int wg, int nwg,
                                        int wave, int lane, Ring<FB>& ring, float* part) {
     constexpr int GSH = FB == 4 ? 5 : 6;          // log2 of the group size
@@ -190,21 +191,43 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
         const float* xb = xh + (lane >> 4) * 4 + f * (4 * FB) * XH_STRIDE;   // this lane's slot of the group's first chunk
         // two accumulators (even / odd chunks): half the dependent MFMA chain
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+        // one scale group: straight-line code when the reloads' condition is taken outside it
+        // (STRAIGHT), so the compiler issues the B-operand LDS reads ahead of the MFMAs that use
+        // them; with the condition inside, each slot's reload follows its MFMAs directly, which
+        // keeps a long stream of groups fed (the standalone matvec)
+        auto group = [&](auto reload) {
 #pragma unroll
-        for (int k = 0; k < FB; k++) {
-            const uint4 unit = ring.u[k + 1];
-            const uint32_t wd[4] = {unit.x, unit.y, unit.z, unit.w};
+            for (int k = 0; k < FB; k++) {
+                const uint4 unit = ring.u[k + 1];
+                const uint32_t wd[4] = {unit.x, unit.y, unit.z, unit.w};
+                f16x8_t b[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                constexpr int CPG = 1 << (GSH - 5);                       // chunks per group
-                const int gcol = (4 * k + j) / CPG;                        // the chunk's group column
-                const float* bp = col == gcol ? xb + (4 * k + j) * XH_STRIDE : zero16;
-                const f16x8_t b = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(bp));
-                if (j & 1) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b, acc2, 0, 0, 0);
-                else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b, acc, 0, 0, 0);
+                for (int j = 0; j < 4; j++) {
+                    constexpr int CPG = 1 << (GSH - 5);                       // chunks per group
+                    const int gcol = (4 * k + j) / CPG;                        // the chunk's group column
+                    const float* bp = col == gcol ? xb + (4 * k + j) * XH_STRIDE : zero16;
+                    b[j] = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(bp));
+                    if constexpr (!STRAIGHT) {   // each operand read right before its MFMA
+                        if (j & 1) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b[j], acc2, 0, 0, 0);
+                        else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b[j], acc, 0, 0, 0);
+                    }
+                }
+                if constexpr (STRAIGHT) {        // the four reads first, then the four MFMAs
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        if (j & 1) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b[j], acc2, 0, 0, 0);
+                        else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b[j], acc, 0, 0, 0);
+                    }
+                }
+                if constexpr (!STRAIGHT) {
+                    if (more) ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
+                } else if constexpr (decltype(reload)::value) {
+                    ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
+                }
             }
-            if (more) ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
-        }
+        };
+        if (!STRAIGHT || more) group(std::true_type{});
+        else group(std::false_type{});
         // scales of the 16 groups (groups past the row's last are zero-scaled; their sums may be junk)
         const int gi = 16 * f + col;
         const bool real = gi < gpr;
