@@ -327,8 +327,64 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
     }
 }
 
+// The same for D = rot_dim = 128, one wave per (head, token) and no workgroup barrier: lane l holds
+// dims (l, l + 64), or (2 l, 2 l + 1) for traditional RoPE, which are each other's rotation
+// partners (angle index l for both), so the norm is one wave sum and the rotation needs no exchange.
+__global__ __launch_bounds__(256) void qkv_post_wave_kernel(QkvPostArgs a) {
+    const int NHT = a.nH + 2 * a.nKV;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (item >= NHT * a.T) return;
+    const int h = item % NHT, t = item / NHT;
+    const int d0 = a.traditional ? 2 * l : l, d1 = a.traditional ? 2 * l + 1 : l + 64;
+    float* base = a.qkv + (int64_t)t * a.row_stride + (int64_t)h * 128;
+    const int pos = *a.dpos + a.pos_add + t;
+    float v0 = base[d0], v1 = base[d1];
+    if (h >= a.nH + a.nKV) {   // value head: straight to the cache
+        const int64_t row = kv_row(a.pt, a.nKV, h - a.nH - a.nKV, pos) * 128;
+        a.vc[row + d0] = f32_to_bf16(v0);
+        a.vc[row + d1] = f32_to_bf16(v1);
+        return;
+    }
+    const bool isQ = h < a.nH;
+    const float* nw = isQ ? a.qn : a.kn;
+    if (nw) {
+        const float r = 1.0f / sqrtf(wave_sum(v0 * v0 + v1 * v1) / 128.0f + a.eps);
+        v0 = v0 * r * nw[d0];
+        v1 = v1 * r * nw[d1];
+    }
+    const float ang = (float)pos * a.inv_freq[l];
+    const float c = cosf(ang), sn = sinf(ang);
+    const float o0 = v0 * c - v1 * sn, o1 = v1 * c + v0 * sn;
+    if (isQ) { base[d0] = o0; base[d1] = o1; return; }
+    const int kvh = h - a.nH;
+    const int64_t row = kv_row(a.pt, a.nKV, kvh, pos) * 128;
+    const uint16_t k0 = f32_to_bf16(o0), k1 = f32_to_bf16(o1);
+    a.kc[row + d0] = k0;
+    a.kc[row + d1] = k1;
+    if (a.idx && a.T == 1 && (pos & 3) == 3) {
+        // the block of keys pos - 3 .. pos is complete: its index row is the bf16 mean of the four
+        // keys, summed in position order as sparse_index_kernel does
+        float s0 = 0.0f, s1 = 0.0f;
+        for (int j = pos - 3; j < pos; j++) {
+            const int64_t rj = kv_row(a.pt, a.nKV, kvh, j) * 128;
+            s0 += bf16_to_f32(a.kc[rj + d0]);
+            s1 += bf16_to_f32(a.kc[rj + d1]);
+        }
+        s0 += bf16_to_f32(k0);
+        s1 += bf16_to_f32(k1);
+        uint16_t* ir = a.idx + ((int64_t)(pos >> 2) * a.nKV + kvh) * 128;
+        ir[d0] = f32_to_bf16(s0 / 4.0f);
+        ir[d1] = f32_to_bf16(s1 / 4.0f);
+    }
+}
+
 hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(qkv_post_kernel, dim3(a.nH + 2 * a.nKV, a.T), dim3(a.D), 0, s, a);
+    if (a.D == 128 && a.rot_dim == 128) {
+        const int items = (a.nH + 2 * a.nKV) * a.T;
+        hipLaunchKernelGGL(qkv_post_wave_kernel, dim3((items + 3) / 4), dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(qkv_post_kernel, dim3(a.nH + 2 * a.nKV, a.T), dim3(a.D), 0, s, a);
+    }
     return hipGetLastError();
 }
 

@@ -313,13 +313,16 @@ def from_paged(c, nKV, D, page=64):
     return np.ascontiguousarray(c.reshape(pages, nKV, page, D).transpose(1, 0, 2, 3).reshape(nKV, pages * page, D))
 
 
-@pytest.mark.parametrize("qk_norm,traditional", [(True, False), (False, False), (True, True)])
-def test_qkv_post(gpu, qk_norm, traditional):
+@pytest.mark.parametrize("qk_norm,traditional,rot", [(True, False, 128), (False, False, 128), (True, True, 128),
+                                                    (True, False, 64)])
+def test_qkv_post(gpu, qk_norm, traditional, rot):
+    """q/k norm + RoPE + K/V append against the oracle: full rotation (one wave per head) and
+    partial rotation (rot_dim 64: the workgroup-per-head kernel)."""
     nH, nKV, D, S, T, off = 4, 2, 128, 128, 5, 37
     rng = np.random.default_rng(7)
     cols = (nH + 2 * nKV) * D
     qkv = rng.normal(0, 1, (T, cols)).astype(np.float32)
-    invf = oracle.inv_freq(1e6, D)
+    invf = oracle.inv_freq(1e6, rot)
     qn = rng.uniform(0.5, 1.5, D).astype(np.float32) if qk_norm else None
     kn = rng.uniform(0.5, 1.5, D).astype(np.float32) if qk_norm else None
     dq = gpu.DeviceArray.from_numpy(qkv)
@@ -329,7 +332,7 @@ def test_qkv_post(gpu, qk_norm, traditional):
     dqn = gpu.DeviceArray.from_numpy(qn) if qk_norm else None
     dkn = gpu.DeviceArray.from_numpy(kn) if qk_norm else None
     gpu.check(gpu.lib.mlxr_k_qkv_post(dq.ptr, cols, di.ptr, dk.ptr, dv.ptr, S, dqn.ptr if dqn else None, dkn.ptr if dkn else None,
-                                      D, nH, nKV, D, int(traditional), off, T, 1e-6))
+                                      D, nH, nKV, rot, int(traditional), off, T, 1e-6))
     gpu.synchronize()
     got_q = dq.numpy()
     kc = bf16_to_f32(from_paged(dk.numpy(), nKV, D))
@@ -340,7 +343,7 @@ def test_qkv_post(gpu, qk_norm, traditional):
             v = qkv[t, h * D:(h + 1) * D]
             if qk_norm:
                 v = oracle.rms_norm(v[None], qn if h < nH else kn, 1e-6)[0]
-            ref = oracle.rope(v, pos, invf, traditional=traditional)
+            ref = oracle.rope(v, pos, invf, rot_dim=rot, traditional=traditional)
             if h < nH:
                 assert np.max(np.abs(got_q[t, h * D:(h + 1) * D] - ref)) < 2e-5
             else:
