@@ -531,10 +531,12 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         int n0, n1; att_range(pos_l + 1, nsplit, split, n0, n1);
         uint8_t* kvl = reinterpret_cast<uint8_t*>(lds) + ATT_KVL_OFF;
         const bool staged = a.kv_stage && n1 - n0 > 128;   // chunk 1 joins chunk 0's pass from LDS
-        // the q / k norm weights, loaded before the K / V loads (the memory counter completes in
-        // order: a load issued after them could only be used once they are in)
         const int QKV = (nH + 2 * nKV) * D;
-        // (rot_dim 128: lane l's two dims, (l, l + 64) or (2 l, 2 l + 1) traditional; else dim tid & 127)
+        // q / k norm + RoPE: with rot_dim 128 wave-local (lane l holds dims nd0, nd1 = (l, l + 64), or
+        // (2 l, 2 l + 1) traditional; their norm weights load later, with the q / k values); else
+        // one dim per thread (tid & 127), whose norm weights load here, before the K / V loads (the
+        // memory counter completes in order: a load issued after them could only be used once
+        // they are in)
         const bool wave_rope = a.rot_dim == 128;
         const int nd0 = wave_rope ? (a.traditional ? 2 * (tid & 63) : (tid & 63)) : (tid & 127);
         const int nd1 = a.traditional ? nd0 + 1 : nd0 + 64;
