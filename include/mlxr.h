@@ -142,6 +142,11 @@ int mlxr_synth_write(const char* config_json, uint64_t seed, float std, const ch
  * scale = (max-min)/(2^bits-1), bias = min, both rounded to bf16; codes packed little-endian). */
 int mlxr_quantize_row(const float* w, int K, int bits, int group_size, uint8_t* codes, uint16_t* scales_bf16,
                       uint16_t* biases_bf16);
+/* One seeded synthetic matrix [O][K], drawn and quantized exactly as mlxr_synth_write draws tensor
+ * number `tensor_id`: codes [O][K*bits/8], bf16 scales / biases [O][K/group_size] (host buffers).
+ * Test and benchmark fixtures at real model shapes; no counterpart in the reference. */
+int mlxr_synth_matrix(uint64_t seed, uint64_t tensor_id, int O, int K, int bits, int group_size, float std,
+                      uint8_t* codes, uint16_t* scales_bf16, uint16_t* biases_bf16);
 
 /* ---------------------------------------------------------------- device helpers */
 int mlxr_device_count(void);

@@ -407,7 +407,7 @@ static int mega_setup(Model* m) {
     const size_t lds = mega_lds_bytes(a, max_keys);
     a.desc_lds_off = (int)mega_desc_offset(a);
     a.pt_lds_off = a.desc_lds_off + (int)(sizeof(LayerDev) * c.L);
-    if (lds > 150 * 1024) return no("LDS need " + std::to_string(lds >> 10) + " KiB");
+    if (lds > 158 * 1024) return no("LDS need " + std::to_string(lds >> 10) + " KiB");
     if (mega_set_lds_limit(lds) != hipSuccess) return no("LDS attribute");
     if (nwg > MEGA_MAX_WG) return no("too many workgroups");
     // the layers' repacked phases (tiles_setup), plus the lm_head's

@@ -8,7 +8,7 @@ namespace mlxr {
 
 constexpr int MK_THREADS = 512;
 constexpr int MK_WAVES = MK_THREADS / 64;
-constexpr int MK_TPW = 64;           // 16-row tiles of one workgroup in a matvec phase (max)
+constexpr int MK_TPW = 40;           // 16-row tiles of one workgroup in a matvec phase (max; a 152K vocab over 256 CUs needs 38)
 
 // ------------------------------------------------------------------------------- matvec phase
 // Weights of the persistent step are a repacked copy (DPack, built once at load by dpack_kernel).
@@ -23,13 +23,17 @@ constexpr int MK_TPW = 64;           // 16-row tiles of one workgroup in a matve
 // A wave streams whole scale groups, so its loads walk one contiguous range and every ring slot
 // has a fixed role (slot 0: scales, slot k: code block k - 1).
 //
-// MFMA formulation: a nibble masked into the mantissa of the f16 1024.0 is the half 1024 + q (the
-// nibble at bits 4..7 gives 1024 + 16 q, met by x / 16 in the operand), so A is built with one
-// AND-OR per two codes. B is the chunk's x (f16) in the column of the chunk's group and zero in the
-// other 15, so the accumulator holds per-(row, group) sums sum (1024 + q) x = 1024 X'_g + sum q x
-// for 16 groups at once; the scale and bias are applied once per scale group:
-//   y_row += s_rg (D_rg - Cs_g) + b_rg Xs_g,   Cs_g = 1024 * sum of the group's stored halves.
-// Products of halves are exact and accumulate in fp32.
+// MFMA formulation: a code masked into the low mantissa bits of an f16 with a zero exponent is the
+// subnormal q * 2^-24 (the nibble at bits 4..7 gives 16 q * 2^-24, met by x / 16 in the operand), so
+// A is built with one AND per two codes and carries the codes exactly, with no offset. The input
+// enters as two f16 parts, x = hi + lo (lo = f16(x - hi): ~22 significant bits, fp32 accuracy for
+// the matvec). B holds the chunk's hi in the column of the chunk's group g and its lo in column
+// g ^ 8, zeros elsewhere. Groups 0-7 of a scale group accumulate into one register set and groups
+// 8-15 into another, so in each set columns c and c ^ 8 are the hi and lo sums of one group; one
+// cross-lane add per set joins them:
+//   D_rg = sum q (hi + lo) * 2^-24      (products exact, fp32 accumulation)
+// and the scale and bias are applied once per scale group:
+//   y_row += s_rg 2^24 D_rg + b_rg Xs_g,   Xs_g = sum of the group's x (fp32).
 typedef MvPhaseDesc MvPhase;
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -90,28 +94,23 @@ __device__ __forceinline__ void mv_prefetch(const MvPhase p, int wg, int nwg, in
     for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
 }
 
-// Constants of the A-operand build, made opaque to constant folding (ORed with a per-lane register
-// that is 0 at run time) so that (w & m) | c becomes one v_and_or_b32 with the constants in registers rather
-// than an AND and an OR with literals. No inline assembly here: the compiler must see every VGPR
-// write that feeds an MFMA operand to insert the wait states the matrix core requires.
-struct DotConsts { uint32_t m_lo, m_hi, magic; };   // magic: two halves of 1024.0
-__device__ __forceinline__ DotConsts dot_consts(int zero) {
-    const uint32_t z = (uint32_t)zero;
-    return DotConsts{0x000F000Fu | z, 0x00F000F0u | z, 0x64006400u | z};
-}
-// A operand of one code dword: halves (n0, n4, 16 n1, 16 n5, n2, n6, 16 n3, 16 n7) + 1024.
-__device__ __forceinline__ f16x8_t a_operand(uint32_t w, const DotConsts& k) {
+// A operand of one code dword: halves (n0, n4, 16 n1, 16 n5, n2, n6, 16 n3, 16 n7) * 2^-24 (subnormal).
+// No inline assembly here: the compiler must see every VGPR write that feeds an MFMA operand to
+// insert the wait states the matrix core requires.
+__device__ __forceinline__ f16x8_t a_operand(uint32_t w) {
     const uint32_t w8 = w >> 8;
-    const u32x4_t v = {(w & k.m_lo) | k.magic, (w & k.m_hi) | k.magic, (w8 & k.m_lo) | k.magic, (w8 & k.m_hi) | k.magic};
+    const u32x4_t v = {w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u};
     return __builtin_bit_cast(f16x8_t, v);
 }
 
-// LDS layout of the matvec input (f16): chunk c of 32 values at xh + 20 * c (80 bytes), code dword i
+// LDS layout of the matvec input (f16): chunk c of 32 values at xh + 32 * c (128 bytes); code dword i
 // of the chunk (codes 8i..8i+7, nibble j at bits 4j) matched by the 16-byte slot i holding
-//   (x0, x4), (x1 / 16, x5 / 16), (x2, x6), (x3 / 16, x7 / 16)      (x of codes 8i..8i+7)
-// after a power-of-two scaling of the whole vector (bytes 64..79 of a chunk are padding). gsum[g]
-// holds (Cs, Xs) of quantization group g; zero16 is 16 bytes of zeros (the masked B operand).
-constexpr int XH_STRIDE = 20;          // floats per chunk
+//   (x0, x4), (x1 / 16, x5 / 16), (x2, x6), (x3 / 16, x7 / 16)      (hi parts of codes 8i..8i+7)
+// after a power-of-two scaling of the whole vector, and slot 4 + i holding the lo parts in the same
+// order. gsum[g] holds Xs, the sum of quantization group g's scaled x; zero16 is 16 bytes of zeros
+// (the masked B operand).
+constexpr int XH_STRIDE = 32;          // floats per chunk
+constexpr int XH_LO = 16;              // floats from a chunk's hi slots to its lo slots
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
@@ -134,26 +133,33 @@ __device__ __forceinline__ float pack_x16_from(const LD& ld, int K, float gmax, 
     for (int t = threadIdx.x; t < (K >> 3); t += MK_THREADS) {   // t: 8 values; 4 consecutive t per chunk
         float4 lo, hi;
         ld(t, lo, hi);
-        const _Float16 h0 = (_Float16)(lo.x * up), h4 = (_Float16)(hi.x * up);
-        const _Float16 h1 = (_Float16)(lo.y * up * 0.0625f), h5 = (_Float16)(hi.y * up * 0.0625f);
-        const _Float16 h2 = (_Float16)(lo.z * up), h6 = (_Float16)(hi.z * up);
-        const _Float16 h3 = (_Float16)(lo.w * up * 0.0625f), h7 = (_Float16)(hi.w * up * 0.0625f);
-        uint4 o;
-        o.x = __builtin_bit_cast(uint32_t, h2_t{h0, h4});
-        o.y = __builtin_bit_cast(uint32_t, h2_t{h1, h5});
-        o.z = __builtin_bit_cast(uint32_t, h2_t{h2, h6});
-        o.w = __builtin_bit_cast(uint32_t, h2_t{h3, h7});
+        // scaled values in slot order (x0, x4, x1 / 16, x5 / 16, x2, x6, x3 / 16, x7 / 16)
+        const float v[8] = {lo.x * up, hi.x * up, lo.y * up * 0.0625f, hi.y * up * 0.0625f,
+                            lo.z * up, hi.z * up, lo.w * up * 0.0625f, hi.w * up * 0.0625f};
+        _Float16 hh[8], hl[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            hh[i] = (_Float16)v[i];
+            hl[i] = (_Float16)(v[i] - (float)hh[i]);
+        }
+        uint4 o, ol;
+        o.x = __builtin_bit_cast(uint32_t, h2_t{hh[0], hh[1]});
+        o.y = __builtin_bit_cast(uint32_t, h2_t{hh[2], hh[3]});
+        o.z = __builtin_bit_cast(uint32_t, h2_t{hh[4], hh[5]});
+        o.w = __builtin_bit_cast(uint32_t, h2_t{hh[6], hh[7]});
+        ol.x = __builtin_bit_cast(uint32_t, h2_t{hl[0], hl[1]});
+        ol.y = __builtin_bit_cast(uint32_t, h2_t{hl[2], hl[3]});
+        ol.z = __builtin_bit_cast(uint32_t, h2_t{hl[4], hl[5]});
+        ol.w = __builtin_bit_cast(uint32_t, h2_t{hl[6], hl[7]});
         const int c = t >> 2;
         *reinterpret_cast<uint4*>(xh + c * XH_STRIDE + (t & 3) * 4) = o;
-        // (Cs, Xs) of the quantization group: the 4 (gs 32) or 8 (gs 64) t of a group sit in
-        // consecutive lanes of one wave (K is a multiple of 128, so whole groups are active)
-        const float ev = (float)h0 + (float)h4 + (float)h2 + (float)h6;
-        const float od = (float)h1 + (float)h5 + (float)h3 + (float)h7;
-        float cs = ev + od, xsum = ev + 16.0f * od;
-        cs += __shfl_xor(cs, 1, 64); cs += __shfl_xor(cs, 2, 64);
+        *reinterpret_cast<uint4*>(xh + c * XH_STRIDE + XH_LO + (t & 3) * 4) = ol;
+        // Xs of the quantization group: the 4 (gs 32) or 8 (gs 64) t of a group sit in consecutive
+        // lanes of one wave (K is a multiple of 128, so whole groups are active)
+        float xsum = ((lo.x + lo.y) + (lo.z + lo.w) + ((hi.x + hi.y) + (hi.z + hi.w))) * up;
         xsum += __shfl_xor(xsum, 1, 64); xsum += __shfl_xor(xsum, 2, 64);
-        if (gsh == 6) { cs += __shfl_xor(cs, 4, 64); xsum += __shfl_xor(xsum, 4, 64); }
-        if ((t & ((1 << (gsh - 3)) - 1)) == 0) *reinterpret_cast<float2*>(gsum + 2 * (t >> (gsh - 3))) = float2{1024.0f * cs, xsum};
+        if (gsh == 6) xsum += __shfl_xor(xsum, 4, 64);
+        if ((t & ((1 << (gsh - 3)) - 1)) == 0) gsum[t >> (gsh - 3)] = xsum;
     }
     lds_barrier();
     return 1.0f / up;
@@ -178,7 +184,6 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
     if (nfb <= 0) return;
     const int gpr = p.K >> GSH;                   // groups per row
     const gptr8 base = mv_base<FB>(p, g, lane);
-    const DotConsts kc = dot_consts(__float_as_int(zero16[lane & 3]));   // a zero the compiler cannot fold
     const int col = lane & 15;
     f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f};
     int tile = g.f0 / g.NF, f = g.f0 - tile * g.NF;   // scale group within the tile
@@ -189,8 +194,10 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
         const uint4 sbr = ring.u[0];
         if (more) ring.u[0] = ld_stream16(nxt);
         const float* xb = xh + (lane >> 4) * 4 + f * (4 * FB) * XH_STRIDE;   // this lane's slot of the group's first chunk
-        // two accumulators (even / odd chunks): half the dependent MFMA chain
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+        // groups 0-7 of the scale group accumulate in accA, 8-15 in accB; each split in two (even /
+        // odd chunks) for half the dependent MFMA chain
+        f32x4_t accA = {0.0f, 0.0f, 0.0f, 0.0f}, accA2 = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4_t accB = {0.0f, 0.0f, 0.0f, 0.0f}, accB2 = {0.0f, 0.0f, 0.0f, 0.0f};
         // one scale group: straight-line code when the reloads' condition is taken outside it
         // (STRAIGHT), so the compiler issues the B-operand LDS reads ahead of the MFMAs that use
         // them; with the condition inside, each slot's reload follows its MFMAs directly, which
@@ -201,23 +208,29 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
                 const uint4 unit = ring.u[k + 1];
                 const uint32_t wd[4] = {unit.x, unit.y, unit.z, unit.w};
                 f16x8_t b[4];
+                constexpr int CPG = 1 << (GSH - 5);                            // chunks per group
+                const bool high = (4 * k) / CPG >= 8;                          // groups 8-15 (accB)
+                auto mfma = [&](int j, const f16x8_t& bj) {   // k and j are constants after unrolling
+                    const f16x8_t av = a_operand(wd[j]);
+                    if (high) {
+                        if (j & 1) accB2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bj, accB2, 0, 0, 0);
+                        else accB = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bj, accB, 0, 0, 0);
+                    } else {
+                        if (j & 1) accA2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bj, accA2, 0, 0, 0);
+                        else accA = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bj, accA, 0, 0, 0);
+                    }
+                };
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    constexpr int CPG = 1 << (GSH - 5);                       // chunks per group
                     const int gcol = (4 * k + j) / CPG;                        // the chunk's group column
-                    const float* bp = col == gcol ? xb + (4 * k + j) * XH_STRIDE : zero16;
+                    const float* bp = col == gcol ? xb + (4 * k + j) * XH_STRIDE
+                                    : col == (gcol ^ 8) ? xb + (4 * k + j) * XH_STRIDE + XH_LO : zero16;
                     b[j] = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(bp));
-                    if constexpr (!STRAIGHT) {   // each operand read right before its MFMA
-                        if (j & 1) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b[j], acc2, 0, 0, 0);
-                        else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b[j], acc, 0, 0, 0);
-                    }
+                    if constexpr (!STRAIGHT) mfma(j, b[j]);   // each operand read right before its MFMA
                 }
                 if constexpr (STRAIGHT) {        // the four reads first, then the four MFMAs
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        if (j & 1) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b[j], acc2, 0, 0, 0);
-                        else acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j], kc), b[j], acc, 0, 0, 0);
-                    }
+                    for (int j = 0; j < 4; j++) mfma(j, b[j]);
                 }
                 if constexpr (!STRAIGHT) {
                     if (more) ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
@@ -231,13 +244,19 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
         // scales of the 16 groups (groups past the row's last are zero-scaled; their sums may be junk)
         const int gi = 16 * f + col;
         const bool real = gi < gpr;
-        const float2 gs2 = *reinterpret_cast<const float2*>(gsum + 2 * (real ? gi : 0));
-        acc += acc2;
+        const float xs = gsum[real ? gi : 0];
+        accA += accA2; accB += accB2;
+        f32x4_t acc;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {   // hi (column c) + lo (column c ^ 8) of each group
+            const float sa = accA[r] + __shfl_xor(accA[r], 8, 64), sb = accB[r] + __shfl_xor(accB[r], 8, 64);
+            acc[r] = col < 8 ? sa : sb;
+        }
         const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float sc = __uint_as_float(sv[r] << 16), bb = __uint_as_float(sv[r] & 0xffff0000u);
-            const float t = sc * (acc[r] - gs2.x) + bb * gs2.y;
+            const float sc = __uint_as_float(sv[r] << 16) * 16777216.0f, bb = __uint_as_float(sv[r] & 0xffff0000u);
+            const float t = sc * acc[r] + bb * xs;
             run[r] += real ? t : 0.0f;
         }
         if (f == g.NF - 1 || i == nfb - 1) {     // tile done (or the wave's range): row sums to LDS

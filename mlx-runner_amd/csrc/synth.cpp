@@ -196,3 +196,16 @@ extern "C" int mlxr_quantize_row(const float* w, int K, int bits, int gs, uint8_
     }
     return MLXR_OK;
 }
+
+extern "C" int mlxr_synth_matrix(uint64_t seed, uint64_t tid, int O, int K, int bits, int gs, float std_, uint8_t* codes,
+                                 uint16_t* sc, uint16_t* bi) {
+    if (!codes || !sc || !bi || O <= 0 || K <= 0 || K % 2 || gs <= 0 || K % gs || bits < 1 || bits > 8 || (int64_t)K * bits % 8)
+        return MLXR_E_INVALID_ARG;
+    const int64_t rowBytes = (int64_t)K * bits / 8, groups = K / gs;
+    mlxr::parallel_rows(O, [&](int64_t r) {
+        std::vector<float> row(K);
+        mlxr::gen_row(seed, tid, r, K, std_, row.data());
+        mlxr_quantize_row(row.data(), K, bits, gs, codes + r * rowBytes, sc + r * groups, bi + r * groups);
+    });
+    return MLXR_OK;
+}

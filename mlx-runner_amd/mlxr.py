@@ -72,6 +72,7 @@ def _load():
         "mlxr_profile_kernel": (I, [P, C.c_char_p, I, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
         "mlxr_synth_write": (I, [C.c_char_p, C.c_uint64, F, C.c_char_p]),
         "mlxr_quantize_row": (I, [P, I, I, I, P, P, P]),
+        "mlxr_synth_matrix": (I, [C.c_uint64, C.c_uint64, I, I, I, I, F, P, P, P]),
         "mlxr_device_count": (I, []), "mlxr_device_name": (C.c_char_p, []),
         "mlxr_dev_alloc": (I, [C.POINTER(P), C.c_size_t]), "mlxr_dev_free": (I, [P]),
         "mlxr_memcpy_h2d": (I, [P, P, C.c_size_t]), "mlxr_memcpy_d2h": (I, [P, P, C.c_size_t]),
@@ -378,6 +379,17 @@ def synth_write(config: dict | str, seed: int, directory: str, std: float = 0.02
     import json
     text = config if isinstance(config, str) else json.dumps(config)
     check(lib.mlxr_synth_write(text.encode(), C.c_uint64(seed), C.c_float(std), directory.encode()))
+
+
+def synth_matrix(seed: int, tensor_id: int, O: int, K: int, bits: int, group_size: int, std: float = 0.02):
+    """One seeded matrix drawn and quantized as mlxr_synth_write draws its tensors: (codes [O][K*bits/8]
+    uint8, bf16 scales [O][K/gs] uint16, bf16 biases [O][K/gs] uint16)."""
+    codes = np.zeros((O, K * bits // 8), np.uint8)
+    s = np.zeros((O, K // group_size), np.uint16)
+    b = np.zeros((O, K // group_size), np.uint16)
+    check(lib.mlxr_synth_matrix(C.c_uint64(seed), C.c_uint64(tensor_id), O, K, bits, group_size, C.c_float(std),
+                                codes.ctypes.data, s.ctypes.data, b.ctypes.data))
+    return codes, s, b
 
 
 def quantize_row(w: np.ndarray, bits: int, group_size: int):

@@ -123,6 +123,19 @@ double orc_round_f16_d(double v) {
 static int f16_mode(const orc_qlinear* l) {
     return l->bits == 4 && (l->gs == 32 || l->gs == 64 || l->gs == 128) && (l->K / l->gs) % 2 == 0;
 }
+/* sum_k w[k] x[k] in double precision: four interleaved partial sums (k mod 4), added at the end. */
+typedef double orc_v4d __attribute__((vector_size(32)));
+static double dot_f64(const float* w, const float* x, int K) {
+    orc_v4d acc = {0, 0, 0, 0};
+    int k = 0;
+    for (; k + 4 <= K; k += 4) {
+        const orc_v4d a = {w[k], w[k + 1], w[k + 2], w[k + 3]}, b = {x[k], x[k + 1], x[k + 2], x[k + 3]};
+        acc += a * b;
+    }
+    double s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    for (; k < K; k++) s += (double)w[k] * (double)x[k];
+    return s;
+}
 static void qlinear_impl(const orc_qlinear* l, const float* x, int T, float* y, int mode) {
     float* xr = NULL;
     double* inv = NULL;
@@ -164,8 +177,7 @@ static void qlinear_impl(const orc_qlinear* l, const float* x, int T, float* y, 
             }
             for (int t = 0; t < T; t++) {
                 const float* xt = x + (int64_t)t * l->K;
-                double acc = 0;
-                for (int k = 0; k < l->K; k++) acc += (double)w[k] * (double)xt[k];
+                double acc = dot_f64(w, xt, l->K);
                 if (mode == 2) acc *= inv[t];
                 y[(int64_t)t * l->O + o] = (float)acc + (l->bias ? l->bias[o] : 0.0f);
             }

@@ -124,31 +124,10 @@ class QMatrix:
         lib.orc_qlinear_prefill(C.byref(self.s), x.ctypes.data, x.shape[0], y.ctypes.data)
         return y
 
-    def matmul_x16(self, x):
-        """The batch-1 decode matvec's declared precision (test infrastructure): x rounded to f16 after
-        the vector's power-of-two scaling (round_x16), exact weights, f64 accumulation."""
-        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.K)
-        return self.matmul_f64(np.stack([round_x16(r) for r in x]))
-
     def dequant_row(self, r):
         out = np.zeros(self.K, np.float32)
         lib.orc_dequant_row(C.byref(self.s), r, out.ctypes.data)
         return out
-
-
-def round_x16(x):
-    """x as the decode matvec holds it: scaled by 2^e (e = 14 - the exponent of max |x|, clamped to
-    +-100, so every scaled value is below 2^14), values at odd positions further by 1/16 (the
-    nibble at bits 4..7 of a code byte carries a factor 16), rounded to f16 and scaled back."""
-    x = np.ascontiguousarray(x, dtype=np.float32)
-    gmax = float(np.max(np.abs(x))) if x.size else 0.0
-    ex = int(np.frexp(np.float32(gmax))[1]) if 0.0 < gmax <= 3.0e38 else 0
-    e = min(max(14 - ex, -100), 100)
-    up = np.float32(np.ldexp(np.float32(1.0), e))
-    odd = (np.arange(x.size) & 1) == 1
-    f = np.where(odd, np.float32(0.0625), np.float32(1.0)).astype(np.float32)
-    h = ((x * up) * f).astype(np.float16).astype(np.float32)
-    return ((h / f) / up).astype(np.float32)
 
 
 def rms_norm(x, w, eps):
@@ -255,7 +234,9 @@ class Model:
         self.vocab = lib.orc_model_vocab(self.h)
         self.max_seq = max_seq
 
-    def forward(self, tokens, offset, small_t=8):
+    def forward(self, tokens, offset, small_t=1 << 30):
+        """Logits of the last token (fp32 semantics: every product in double precision). small_t is a
+        diagnostic: chunks longer than small_t tokens use the GPU GEMM's operand precision instead."""
         t = np.ascontiguousarray(tokens, np.int32)
         out = np.zeros(self.vocab, np.float32)
         rc = lib.orc_forward(self.h, t.ctypes.data, t.size, offset, small_t, out.ctypes.data)

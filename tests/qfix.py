@@ -121,6 +121,30 @@ class QuantFixture:
         return oracle.QMatrix(self.packed, self.scales, self.biases, self.K, self.bits, self.gs, bias=self.bias)
 
 
+class SynthMatrix:
+    """A matrix at a real model shape, N(0, std) weights quantized exactly as the synthetic models are
+    (mlxr_synth_matrix: MLX affine, bf16 scale / bias). Exposes the QuantFixture members the kernel
+    tests use (packed bytes, raw and float scales / biases, device and oracle views)."""
+
+    def __init__(self, mlxr, O, K, bits, gs, seed=1, tensor_id=0, std=0.02):
+        self.O, self.K, self.bits, self.gs, self.st = O, K, bits, gs, "bf16"
+        self.packed, self.s_raw, self.b_raw = mlxr.synth_matrix(seed, tensor_id, O, K, bits, gs, std)
+        self.scales, self.biases = bf16_to_f32(self.s_raw), bf16_to_f32(self.b_raw)
+        self.bias_raw = self.bias = None
+
+    def rows(self, r0, r1):
+        """Rows [r0, r1) as a matrix of their own."""
+        sub = object.__new__(SynthMatrix)
+        sub.O, sub.K, sub.bits, sub.gs, sub.st = r1 - r0, self.K, self.bits, self.gs, self.st
+        sub.packed, sub.s_raw, sub.b_raw = self.packed[r0:r1], self.s_raw[r0:r1], self.b_raw[r0:r1]
+        sub.scales, sub.biases = self.scales[r0:r1], self.biases[r0:r1]
+        sub.bias_raw = sub.bias = None
+        return sub
+
+    device = QuantFixture.device
+    oracle = QuantFixture.oracle
+
+
 def max_rel_err(a, b):
     """assertClose's metric (KernelTests.swift:116-124): |a-b| / max(1, |b|)."""
     a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
