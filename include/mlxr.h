@@ -127,6 +127,12 @@ int mlxr_set_decode_mode(mlxr_model* m, int mode);
  * (-1 where unset; marks 512 + 8 * layer + k are sub-phase points), out sized for every
  * workgroup; returns the workgroup count. */
 int mlxr_profile_decode_phases(mlxr_model* m, int offset, double* out, int max_intervals);
+/* Test hook of the persistent step's failure path: the next persistent decode step's first input
+ * wait (workgroup 0) asks for a tag no launch writes, with a short bound, so the wait expires, the
+ * abort flag propagates and every wave still ends normally. That step's finish, and that of any
+ * step queued behind it, return MLXR_E_GPU; the model falls back to the kernel-per-op step. No
+ * counterpart in the reference. */
+int mlxr_debug_stall_next_step(mlxr_model* m);
 /* 1 when begin_decode runs the persistent kernel for dense steps. */
 int mlxr_decode_mode(const mlxr_model* m);
 /* Decode steps with the whole step captured as a hipGraph (1, default) or launched kernel by kernel (0). */

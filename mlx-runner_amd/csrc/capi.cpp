@@ -144,6 +144,7 @@ int mlxr_profile_decode_phases(mlxr_model* m, int offset, double* out, int max_i
     if (!m || !out) return set_error(MLXR_E_INVALID_ARG, "null argument");
     return model_phase_times(m->m, offset, out, max_intervals);
 }
+int mlxr_debug_stall_next_step(mlxr_model* m) { return m ? model_stall_next_step(m->m) : set_error(MLXR_E_INVALID_ARG, "null model"); }
 int mlxr_set_graphs(mlxr_model* m, int enabled) { if (!m) return MLXR_E_INVALID_ARG; m->m->use_graphs = enabled != 0; return MLXR_OK; }
 
 int mlxr_synth_write(const char* config_json, uint64_t seed, float std_, const char* dir) {

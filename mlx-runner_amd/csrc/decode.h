@@ -74,13 +74,17 @@ struct MegaArgs {
     int n_pages, pt_lds_off;          // page table entries, byte offset of their LDS copy
     int* ring_tok; int* ring_status; int ring_mask;
     unsigned long long* prof;         // optional: per workgroup, wall-clock at every phase start / end
+    unsigned spin_limit;              // polls of a wait before it gives up (MEGA_SPIN_LIMIT)
+    int stall;                        // test hook, 1: workgroup 0's first wait asks for a tag no launch writes
 };
+constexpr unsigned MEGA_SPIN_LIMIT = 1u << 20;
 constexpr int MEGA_PROF_EVENTS = 1024;
 
 size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split);   // a.L, a.kv_stage and the shape set
 size_t mega_desc_offset(const MegaArgs& a);
 hipError_t launch_decode_step(const MegaArgs& a, int nwg, size_t lds, hipStream_t s);
 hipError_t mega_set_lds_limit(size_t lds);
+int mega_blocks_per_cu(const MegaArgs& a, size_t lds);   // resident workgroups per CU at this LDS size (0: error)
 int mega_threads();
 int mega_tiles_per_wg_cap();   // 16-row tiles of one phase one workgroup may own
 int mega_wg_row_cap();     // rows of an accumulate phase one workgroup may own

@@ -410,6 +410,15 @@ static int mega_setup(Model* m) {
     if (lds > 158 * 1024) return no("LDS need " + std::to_string(lds >> 10) + " KiB");
     if (mega_set_lds_limit(lds) != hipSuccess) return no("LDS attribute");
     if (nwg > MEGA_MAX_WG) return no("too many workgroups");
+    // co-residency: the phases' hand-overs wait for other workgroups, so the whole grid must be
+    // resident at once (the launch is cooperative and fails rather than stalls otherwise)
+    a.head = m->tile_head;   // the kernel variant follows the group size
+    const int per_cu = mega_blocks_per_cu(a, lds);
+    if (per_cu < 1 || nwg > per_cu * cus)
+        return no("the grid cannot be resident at once (" + std::to_string(per_cu) + " workgroups per CU)");
+    int coop = 0;
+    HIPCHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, 0));
+    if (!coop) return no("no cooperative launch");
     // the layers' repacked phases (tiles_setup), plus the lm_head's
     int rc = MLXR_OK;
     if ((rc = dalloc(m, &m->mega_layers, c.L))) return rc;
@@ -444,6 +453,7 @@ static int mega_setup(Model* m) {
     a.ring_tok = m->ring_tok_dev; a.ring_status = m->ring_status_dev; a.ring_mask = Model::RING - 1;
     *m->abort_host = 0;
     a.abort_host = m->abort_host_dev;
+    a.spin_limit = MEGA_SPIN_LIMIT; a.stall = 0;
     m->mega_nwg = nwg; m->mega_lds = lds; m->mega_ok = true;
     return MLXR_OK;
 }
@@ -906,6 +916,10 @@ int model_begin_decode(Model* m, int offset, const mlxr_sample_params* sp, mlxr_
         const bool greedy = sp->temperature <= 0.001f && sp->penalty == 1.0f;
         MegaArgs a = m->mega;
         a.select = greedy ? 1 : 0;
+        if (m->stall_next) {   // test hook: this step's first wait expires after a few polls
+            a.stall = 1; a.spin_limit = 4096;
+            m->stall_next = false;
+        }
         HIPCHECK(launch_decode_step(a, m->mega_nwg, m->mega_lds, m->stream));
         if (!greedy) {
             const int V = std::min(sp->V > 0 ? (int)sp->V : m->cfg.V, m->cfg.V);
@@ -951,13 +965,35 @@ int model_finish(Model* m, const mlxr_step* st, int32_t* tok) {
     slot.busy = false;
     if (e != hipSuccess) return set_error(MLXR_E_GPU, std::string("GPU error: ") + hipGetErrorString(e));
     record_gpu_time(m, slot);
+    if (slot.failed) {
+        slot.failed = false;
+        return set_error(MLXR_E_GPU, "decode step discarded: an earlier step in flight failed");
+    }
     if (m->mega_ok && *(volatile int*)m->abort_host) {
-        m->mega_ok = false;   // fall back to the kernel-per-op step from now on
-        *m->abort_host = 0;
-        HIPCHECK(hipMemset(m->mega.sync, 0, sizeof(MegaSync)));
-        return set_error(MLXR_E_GPU, "persistent decode step: a grid barrier expired (step result discarded)");
+        // A wait of the persistent step expired. Every kernel still ran to its end, but a step queued
+        // behind this one ran with the abort flag raised: wait for it and fail it too.
+        HIPCHECK(hipStreamSynchronize(m->stream));
+        for (auto& other : m->slots)
+            if (other.busy) other.failed = true;
+        // clear the device abort flag (the launch counter keeps counting, so no later tag can match a
+        // stale value) and the argmax counter, on the model stream; then fall back to the
+        // kernel-per-op step for good
+        HIPCHECK(hipMemsetAsync(&m->mega.sync->abort, 0, sizeof(unsigned), m->stream));
+        HIPCHECK(hipMemsetAsync(m->mega.head_done, 0, sizeof(unsigned), m->stream));
+        HIPCHECK(hipStreamSynchronize(m->stream));
+        *(volatile int*)m->abort_host = 0;
+        m->mega_ok = false;
+        m->mega_reason = "a persistent step's bounded wait expired";
+        m->dev_pos_known = -1;   // the failed steps advanced *dpos; the next step writes it again
+        return set_error(MLXR_E_GPU, "persistent decode step: a bounded wait expired (step result discarded)");
     }
     return read_ring(m, st->offset + 1, tok);
+}
+
+int model_stall_next_step(Model* m) {
+    if (!m->mega_ok || m->decode_mode != 1) return set_error(MLXR_E_UNSUPPORTED, "the persistent decode step is not in use");
+    m->stall_next = true;
+    return MLXR_OK;
 }
 
 // reusablePrefix (Transformer.swift:1193-1209): every cache of this build holds the full context.

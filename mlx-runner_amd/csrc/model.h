@@ -92,10 +92,11 @@ struct Model {
     std::vector<LayerDev> tile_layers;  // host copy of the repacked phases: the prefill GEMMs use them too
     MvPhaseDesc tile_head{};            // repacked lm_head (code == nullptr: none)
     int mega_nwg = 0; size_t mega_lds = 0;
+    bool stall_next = false;         // test hook: the next persistent step's first wait expires
     std::string mega_reason;
     double last_gpu_time = 0;
 
-    struct StepSlot { hipEvent_t start = nullptr, stop = nullptr; int offset = -1; bool busy = false; };
+    struct StepSlot { hipEvent_t start = nullptr, stop = nullptr; int offset = -1; bool busy = false, failed = false; };
     StepSlot slots[4];
     int next_slot = 0;
 
@@ -118,6 +119,7 @@ int model_prefill(Model* m, const int32_t* tokens, int n, int offset, const mlxr
 int model_begin_decode(Model* m, int offset, const mlxr_sample_params* sp, mlxr_step* out);
 int model_finish(Model* m, const mlxr_step* st, int32_t* tok);
 int model_reusable_prefix(Model* m, int common, int prev_len);
+int model_stall_next_step(Model* m);
 int model_seed(Model* m, uint64_t seed);
 int model_set_sparse(Model* m, const mlxr_sparse_cfg* cfg);
 int model_read_kv(Model* m, int layer, int rows, float* k, float* v);

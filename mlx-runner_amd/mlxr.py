@@ -68,7 +68,7 @@ def _load():
         "mlxr_finish": (I, [P, C.POINTER(Step), C.POINTER(C.c_int32)]),
         "mlxr_reusable_prefix": (I, [P, I, I]), "mlxr_reset_write_tracking": (V, [P]),
         "mlxr_seed_sampler": (I, [P, C.c_uint64]), "mlxr_set_sparse": (I, [P, C.POINTER(SparseCfg)]),
-        "mlxr_last_gpu_time": (C.c_double, [P]), "mlxr_read_kv": (I, [P, I, I, P, P]), "mlxr_set_graphs": (I, [P, I]), "mlxr_set_decode_mode": (I, [P, I]), "mlxr_decode_mode": (I, [P]), "mlxr_profile_decode_phases": (I, [P, I, P, I]),
+        "mlxr_last_gpu_time": (C.c_double, [P]), "mlxr_read_kv": (I, [P, I, I, P, P]), "mlxr_set_graphs": (I, [P, I]), "mlxr_set_decode_mode": (I, [P, I]), "mlxr_decode_mode": (I, [P]), "mlxr_profile_decode_phases": (I, [P, I, P, I]), "mlxr_debug_stall_next_step": (I, [P]),
         "mlxr_profile_kernel": (I, [P, C.c_char_p, I, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
         "mlxr_synth_write": (I, [C.c_char_p, C.c_uint64, F, C.c_char_p]),
         "mlxr_quantize_row": (I, [P, I, I, I, P, P, P]),
@@ -307,6 +307,10 @@ class Transformer:
         if n < 0:
             check(n)
         return out[:n * 1024].reshape(n, 1024)
+
+    def debug_stall_next_step(self):
+        """Makes the next persistent decode step's first wait expire (mlxr_debug_stall_next_step)."""
+        check(lib.mlxr_debug_stall_next_step(self._h))
 
     def set_graphs(self, on: bool):
         check(lib.mlxr_set_graphs(self._h, 1 if on else 0))

@@ -283,3 +283,26 @@ def test_sampled_generation_is_seeded(gpu, models):
     assert a == b
     assert all(0 <= t < 1000 for t in a)
     assert a != c or len(set(a)) == 1
+
+
+def test_persistent_abort_fails_both_steps_in_flight(gpu, models):
+    """Failure path of the persistent step, forced from the host: the first step's first wait asks for
+    a tag no launch writes with a short bound, so it expires and raises the abort flag; every kernel
+    still runs to its end. Both steps in flight then report a GPU error, the model falls back to the
+    kernel-per-op step, and a fresh turn decodes the same tokens as a healthy model."""
+    d = models["qwen3"]
+    toks = prompt(20, 1000, seed=12)
+    with mlxr.Transformer(d, context_length=512) as m:
+        assert m.persistent_decode
+        want = m.generate(toks, 8, GREEDY)
+        first = m.prefill(toks, 0, GREEDY)
+        m.debug_stall_next_step()
+        s1 = m.begin_decode_step(len(toks), GREEDY)
+        s2 = m.begin_decode_step(len(toks) + 1, GREEDY)
+        for s in (s1, s2):
+            with pytest.raises(mlxr.EngineError) as e:
+                m.finish(s)
+            assert e.value.case == "gpuFailure"
+        assert not m.persistent_decode
+        assert first == want[0]
+        assert m.generate(toks, 8, GREEDY) == want
