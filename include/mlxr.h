@@ -80,15 +80,27 @@ int mlxr_sparse_available(const mlxr_model* m);            /* Transformer.sparse
 int mlxr_written_high(const mlxr_model* m);                /* Transformer.writtenHigh (:665) */
 
 /* ---------------------------------------------------------------- the step API */
-/* forward(_:offset:allLogits:dense:) (Transformer.swift:1117-1136): runs tokens at
- * offset..offset+n-1 in chunks of 512; *logits_out = last row's logits (V floats) or, with
- * all_logits (n <= 8), [n][V]. Owned by the model, valid until the next call. */
+/* The isCancelled closure of forward / prefill (Transformer.swift:1118,1224): called with `user`
+ * between chunks (never before the first); nonzero stops the call with MLXR_E_CANCELLED. The rows
+ * of the chunks already run stay in the KV cache, as in the reference. NULL: never cancelled. */
+typedef int (*mlxr_cancel_fn)(void* user);
+/* forward(_:offset:allLogits:dense:isCancelled:) (Transformer.swift:1117-1136): runs tokens at
+ * offset..offset+n-1 in chunks of MLXR_PREFILL_CHUNK; *logits_out = last row's logits (V floats)
+ * or, with all_logits (n <= 8), [n][V]. Owned by the model, valid until the next call. */
 int mlxr_forward(mlxr_model* m, const int32_t* tokens, int n, int offset, int all_logits, int dense,
-                 const float** logits_out);
-/* prefill(_:offset:sample:) (Transformer.swift:1224-1249): token selected on the GPU from the last
- * row, stored at position offset + n. */
+                 const float** logits_out, mlxr_cancel_fn is_cancelled, void* user);
+/* prefill(_:offset:sample:isCancelled:) (Transformer.swift:1224-1249): token selected on the GPU
+ * from the last row, stored at position offset + n. */
 int mlxr_prefill(mlxr_model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp,
-                 int32_t* token_out);
+                 int32_t* token_out, mlxr_cancel_fn is_cancelled, void* user);
+/* Tokens per batched pass of forward / prefill: the reference's maxBatch is 512
+ * (ModelConfig.swift); here 2048, so a cancel request is seen after at most one 2048-token chunk
+ * (about 40 ms of an 8B prefill on one MI355X). */
+#define MLXR_PREFILL_CHUNK 2048
+/* Logits of the last decode step (V floats, the row its token was selected from), after its
+ * finish and with no step in flight. Owned by the model, valid until the next call. No
+ * counterpart in the reference, whose logits buffer the caller reads directly (Transformer.logits). */
+int mlxr_step_logits(mlxr_model* m, const float** logits_out);
 /* beginDecodeStep(offset:sample:) (Transformer.swift:1255-1264): commits the step for the token at
  * position offset (written by the previous step's sampler or by prefill) without waiting. Steps
  * must be begun and finished in position order, at most two in flight. */

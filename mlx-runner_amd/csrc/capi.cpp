@@ -109,13 +109,19 @@ const char* mlxr_quant_description(const mlxr_model* m) { return m ? m->m->quant
 int mlxr_sparse_available(const mlxr_model* m) { return m && m->m->sparse_alloc ? 1 : 0; }
 int mlxr_written_high(const mlxr_model* m) { return m ? m->m->written_high : 0; }
 
-int mlxr_forward(mlxr_model* m, const int32_t* tokens, int n, int offset, int all_logits, int dense, const float** logits_out) {
+int mlxr_forward(mlxr_model* m, const int32_t* tokens, int n, int offset, int all_logits, int dense, const float** logits_out,
+                 mlxr_cancel_fn is_cancelled, void* user) {
     if (!m || !logits_out) return set_error(MLXR_E_INVALID_ARG, "null argument");
-    return model_forward(m->m, tokens, n, offset, all_logits != 0, dense != 0, logits_out);
+    return model_forward(m->m, tokens, n, offset, all_logits != 0, dense != 0, logits_out, Cancel{is_cancelled, user});
 }
-int mlxr_prefill(mlxr_model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, int32_t* token_out) {
+int mlxr_prefill(mlxr_model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, int32_t* token_out,
+                 mlxr_cancel_fn is_cancelled, void* user) {
     if (!m || !token_out) return set_error(MLXR_E_INVALID_ARG, "null argument");
-    return model_prefill(m->m, tokens, n, offset, sp, token_out);
+    return model_prefill(m->m, tokens, n, offset, sp, token_out, Cancel{is_cancelled, user});
+}
+int mlxr_step_logits(mlxr_model* m, const float** logits_out) {
+    if (!m || !logits_out) return set_error(MLXR_E_INVALID_ARG, "null argument");
+    return model_step_logits(m->m, logits_out);
 }
 int mlxr_begin_decode(mlxr_model* m, int offset, const mlxr_sample_params* sp, mlxr_step* out) {
     if (!m || !out) return set_error(MLXR_E_INVALID_ARG, "null argument");

@@ -831,12 +831,13 @@ void record_gpu_time(Model* m, const Model::StepSlot& s) {
 }
 }  // namespace
 
-int model_forward(Model* m, const int32_t* tokens, int n, int offset, bool all_logits, bool dense, const float** out) {
+int model_forward(Model* m, const int32_t* tokens, int n, int offset, bool all_logits, bool dense, const float** out, Cancel cancel) {
     if (n <= 0 || !tokens) return set_error(MLXR_E_INVALID_ARG, "no tokens");
     if (all_logits && n > 8) return set_error(MLXR_E_INVALID_OUTPUT, "verify batch too large");
     if (offset < 0 || offset + n > m->max_seq) return set_error(MLXR_E_CONTEXT_FULL, "The context window is full.");
     if (int rc = check_tokens(m, tokens, n)) return rc;
     for (int start = 0; start < n;) {
+        if (start > 0 && cancel.requested()) return set_error(MLXR_E_CANCELLED, "cancelled");   // Transformer.swift:1127
         const int k = std::min(m->max_batch, n - start);
         const bool last = start + k == n;
         if (int rc = run_chunk(m, tokens + start, k, offset + start, last, last && all_logits, dense || n > 1)) return rc;
@@ -867,11 +868,12 @@ static int read_ring(Model* m, int pos, int32_t* tok) {
     return MLXR_OK;
 }
 
-int model_prefill(Model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, int32_t* tok) {
+int model_prefill(Model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, int32_t* tok, Cancel cancel) {
     if (n <= 0 || !tokens || offset < 0 || offset + n >= m->max_seq) return set_error(MLXR_E_CONTEXT_FULL, "The context window is full.");
     if (int rc = check_sample(sp)) return rc;
     if (int rc = check_tokens(m, tokens, n)) return rc;
     for (int start = 0; start < n;) {
+        if (start > 0 && cancel.requested()) return set_error(MLXR_E_CANCELLED, "cancelled");   // Transformer.swift:1233
         const int k = std::min(m->max_batch, n - start);
         const bool last = start + k == n;
         const int at = offset + start;
@@ -888,6 +890,15 @@ int model_prefill(Model* m, const int32_t* tokens, int n, int offset, const mlxr
         start += k;
     }
     return read_ring(m, offset + n, tok);
+}
+
+int model_step_logits(Model* m, const float** out) {
+    for (auto& s : m->slots)
+        if (s.busy) return set_error(MLXR_E_INVALID_ARG, "a decode step is in flight");
+    HIPCHECK(hipStreamSynchronize(m->stream));
+    HIPCHECK(hipMemcpy(m->h_logits, m->logits, (size_t)m->cfg.V * 4, hipMemcpyDeviceToHost));
+    *out = m->h_logits;
+    return MLXR_OK;
 }
 
 // SparseAttention.plan(position:) != nil (SparseAttention.swift:80-94), on the host.

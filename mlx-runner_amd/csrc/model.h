@@ -80,7 +80,7 @@ struct Model {
 
     hipStream_t stream = nullptr;
     int qkv_cols = 0, nsplit_dec = 32;
-    int max_batch = 2048;                // prefill chunk (tokens per batched pass)
+    int max_batch = MLXR_PREFILL_CHUNK;                // prefill chunk (tokens per batched pass)
     int dev_pos_known = -1;              // value *dpos will hold once queued work completes
     int written_high = 0;
     bool use_graphs = true;
@@ -114,8 +114,16 @@ struct Model {
 };
 
 int model_open(const char* dir, int context_len, const mlxr_sparse_cfg* sparse, Model** out);
-int model_forward(Model* m, const int32_t* tokens, int n, int offset, bool all_logits, bool dense, const float** out);
-int model_prefill(Model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, int32_t* tok);
+// The caller's isCancelled closure: polled between chunks.
+struct Cancel {
+    mlxr_cancel_fn fn; void* user;
+    bool requested() const { return fn && fn(user) != 0; }
+};
+int model_forward(Model* m, const int32_t* tokens, int n, int offset, bool all_logits, bool dense, const float** out,
+                  Cancel cancel = {});
+int model_prefill(Model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, int32_t* tok,
+                  Cancel cancel = {});
+int model_step_logits(Model* m, const float** out);
 int model_begin_decode(Model* m, int offset, const mlxr_sample_params* sp, mlxr_step* out);
 int model_finish(Model* m, const mlxr_step* st, int32_t* tok);
 int model_reusable_prefix(Model* m, int common, int prev_len);

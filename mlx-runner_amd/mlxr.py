@@ -51,6 +51,17 @@ class QMat(C.Structure):
     _fields_ = [("w", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p), ("bias", C.c_void_p), ("O", C.c_int32)]
 
 
+CancelFn = C.CFUNCTYPE(C.c_int, C.c_void_p)   # mlxr_cancel_fn
+
+
+def _cancel_fn(is_cancelled):
+    """A C callback for an isCancelled closure (a null function pointer for None). The caller keeps
+    the returned object alive for the duration of the call."""
+    if is_cancelled is None:
+        return CancelFn()
+    return CancelFn(lambda _user: 1 if is_cancelled() else 0)
+
+
 def _load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} is not built: run `python mlx-runner_amd/build.py`")
@@ -62,8 +73,9 @@ def _load():
         "mlxr_vocab_size": (I, [P]), "mlxr_max_seq": (I, [P]), "mlxr_hidden_size": (I, [P]), "mlxr_num_layers": (I, [P]),
         "mlxr_weight_bytes": (C.c_int64, [P]), "mlxr_device_bytes": (C.c_int64, [P]),
         "mlxr_quant_description": (C.c_char_p, [P]), "mlxr_sparse_available": (I, [P]), "mlxr_written_high": (I, [P]),
-        "mlxr_forward": (I, [P, P, I, I, I, I, C.POINTER(C.POINTER(F))]),
-        "mlxr_prefill": (I, [P, P, I, I, C.POINTER(SampleParams), C.POINTER(C.c_int32)]),
+        "mlxr_forward": (I, [P, P, I, I, I, I, C.POINTER(C.POINTER(F)), CancelFn, P]),
+        "mlxr_prefill": (I, [P, P, I, I, C.POINTER(SampleParams), C.POINTER(C.c_int32), CancelFn, P]),
+        "mlxr_step_logits": (I, [P, C.POINTER(C.POINTER(F))]),
         "mlxr_begin_decode": (I, [P, I, C.POINTER(SampleParams), C.POINTER(Step)]),
         "mlxr_finish": (I, [P, C.POINTER(Step), C.POINTER(C.c_int32)]),
         "mlxr_reusable_prefix": (I, [P, I, I]), "mlxr_reset_write_tracking": (V, [P]),
@@ -237,6 +249,7 @@ class Transformer:
         check(lib.mlxr_model_open(directory.encode(), int(context_length), C.byref(cfg) if cfg is not None else None,
                                   C.byref(h)))
         self._h = h.value
+        self._sparse = sparse if sparse is not None and self.sparse_available else None
         self.vocab_size = lib.mlxr_vocab_size(self._h)
         self.max_seq = lib.mlxr_max_seq(self._h)
         self.hidden_size = lib.mlxr_hidden_size(self._h)
@@ -273,9 +286,15 @@ class Transformer:
     def last_gpu_time(self) -> float:
         return lib.mlxr_last_gpu_time(self._h)
 
+    @property
+    def sparse(self) -> SparseAttention | None:
+        """The sparse decode attention budget in use (Transformer.sparse, :813), None when off."""
+        return self._sparse
+
     def set_sparse(self, sparse: SparseAttention | None):
         cfg = sparse.cfg() if sparse is not None else None
         check(lib.mlxr_set_sparse(self._h, C.byref(cfg) if cfg is not None else None))
+        self._sparse = sparse
 
     def profile_kernel(self, kind: str, iters: int = 100, context: int = 1):
         """(mean launch ms, algorithmic bytes per launch) of one decode kernel class."""
@@ -315,20 +334,29 @@ class Transformer:
     def set_graphs(self, on: bool):
         check(lib.mlxr_set_graphs(self._h, 1 if on else 0))
 
-    def forward(self, tokens, offset: int, all_logits: bool = False, dense: bool = False) -> np.ndarray:
+    def forward(self, tokens, offset: int, all_logits: bool = False, dense: bool = False, is_cancelled=None) -> np.ndarray:
+        """forward(_:offset:allLogits:dense:isCancelled:): is_cancelled() is polled between chunks."""
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         out = C.POINTER(C.c_float)()
-        check(lib.mlxr_forward(self._h, t.ctypes.data, len(t), int(offset), int(all_logits), int(dense), C.byref(out)))
+        cb = _cancel_fn(is_cancelled)
+        check(lib.mlxr_forward(self._h, t.ctypes.data, len(t), int(offset), int(all_logits), int(dense), C.byref(out), cb, None))
         rows = len(t) if all_logits else 1
         arr = np.ctypeslib.as_array(out, shape=(rows * self.vocab_size,)).copy()
         return arr.reshape(rows, self.vocab_size) if all_logits else arr
 
-    def prefill(self, tokens, offset: int, sample: SamplingParameters) -> int:
+    def prefill(self, tokens, offset: int, sample: SamplingParameters, is_cancelled=None) -> int:
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         sp = sample.params(self.vocab_size)
         tok = C.c_int32()
-        check(lib.mlxr_prefill(self._h, t.ctypes.data, len(t), int(offset), C.byref(sp), C.byref(tok)))
+        cb = _cancel_fn(is_cancelled)
+        check(lib.mlxr_prefill(self._h, t.ctypes.data, len(t), int(offset), C.byref(sp), C.byref(tok), cb, None))
         return tok.value
+
+    def step_logits(self) -> np.ndarray:
+        """Logits of the last finished decode step (mlxr_step_logits)."""
+        out = C.POINTER(C.c_float)()
+        check(lib.mlxr_step_logits(self._h, C.byref(out)))
+        return np.ctypeslib.as_array(out, shape=(self.vocab_size,)).copy()
 
     def begin_decode_step(self, offset: int, sample: SamplingParameters) -> DecodeStep:
         sp = sample.params(self.vocab_size)

@@ -306,3 +306,80 @@ def test_persistent_abort_fails_both_steps_in_flight(gpu, models):
         assert not m.persistent_decode
         assert first == want[0]
         assert m.generate(toks, 8, GREEDY) == want
+
+
+@pytest.mark.parametrize("name", ["qwen3", "llama"])
+def test_verify_batch_matches_incremental_decode(gpu, models, name):
+    """verifyBatchMatchesIncrementalDecode (ModelTests.swift:201-230): each row of a T = 2..8 batch
+    (all_logits) gives the next-token logits of decoding the tokens one at a time: same argmax, max
+    difference < 0.1; and the batch rows against the oracle within the 2e-2 gate."""
+    d = models[name]
+    ids = prompt(40, 1000, seed=21)
+    o = 24
+    with mlxr.Transformer(d, context_length=512) as m:
+        ref = oracle.Model(d, m.max_seq)
+        for T in (2, 3, 5, 8):
+            m.forward(ids[:o], 0)
+            batch = ids[o:o + T]
+            rows = m.forward(batch, o, all_logits=True)
+            assert rows.shape == (T, m.vocab_size)
+            for i, t in enumerate(batch):
+                inc = m.forward(np.array([t], np.int32), o + i)
+                assert int(np.argmax(rows[i])) == int(np.argmax(inc)), (T, i)
+                assert np.max(np.abs(rows[i] - inc)) < 0.1, (T, i)
+            want = ref.forward(ids[:o + T], 0)
+            assert np.max(np.abs(rows[-1] - want)) < LOGIT_TOL, T
+
+
+def test_cancel_between_prefill_chunks(gpu, models):
+    """isCancelled is polled between chunks (Transformer.swift:1127,1233): a cancel after the first
+    2048-token chunk returns `cancelled`; the chunk's rows stay cached, so prefilling the rest at
+    offset 2048 gives the token of an uncancelled prefill."""
+    d = models["qwen3"]
+    ids = prompt(2100, 1000, seed=8)
+    with mlxr.Transformer(d, context_length=4096) as m:
+        want = m.prefill(ids, 0, GREEDY)
+        calls = []
+        with pytest.raises(mlxr.EngineError) as e:
+            m.prefill(ids, 0, GREEDY, is_cancelled=lambda: calls.append(1) or True)
+        assert e.value.case == "cancelled" and len(calls) == 1
+        assert m.prefill(ids[2048:], 2048, GREEDY) == want
+        with pytest.raises(mlxr.EngineError) as e:
+            m.forward(ids, 0, is_cancelled=lambda: True)
+        assert e.value.case == "cancelled"
+        assert np.argmax(m.forward(ids, 0, is_cancelled=lambda: False)) == want
+        assert m.prefill(ids[:100], 0, GREEDY, is_cancelled=lambda: True) == m.prefill(ids[:100], 0, GREEDY)   # one chunk: never polled
+
+
+def test_engine_speculative_greedy_is_identical(gpu, models):
+    """speculativeGreedyOutputIsIdentical (ModelTests.swift:411-434) on token ids: a prompt that
+    repeats itself, decoded plainly (GPU sampling, pipelined steps) and speculatively (prompt-lookup
+    drafts verified in batched passes): same tokens; drafts are accepted; a second turn reuses the
+    prompt cache and still matches a fresh engine."""
+    import engine
+    d = models["qwen3"]
+    base = list(prompt(24, 1000, seed=30))
+    ids = base * 3
+    with mlxr.Transformer(d, context_length=1024) as m:
+        eng = engine.InferenceEngine(m)
+        p = engine.GenerationParameters(temperature=0.0, repetition_penalty=1.0, max_tokens=48)
+        plain = eng.generate(ids, p)
+        spec = eng.generate(ids, engine.GenerationParameters(temperature=0.0, repetition_penalty=1.0, max_tokens=48, speculative=True))
+        tp = [e[1] for e in plain if e[0] == "token"]
+        ts = [e[1] for e in spec if e[0] == "token"]
+        st = spec[-1][1]
+        assert len(tp) == 48
+        amb = greedy_check(m, oracle.Model(d, m.max_seq), np.array(ids, np.int32), tp)
+        assert amb <= 2
+        if tp != ts:   # only where the oracle's top-2 margin cannot decide at the 2e-2 gate
+            i = next(k for k in range(len(tp)) if tp[k] != ts[k])
+            ref = oracle.Model(d, m.max_seq).forward(np.array(ids + tp[:i], np.int32), 0)
+            assert abs(ref[tp[i]] - ref[ts[i]]) < LOGIT_TOL
+        assert st.draft_tokens and st.accepted_draft_tokens > 0
+        follow = ids + tp + base[:5]
+        again = eng.generate(follow, p)
+        assert again[-1][1].cached_prompt_tokens > len(ids)
+        fresh = engine.InferenceEngine(m)
+        m.reset_write_tracking()
+        ref_turn = fresh.generate(follow, p)
+        assert [e[1] for e in again if e[0] == "token"] == [e[1] for e in ref_turn if e[0] == "token"]
