@@ -1,0 +1,244 @@
+"""The five benchmark configurations at their real shapes, on the MI355X against the CPU oracle.
+
+Mirrors the reference's model tests (Tests/MLXEngineTests/ModelTests.swift:50-255) on seeded
+synthetic weights (N(0, 0.02), MLX affine 4-bit g64 as mlxr_synth_write draws them):
+
+1. Qwen3-0.6B, all 28 layers, tied 151936-row lm_head: a 32-token prompt and 64 greedy steps on
+   the persistent decode step, every step's logits against the oracle teacher-forced.
+2. Qwen3-8B at full width (2 of its 36 layers; every layer has the same shapes): a 4096-token prefill,
+   then persistent decode steps over the GPU's own K/V cache loaded into the oracle.
+3. Llama-3-8B at full width (2 layers), a 2048-token prefill: last-row logits against the oracle's
+   fp64 forward.
+4. The matvec / GEMM sweep (K, N) x {3b g32, 4b g64, 6b g128, 8b g64} x T {1, 4, 512}, and the
+   3- and 6-bit code streams unpacked bit-exactly.
+5. Qwen2.5-32B at full width (2 layers, q/k/v biases), a 32768-token context with sparse decode
+   attention and a 30000-token prefix reused from a previous turn.
+
+Logit gate 2e-2 max-abs (north star); greedy tokens must agree wherever the oracle's top-2 margin
+exceeds that gate (a closer margin cannot decide the argmax at this tolerance, and is counted).
+"""
+import os
+import shutil
+import tempfile
+
+import numpy as np
+import pytest
+
+import configs
+import mlxr
+import oracle
+from qfix import SynthMatrix, bf16_round, bf16_to_f32, max_rel_err, unpack_codes
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 2e-2
+GREEDY = mlxr.SamplingParameters.greedy()
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def workdir():
+    d = tempfile.mkdtemp(prefix="mlxr_cfg_")
+    yield d
+    shutil.rmtree(d, ignore_errors=True)
+
+
+def synth(workdir, name, cfg, seed):
+    d = os.path.join(workdir, name)
+    if not os.path.exists(os.path.join(d, "config.json")):
+        say("synth", name)
+        mlxr.synth_write(cfg, seed=seed, directory=d)
+    return d
+
+
+def check_step(got, want, tok, what):
+    """Logits within the gate; the GPU's token is the oracle's argmax unless the top-2 margin is
+    below the gate. Returns 1 for an undecidable step."""
+    err = float(np.max(np.abs(got - want)))
+    assert err < LOGIT_TOL, (what, err)
+    best = int(np.argmax(want))
+    if tok == best:
+        return 0
+    assert want[best] - want[tok] < LOGIT_TOL, (what, tok, best)
+    return 1
+
+
+def test_config1_qwen3_0_6b_greedy(gpu, workdir):
+    d = synth(workdir, "qwen3-0.6b", configs.QWEN3_0_6B, 101)
+    ids = np.random.default_rng(1).integers(0, 151936, 32).astype(np.int32)
+    with mlxr.Transformer(d, context_length=1024) as m:
+        assert m.persistent_decode, "config 1 must run the persistent decode step"
+        ref = oracle.Model(d, m.max_seq)
+        tok = m.prefill(ids, 0, GREEDY)
+        want = ref.forward(ids, 0)
+        amb = check_step(m.forward(ids, 0), want, tok, "prefill")
+        m.prefill(ids, 0, GREEDY)
+        toks = [tok]
+        for i in range(63):
+            pos = 32 + i
+            st = m.begin_decode_step(pos, GREEDY)
+            nxt = m.finish(st)
+            got = m.step_logits()
+            want = ref.forward(np.array([toks[-1]], np.int32), pos)
+            amb += check_step(got, want, nxt, f"step {i}")
+            toks.append(nxt)
+        say("config 1: undecidable steps", amb)
+        assert amb <= 3
+        # the pipelined loop (two steps in flight) gives the same tokens
+        assert m.generate(ids, 64, GREEDY) == toks
+
+
+def test_config2_qwen3_8b_decode_at_4k(gpu, workdir):
+    d = synth(workdir, "qwen3-8b-2l", configs.with_layers(configs.QWEN3_8B, 2), 102)
+    n = 4096
+    ids = np.random.default_rng(2).integers(0, 151936, n).astype(np.int32)
+    with mlxr.Transformer(d, context_length=n + 256) as m:
+        assert m.persistent_decode
+        ref = oracle.Model(d, m.max_seq)
+        tok = m.prefill(ids, 0, GREEDY)
+        for layer in range(2):
+            ref.set_kv(layer, *m.read_kv(layer, n, 8, 128))
+        amb = 0
+        for i in range(4):
+            st = m.begin_decode_step(n + i, GREEDY)
+            nxt = m.finish(st)
+            got = m.step_logits()
+            want = ref.forward(np.array([tok], np.int32), n + i)
+            amb += check_step(got, want, nxt, f"step {i}")
+            tok = nxt
+        assert amb <= 1
+
+
+def test_config3_llama3_8b_prefill_2048(gpu, workdir):
+    d = synth(workdir, "llama3-8b-2l", configs.with_layers(configs.LLAMA3_8B, 2), 103)
+    ids = np.random.default_rng(3).integers(0, 128256, 2048).astype(np.int32)
+    with mlxr.Transformer(d, context_length=2304) as m:
+        got = m.forward(ids, 0)
+        ref = oracle.Model(d, m.max_seq)
+        say("config 3: oracle forward of 2048 tokens on", oracle.threads(), "threads")
+        want = ref.forward(ids, 0)
+        err = float(np.max(np.abs(got - want)))
+        say("config 3: max |d logit|", err)
+        assert err < LOGIT_TOL
+        tok = m.prefill(ids, 0, GREEDY)
+        check_step(got, want, tok, "prefill token")
+
+
+SWEEP_SHAPES = [(4096, 14336), (14336, 4096), (4096, 151936)]
+SWEEP_QUANT = [(3, 32), (4, 64), (6, 128), (8, 64)]
+
+
+def _x_bf16(rng, T, K):
+    """x ~ N(0, 1) rounded to bf16 values (stored fp32)."""
+    return bf16_to_f32(bf16_round(rng.normal(0, 1, (T, K)).astype(np.float32))).reshape(T, K)
+
+
+@pytest.mark.parametrize("bits,gs", SWEEP_QUANT, ids=[f"{b}b-g{g}" for b, g in SWEEP_QUANT])
+def test_config4_sweep(gpu, bits, gs):
+    """Every (K, N) at T = 1 (qmv) and T = 4 (qmm) against the fp64 product at 1e-3 relative; T = 512
+    (the prefill GEMM) on 512 output rows against the oracle's model of the GEMM's operand rounding at
+    1e-3 and within the operand-rounding bound of the fp64 product."""
+    for K, N in SWEEP_SHAPES:
+        say(f"config 4: K={K} N={N} {bits}-bit g{gs}")
+        full = SynthMatrix(gpu, N, K, bits, gs, seed=104, tensor_id=K + N)
+        rng = np.random.default_rng(K * 7 + bits)
+        x = _x_bf16(rng, 4, K)
+        q = full.oracle(oracle)
+        qm = (gpu.QMat * 1)(full.device(gpu))
+        # T = 1
+        dx = gpu.DeviceArray.from_numpy(x[0])
+        dy = gpu.DeviceArray.zeros((N,), np.float32)
+        gpu.check(gpu.lib.mlxr_k_qmv(qm, 1, K, bits, gs, 0, dx.ptr, None, 1e-6, dy.ptr, 0))
+        gpu.synchronize()
+        ref4 = q.matmul_f64(x)
+        assert max_rel_err(dy.numpy(), ref4[0]) < 1e-3, ("T=1", K, N)
+        # T = 4
+        dx4 = gpu.DeviceArray.from_numpy(x)
+        dy4 = gpu.DeviceArray.zeros((4, N), np.float32)
+        gpu.check(gpu.lib.mlxr_k_qmm(qm, 1, K, bits, gs, 0, 4, dx4.ptr, K, dy4.ptr, N))
+        gpu.synchronize()
+        assert max_rel_err(dy4.numpy(), ref4) < 1e-3, ("T=4", K, N)
+        # T = 512 on rows [r0, r0 + 512)
+        r0 = (N // 2) // 16 * 16
+        sub = full.rows(r0, r0 + 512)
+        xs = _x_bf16(rng, 512, K)
+        qs = (gpu.QMat * 1)(sub.device(gpu))
+        dxs = gpu.DeviceArray.from_numpy(xs)
+        dys = gpu.DeviceArray.zeros((512, 512), np.float32)
+        gpu.check(gpu.lib.mlxr_k_qgemm(qs, K, bits, gs, 0, 512, dxs.ptr, K, dys.ptr, 512))
+        gpu.synchronize()
+        got = dys.numpy()
+        so = sub.oracle(oracle)
+        assert max_rel_err(got, so.matmul_prefill(xs)) < 1e-3, ("T=512", K, N)
+        rel = 2.0 ** -10 if bits == 4 else 2.0 ** -8
+        bound = rel * (np.abs(xs).astype(np.float64) @ np.abs(sub_dense(sub)).T) + 1e-4
+        assert np.all(np.abs(got - so.matmul_f64(xs)) <= bound), ("T=512 bound", K, N)
+
+
+def sub_dense(m):
+    codes = np.stack([unpack_codes(m.packed[r], m.K, m.bits) for r in range(m.O)]).astype(np.float64)
+    g = np.repeat(np.arange(m.K // m.gs), m.gs)
+    return codes * m.scales[:, g].astype(np.float64) + m.biases[:, g].astype(np.float64)
+
+
+@pytest.mark.parametrize("bits", [3, 6])
+def test_config4_code_streams_bit_exact(gpu, bits):
+    """Non-power-of-two packing: the embedding gather with scale 1 and bias 0 returns the codes
+    themselves, which must equal the numpy bit-array unpack of the same bytes, row by row."""
+    K, N = 4096, 64
+    m = SynthMatrix(gpu, N, K, bits, 32 if bits == 3 else 128, seed=105, tensor_id=bits)
+    m.s_raw = np.full_like(m.s_raw, 0x3F80)   # bf16 1.0
+    m.b_raw = np.zeros_like(m.b_raw)
+    qm = (gpu.QMat * 1)(m.device(gpu))
+    ids = np.arange(N, dtype=np.int32)
+    did = gpu.DeviceArray.from_numpy(ids)
+    out = gpu.DeviceArray.zeros((N, K), np.float32)
+    gpu.check(gpu.lib.mlxr_k_qembed(qm, K, bits, m.gs, 0, did.ptr, N, out.ptr))
+    gpu.synchronize()
+    want = np.stack([unpack_codes(m.packed[r], K, bits) for r in range(N)]).astype(np.float32)
+    assert np.array_equal(out.numpy(), want)
+
+
+def test_config5_qwen2_5_32b_sparse_32k_prefix_reuse(gpu, workdir):
+    d = synth(workdir, "qwen2.5-32b-2l", configs.with_layers(configs.QWEN2_5_32B, 2), 106)
+    ctx, shared = 32768, 30000
+    rng = np.random.default_rng(5)
+    prefix = rng.integers(0, 152064, shared).astype(np.int32)
+    turn_a = np.concatenate([prefix, rng.integers(0, 152064, 1200).astype(np.int32)])
+    turn_b = np.concatenate([prefix, rng.integers(0, 152064, ctx - 8 - shared).astype(np.int32)])
+    sp = mlxr.SparseAttention()
+    with mlxr.Transformer(d, context_length=ctx, sparse=sp) as m:
+        assert m.sparse_available
+        n = len(turn_b)
+        # turn A, then turn B reusing the shared prefix
+        m.prefill(turn_a, 0, GREEDY)
+        common = m.reusable_prefix(shared, len(turn_a))
+        assert common == shared
+        tok = m.prefill(turn_b[common:], common, GREEDY)
+        reused = []
+        t = tok
+        for i in range(4):
+            t = m.finish(m.begin_decode_step(n + i, GREEDY))
+            reused.append((t, m.step_logits()))
+        # the oracle decodes over the GPU's cache with the same sparse budget
+        ref = oracle.Model(d, m.max_seq)
+        ref.set_sparse(True, top_k=sp.top_k, window=sp.window, sink=sp.sink, min_context=sp.min_context)
+        for layer in range(2):
+            ref.set_kv(layer, *m.read_kv(layer, n, 8, 128))
+        amb, prev = 0, tok
+        for i, (t, got) in enumerate(reused):
+            want = ref.forward(np.array([prev], np.int32), n + i)
+            amb += check_step(got, want, t, f"sparse step {i}")
+            prev = t
+        assert amb <= 1
+        # a fresh full prefill of turn B gives the same tokens (prefix reuse changes nothing)
+        m.reset_write_tracking()
+        assert m.prefill(turn_b, 0, GREEDY) == tok
+        t = tok
+        for i in range(4):
+            t = m.finish(m.begin_decode_step(n + i, GREEDY))
+            assert t == reused[i][0], i
+            assert np.max(np.abs(m.step_logits() - reused[i][1])) < LOGIT_TOL
