@@ -19,6 +19,8 @@ Extra objects on the JSON line:
 - step_roofline: the same accounting for the whole decode step (bytes per token at the mean context);
 - prefill: prompt tokens/s of the 4096-token prefill (the config's second metric), with its flops
   (prefill_flops) against the MFMA peak;
+- prefill_config3 / long_config5: the `--mode prefill` and `--mode long`
+  results, each with its own roofline, measured in the same run after the decode workload;
 - cpu_baseline: the CPU oracle (C restatement of the reference's semantics, all host cores) timed on
   a bounded sample: decode steps at the same context, starting from the GPU-built KV cache.
 """
@@ -125,7 +127,7 @@ def prefill_main(a):
                      "frac": round(tfs / MFMA_PEAK_TFS, 4), "traffic": None, "flops": int(fl)},
     }
     model.close()
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def sweep_main(a):
@@ -241,7 +243,7 @@ def long_main(a):
         "metric": "decode tok/s (bs1, 32B-shape 4-bit g64, 32K context, sparse attention) + % HBM roofline",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(el * 1e3 / a.steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u4 weights (affine g64, bf16 scale/bias), fp32 activations, bf16 KV",
+        "dtype": "u4 weights (affine g64, bf16 scale/bias); x as f16 hi+lo MFMA operands (fp32-level), fp32 accumulate, bf16 KV",
         "data": "synthetic: random-init weights N(0,0.02) from a seed, uniform random ids",
         "config": {"workload": f"{a.config}: {total}-token context, {reuse}-token reused prefix, sparse decode (configs[4])",
                    "model": a.config, "global_batch": 1, "seq_len": total + a.warmup + a.steps, "parallelism": "none (1 GPU)"},
@@ -253,7 +255,7 @@ def long_main(a):
         "first_tokens": toks[:8],
     }
     model.close()
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def cpu_baseline(d, model, cfg, ctx, tokens, budget_s):
@@ -291,6 +293,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=2)
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="decode only: skip the prefill_config3 and long_config5 sub-objects (configs[2] and [4])")
     ap.add_argument("--kernel-iters", type=int, default=360)
     ap.add_argument("--step-iters", type=int, default=64)
     ap.add_argument("--no-graphs", action="store_true",
@@ -328,7 +332,8 @@ def main():
             a.steps = 5
         if "--warmup" not in sys.argv:
             a.warmup = 1
-        return prefill_main(a)
+        print(json.dumps(prefill_main(a)), flush=True)
+        return
     if a.mode == "sweep":
         return sweep_main(a)
     if a.mode == "long":
@@ -340,7 +345,8 @@ def main():
             a.steps = 128
         if "--warmup" not in sys.argv:
             a.warmup = 4
-        return long_main(a)
+        print(json.dumps(long_main(a)), flush=True)
+        return
     cfg = configs.CONFIGS[a.config]
     d = model_dir(a.config, a.seed)
     need = a.context + a.warmup + a.steps + a.step_iters + 16
@@ -411,7 +417,8 @@ def main():
         "metric": "decode tok/s (bs1, 8B-shape 4-bit g64) + % HBM roofline; prefill tok/s",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(el * 1e3 / a.steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u4 weights (affine g64, bf16 scale/bias), fp32 activations, bf16 KV",
+        "dtype": "u4 weights (affine g64, bf16 scale/bias); x as f16 hi+lo MFMA operands (fp32-level, 1e-3 gate), "
+                 "fp32 accumulate, bf16 KV",
         "data": "synthetic: random-init weights N(0,0.02) from a seed, uniform random prompt ids",
         "config": {"workload": f"{a.config}: {a.context}-token prefilled context + greedy decode (configs[1])",
                    "model": a.config, "global_batch": 1, "seq_len": a.context + a.warmup + a.steps, "parallelism": "none (1 GPU)"},
@@ -432,7 +439,20 @@ def main():
     if not a.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(d, model, cfg, pos + a.steps, a.cpu_tokens, a.cpu_budget)
     model.close()
+    if not a.no_extra:
+        # the other two model workloads, measured in the same run (short: a few seconds of GPU time each)
+        pa = argparse.Namespace(**vars(a))
+        pa.config, pa.context, pa.steps, pa.warmup = "llama3-8b", 2048, 5, 1
+        result["prefill_config3"] = _sub(prefill_main(pa))
+        la = argparse.Namespace(**vars(a))
+        la.config, la.context, la.steps, la.warmup = "qwen2.5-32b", 32768, 64, 4
+        result["long_config5"] = _sub(long_main(la))
     print(json.dumps(result), flush=True)
+
+
+def _sub(r):
+    """A workload's result as a sub-object of the main line (without the fields the line already has)."""
+    return {k: v for k, v in r.items() if k not in ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "data")}
 
 
 if __name__ == "__main__":
