@@ -247,6 +247,15 @@ int mlxr_k_sparse_select(const float* scores, int rows, int b0, int nb, int p, i
  * rng device u64[2]. */
 int mlxr_k_sample(float* logits, int V, int32_t* hist, int32_t* status, uint64_t* rng, int pos,
                   const mlxr_sample_params* sp);
+/* mlxr_k_sample without any allocation: no counterpart in the reference. For callers that cannot
+ * allocate device memory (code under stream capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The per-block partials and the position word live in a fixed 8.25 KiB device array
+ * of the library (one copy per GPU, held until the process ends) instead of library-allocated
+ * buffers; V <= 262144 (larger: MLXR_E_INVALID_ARG, nothing launched). Kernels go on `stream`
+ * (a hipStream_t; NULL: the null stream) and the call returns without waiting. Every call on one GPU
+ * shares its array: calls that overlap on one GPU race. Same results as mlxr_k_sample. */
+int mlxr_k_sample_noalloc(float* logits, int V, int32_t* hist, int32_t* status, uint64_t* rng, int pos,
+                          const mlxr_sample_params* sp, void* stream);
 
 #ifdef __cplusplus
 }

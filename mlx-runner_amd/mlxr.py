@@ -104,6 +104,7 @@ def _load():
         "mlxr_k_sparse_score": (I, [P, P, I, I, I, I, I, I, P]),
         "mlxr_k_sparse_select": (I, [P, I, I, I, I, I, I, I, P, I]),
         "mlxr_k_sample": (I, [P, I, P, P, P, I, C.POINTER(SampleParams)]),
+        "mlxr_k_sample_noalloc": (I, [P, I, P, P, P, I, C.POINTER(SampleParams), P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
