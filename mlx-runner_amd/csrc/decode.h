@@ -88,5 +88,6 @@ int mega_blocks_per_cu(const MegaArgs& a, size_t lds);   // resident workgroups 
 int mega_threads();
 int mega_tiles_per_wg_cap();   // 16-row tiles of one phase one workgroup may own
 int mega_wg_row_cap();     // rows of an accumulate phase one workgroup may own
+int mega_split_cap();      // key ranges per KV head (workgroups / KV heads) the attention merge handles
 
 }  // namespace mlxr

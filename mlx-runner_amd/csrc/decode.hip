@@ -34,7 +34,7 @@ namespace mlxr {
 
 constexpr int MK_MAXG = 8;
 constexpr int MK_HOWN = 256;         // residual rows of one workgroup in an accumulate phase (max)
-constexpr int MK_MERGE_B = 32;       // partials one merging thread has in flight
+constexpr int MK_MERGE_L = 2;        // attention partials of one merged output per lane (nsplit <= 128)
 
 // ------------------------------------------------------------------------------- coherence
 // Data one workgroup writes and another reads within the launch (h, q|k|v, attention partials and
@@ -174,14 +174,19 @@ __device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, i
 // MK_LDB 16-byte loads (two pairs each) per thread in flight per batch, each polled until its tag
 // appears; returns this thread's sum of squares and max |x|.
 constexpr int MK_LDB = 4;
+#ifndef MK_LATE
+#define MK_LATE 0
+#endif
+constexpr bool MK_LATE_PREFETCH = MK_LATE;   // issue a phase's weight prefetch once its input is in
+template <int NB = MK_LDB>
 __device__ __forceinline__ float2 fetch_to_lds(const uint2* src, int K, unsigned tag, const TagWait& tw, float* xf) {
     float ss = 0.0f, mx = 0.0f;
     const int K2 = K >> 1;
     __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint2*>(src), 0, K * 8, 0x00020000);
-    for (int base = 0; base < K2; base += MK_THREADS * MK_LDB) {
-        coh_u32x4 v[MK_LDB];
+    for (int base = 0; base < K2; base += MK_THREADS * NB) {
+        coh_u32x4 v[NB];
 #pragma unroll
-        for (int j = 0; j < MK_LDB; j++) {
+        for (int j = 0; j < NB; j++) {
             const int i2 = min(base + j * MK_THREADS + (int)threadIdx.x, K2 - 1);
             v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, i2 * 16, 0, 16);
         }
@@ -189,19 +194,19 @@ __device__ __forceinline__ float2 fetch_to_lds(const uint2* src, int K, unsigned
         for (unsigned spins = 0;;) {
             bool ready = true;
 #pragma unroll
-            for (int j = 0; j < MK_LDB; j++) {
+            for (int j = 0; j < NB; j++) {
                 const int i2 = base + j * MK_THREADS + (int)threadIdx.x;
                 ready &= i2 >= K2 || (v[j].y == tag && v[j].w == tag);
             }
             if (ready || !tag_spin(tw, spins)) break;
 #pragma unroll
-            for (int j = 0; j < MK_LDB; j++) {
+            for (int j = 0; j < NB; j++) {
                 const int i2 = base + j * MK_THREADS + (int)threadIdx.x;
                 if (i2 < K2 && (v[j].y != tag || v[j].w != tag)) v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, i2 * 16, 0, 16);
             }
         }
 #pragma unroll
-        for (int j = 0; j < MK_LDB; j++) {
+        for (int j = 0; j < NB; j++) {
             const int i2 = base + j * MK_THREADS + (int)threadIdx.x;
             if (i2 < K2) {
                 const float x0 = __uint_as_float(v[j].x), x1 = __uint_as_float(v[j].z);
@@ -268,12 +273,13 @@ __device__ __forceinline__ float norm_to_lds(const uint2* src, unsigned tag, con
 
 // x := src packed to the f16 matvec layout, plus this workgroup's residual rows h[row0 .. row1)
 // into hown (for the accumulate epilogue, so no row needs its own round trip).
+template <int NB = MK_LDB>
 __device__ __forceinline__ float copy_to_lds(const uint2* src, unsigned tag, const TagWait& tw, int K, const MvLds& L, int gsh,
                                              const uint2* h, unsigned htag, int H, int row0, int row1, float* red) {
     const int n = row1 - row0;
     float hv = 0.0f;
     if ((int)threadIdx.x < n) hv = ld_tag1(h, row0 + threadIdx.x, H, htag, tw);
-    const float mx = fetch_to_lds(src, K, tag, tw, L.xf).y;
+    const float mx = fetch_to_lds<NB>(src, K, tag, tw, L.xf).y;
     if ((int)threadIdx.x < n) L.hown[threadIdx.x] = hv;
     return pack_x16(L.xf, K, block_max(mx, red), L, gsh);
 }
@@ -522,6 +528,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             if (li == 0 && a.stall && wg == 0) itag ^= 0x80000000u;   // test hook: a tag no launch writes
             const float us = norm_to_lds(a.hA, itag, tw, ly.in_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 0);
+            if (MK_LATE_PREFETCH && li > 0) mv_prefetch<FB>(ly.qkv, wg, nwg, wave, lane, ring);
             mv_run<FB, true>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkvT, tag_of(2 + 5 * li), nullptr, nullptr, red, redi);
         }
@@ -834,50 +841,45 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             lds_barrier();
             if (tid == 0) st_tag(a.part_ready + kvh * nsplit + split, 0.0f, atag);
             prof_mark(a.prof, 512 + 8 * li + 3);
-            if (split == nsplit - 1) {
-                // the last range (the fewest keys) merges the KV head's partials in range order once
-                // every range's ready tag is up: all loads of the merge in one round trip, the weights
-                // exp(m_s - M) computed by every (head, dim) thread from the staged maxima
-                if (tid < nsplit) ld_tag1(a.part_ready, kvh * nsplit + tid, nKV * nsplit, atag, tw);
-                lds_barrier();
-                float* wts = wacc;                                  // [G][nsplit] maxima
-                float* lsv = wacc + MK_MAXG * 64;                   // [G][nsplit] sums
-                for (int idx = tid; idx < G * nsplit; idx += MK_THREADS) {
-                    wts[idx] = ld_coh1(pm, prow + idx, P);
-                    lsv[idx] = ld_coh1(pl, prow + idx, P);
-                }
-                for (int idx0 = 0; idx0 < G * 128; idx0 += MK_THREADS) {
-                    const int idx = idx0 + tid;
-                    const int g = min(idx >> 7, G - 1), d = idx & 127;
+            // every range of the KV head merges a slice of its G * 128 outputs once all the head's
+            // ranges are stored: ceil(G * 128 / nsplit) outputs here, one wave per output, the
+            // nsplit partials of an output over the wave's lanes (one round trip of small loads)
+            if (tid < nsplit) ld_tag1(a.part_ready, kvh * nsplit + tid, nKV * nsplit, atag, tw);
+            lds_barrier();
+            {
+                const int opw = (G * 128 + nsplit - 1) / nsplit;
+                const int o0 = split * opw, o1 = min(G * 128, o0 + opw);
+                for (int o = o0 + wave; o < o1; o += MK_WAVES) {
+                    const int g = o >> 7, d = o & 127;
                     const int rb = prow + g * nsplit;
-                    float v[MK_MERGE_B];
+                    float mv[MK_MERGE_L], lv[MK_MERGE_L], av[MK_MERGE_L];
 #pragma unroll
-                    for (int q = 0; q < MK_MERGE_B; q++) v[q] = ld_coh1(pa, (rb + min(q, nsplit - 1)) * 128 + d, P * 128);
-                    lds_barrier();                                // the maxima and sums are staged
-                    float M = -1e30f;
-                    for (int s = 0; s < nsplit; s++) M = fmaxf(M, wts[g * nsplit + s]);
-                    float o = 0.0f, Ls = 0.0f;
-                    for (int s0 = 0; s0 < nsplit; s0 += MK_MERGE_B) {
-                        if (s0 > 0) {
-#pragma unroll
-                            for (int q = 0; q < MK_MERGE_B; q++) v[q] = ld_coh1(pa, (rb + min(s0 + q, nsplit - 1)) * 128 + d, P * 128);
-                        }
-#pragma unroll
-                        for (int q = 0; q < MK_MERGE_B; q++) {
-                            const int s = s0 + q;
-                            if (s < nsplit) {
-                                const float f = expf(wts[g * nsplit + s] - M);
-                                o += v[q] * f;
-                                Ls += lsv[g * nsplit + s] * f;
-                            }
-                        }
+                    for (int q = 0; q < MK_MERGE_L; q++) {
+                        const int sp = lane + 64 * q;
+                        const bool ok = sp < nsplit;
+                        const int r = rb + (ok ? sp : 0);
+                        mv[q] = ok ? ld_coh1(pm, r, P) : -1e30f;
+                        lv[q] = ok ? ld_coh1(pl, r, P) : 0.0f;
+                        av[q] = ok ? ld_coh1(pa, r * 128 + d, P * 128) : 0.0f;
                     }
-                    if (idx < G * 128) st_tag(a.attnT + (kvh * G + g) * 128 + d, o * (1.0f / Ls), atag);
+                    float M = mv[0];
+#pragma unroll
+                    for (int q = 1; q < MK_MERGE_L; q++) M = fmaxf(M, mv[q]);
+                    M = wave_max(M);
+                    float on = 0.0f, ls = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < MK_MERGE_L; q++) {
+                        const float f = expf(mv[q] - M);
+                        on += av[q] * f;
+                        ls += lv[q] * f;
+                    }
+                    on = wave_sum(on); ls = wave_sum(ls);
+                    if (lane == 0) st_tag(a.attnT + (kvh * G + g) * 128 + d, on * (1.0f / ls), atag);
                 }
             }
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
-        mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
+        if (!MK_LATE_PREFETCH) mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- C: o_proj, h += W_o attn
@@ -886,43 +888,51 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const float us = copy_to_lds(a.attnT, tag_of(3 + 5 * li), tw, nH * D, ml, FB == 4 ? 5 : 6, a.hA,
                                          tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), H, 16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 4);
+            if (MK_LATE_PREFETCH) mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
             mv_run<FB, true>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.hB, tag_of(4 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
         nwr = norm_w_load(ly.post_norm, H);
-        mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
+        if (!MK_LATE_PREFETCH) mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- D: gate|up with SiLU
         {
             const float us = norm_to_lds(a.hB, tag_of(4 + 5 * li), tw, ly.post_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 5);
+            if (MK_LATE_PREFETCH) mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
             mv_run<FB, true>(ly.gu, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_GATED, FB>(ly.gu, us, wg, nwg, ml.part, a.mlpT, tag_of(5 + 5 * li), nullptr, nullptr, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
-        mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
+        if (!MK_LATE_PREFETCH) mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- E: down, h += W_d mlp
         {
             const MvGeom<FB> gg = mv_geom<FB>(ly.down, wg, nwg, 0);
-            const float us = copy_to_lds(a.mlpT, tag_of(5 + 5 * li), tw, a.I, ml, FB == 4 ? 5 : 6, a.hB, tag_of(4 + 5 * li), H,
+            // the intermediate vector in two round trips (12288 values: 8 loads per thread per batch; 12
+            // would do it in one but spill)
+            const float us = copy_to_lds<8>(a.mlpT, tag_of(5 + 5 * li), tw, a.I, ml, FB == 4 ? 5 : 6, a.hB, tag_of(4 + 5 * li), H,
                                          16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 6);
+            if (MK_LATE_PREFETCH) mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
             mv_run<FB, true>(ly.down, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.hA, tag_of(6 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
         nwr = norm_w_load(li + 1 < a.L ? ldesc[li + 1].in_norm : a.final_norm, H);
-        if (li + 1 < a.L) mv_prefetch<FB>(ldesc[li + 1].qkv, wg, nwg, wave, lane, ring);
-        else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
+        if (!MK_LATE_PREFETCH) {
+            if (li + 1 < a.L) mv_prefetch<FB>(ldesc[li + 1].qkv, wg, nwg, wave, lane, ring);
+            else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
+        }
         prof_mark(a.prof, 2 * epoch - 1);
     }
 
     // ---- lm_head with the final norm, logits and the greedy token
     const float us = norm_to_lds(a.hA, tag_of(6 + 5 * (a.L - 1)), tw, a.final_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
+    if (MK_LATE_PREFETCH) mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
     mv_run<FB, true>(a.head, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
     const MvResult best = mv_finish<OUT_ARGMAX, FB>(a.head, us, wg, nwg, ml.part, nullptr, 0u, a.logits, nullptr, red, redi);
     prof_mark(a.prof, 2 * epoch);
@@ -1068,5 +1078,6 @@ hipError_t mega_set_lds_limit(size_t lds) {
 int mega_threads() { return MK_THREADS; }
 int mega_tiles_per_wg_cap() { return MK_TPW; }
 int mega_wg_row_cap() { return MK_HOWN; }
+int mega_split_cap() { return 64 * MK_MERGE_L; }
 
 }  // namespace mlxr

@@ -392,6 +392,7 @@ static int mega_setup(Model* m) {
     const int nsplit = nwg / c.nKV;
     const int max_keys = (m->max_seq + nsplit - 1) / nsplit;
     if ((c.nH / c.nKV) * nsplit > 512) return no("too many attention partials per KV head");
+    if (nsplit > mega_split_cap()) return no("too many key ranges per KV head");
     {
         const int tmax = std::max({(c.V + 15) / 16, ((c.nH + 2 * c.nKV) * c.D + 15) / 16, (c.I + 7) / 8, (c.H + 15) / 16});
         if ((tmax + nwg - 1) / nwg > mega_tiles_per_wg_cap()) return no("too many row tiles per workgroup");
