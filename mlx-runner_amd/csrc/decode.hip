@@ -174,10 +174,6 @@ __device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, i
 // MK_LDB 16-byte loads (two pairs each) per thread in flight per batch, each polled until its tag
 // appears; returns this thread's sum of squares and max |x|.
 constexpr int MK_LDB = 4;
-#ifndef MK_LATE
-#define MK_LATE 0
-#endif
-constexpr bool MK_LATE_PREFETCH = MK_LATE;   // issue a phase's weight prefetch once its input is in
 template <int NB = MK_LDB>
 __device__ __forceinline__ float2 fetch_to_lds(const uint2* src, int K, unsigned tag, const TagWait& tw, float* xf) {
     float ss = 0.0f, mx = 0.0f;
@@ -528,7 +524,6 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             if (li == 0 && a.stall && wg == 0) itag ^= 0x80000000u;   // test hook: a tag no launch writes
             const float us = norm_to_lds(a.hA, itag, tw, ly.in_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 0);
-            if (MK_LATE_PREFETCH && li > 0) mv_prefetch<FB>(ly.qkv, wg, nwg, wave, lane, ring);
             mv_run<FB, true>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkvT, tag_of(2 + 5 * li), nullptr, nullptr, red, redi);
         }
@@ -879,7 +874,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             }
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
-        if (!MK_LATE_PREFETCH) mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
+        mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- C: o_proj, h += W_o attn
@@ -888,25 +883,23 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const float us = copy_to_lds(a.attnT, tag_of(3 + 5 * li), tw, nH * D, ml, FB == 4 ? 5 : 6, a.hA,
                                          tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), H, 16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 4);
-            if (MK_LATE_PREFETCH) mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
             mv_run<FB, true>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.hB, tag_of(4 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
         nwr = norm_w_load(ly.post_norm, H);
-        if (!MK_LATE_PREFETCH) mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
+        mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- D: gate|up with SiLU
         {
             const float us = norm_to_lds(a.hB, tag_of(4 + 5 * li), tw, ly.post_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 5);
-            if (MK_LATE_PREFETCH) mv_prefetch<FB>(ly.gu, wg, nwg, wave, lane, ring);
             mv_run<FB, true>(ly.gu, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_GATED, FB>(ly.gu, us, wg, nwg, ml.part, a.mlpT, tag_of(5 + 5 * li), nullptr, nullptr, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
-        if (!MK_LATE_PREFETCH) mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
+        mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- E: down, h += W_d mlp
@@ -917,22 +910,18 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const float us = copy_to_lds<8>(a.mlpT, tag_of(5 + 5 * li), tw, a.I, ml, FB == 4 ? 5 : 6, a.hB, tag_of(4 + 5 * li), H,
                                          16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 6);
-            if (MK_LATE_PREFETCH) mv_prefetch<FB>(ly.down, wg, nwg, wave, lane, ring);
             mv_run<FB, true>(ly.down, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
             mv_finish<OUT_ADD, FB>(ly.down, us, wg, nwg, ml.part, a.hA, tag_of(6 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
         nwr = norm_w_load(li + 1 < a.L ? ldesc[li + 1].in_norm : a.final_norm, H);
-        if (!MK_LATE_PREFETCH) {
-            if (li + 1 < a.L) mv_prefetch<FB>(ldesc[li + 1].qkv, wg, nwg, wave, lane, ring);
-            else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
-        }
+        if (li + 1 < a.L) mv_prefetch<FB>(ldesc[li + 1].qkv, wg, nwg, wave, lane, ring);
+        else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
     }
 
     // ---- lm_head with the final norm, logits and the greedy token
     const float us = norm_to_lds(a.hA, tag_of(6 + 5 * (a.L - 1)), tw, a.final_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
-    if (MK_LATE_PREFETCH) mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
     mv_run<FB, true>(a.head, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
     const MvResult best = mv_finish<OUT_ARGMAX, FB>(a.head, us, wg, nwg, ml.part, nullptr, 0u, a.logits, nullptr, red, redi);
     prof_mark(a.prof, 2 * epoch);
