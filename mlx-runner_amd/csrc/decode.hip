@@ -461,7 +461,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
     ml.xf = ml.hown + MK_HOWN;                    // matvec input, f32 staging (Kmax floats)
     ml.xh = ml.xf + Kmax;                         // matvec input, f16 layout (Kmax / 32 chunks)
     ml.gsum = ml.xh + (Kmax >> 5) * XH_STRIDE;    // per-group sums of x (Kmax / 32 at most)
-    ml.zero16 = ml.gsum + (((Kmax >> 5) + 3) & ~3);   // 16 bytes of zeros (16-byte aligned)
+    ml.zero16 = ml.gsum + (((Kmax >> 5) + 3) & ~3);   // MV_ZERO floats of zeros (16-byte aligned)
     __shared__ int redi[MK_WAVES];
     Ring<FB> ring;
     KVPrefetch kvpf;
@@ -1018,7 +1018,7 @@ hipError_t launch_dpack(const DPackSrc& s, uint8_t* out, hipStream_t st) {
 size_t mega_lds_bytes(const MegaArgs& a, int max_keys_per_split) {
     const int G = a.nH / a.nKV;
     const size_t kmax = (size_t)std::max(a.H, std::max(a.I, a.nH * 128));
-    size_t mv = (kmax + kmax / 32 * XH_STRIDE + (kmax / 32 + 3) / 4 * 4 + 4 + MK_HOWN + MK_TPW * MK_WAVES * 16) * 4;
+    size_t mv = (kmax + kmax / 32 * XH_STRIDE + (kmax / 32 + 3) / 4 * 4 + MV_ZERO + MK_HOWN + MK_TPW * MK_WAVES * 16) * 4;
     // attention: q hi/lo image, new k/v, rope scratch, exchanges, probabilities, P.V partials, merge scale
     size_t att = 2 * 16 * 128 * 2 + 2 * 128 * 2 + (size_t)(4 * 128 + 2 * MK_WAVES * 16 + 32 + MK_MAXG * ATT_PPS +
                  MK_WAVES * MK_MAXG * 128 + MK_MAXG) * 4;

@@ -54,7 +54,7 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
     L.xh = lds;
     L.gsum = L.xh + (K >> 5) * XH_STRIDE;
     L.zero16 = L.gsum + (((K >> GSH) + 3) & ~3);   // 16-byte aligned
-    L.part = L.zero16 + 4;
+    L.part = L.zero16 + MV_ZERO;
     float* red = L.part + tpw * MK_WAVES * 16;
     const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     Ring<FB> ring;
@@ -190,7 +190,7 @@ hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* no
     const int nwg = std::min(p.tiles, 4 * cus);
     const int tpw = (p.tiles + nwg - 1) / nwg;
     if (tpw > MK_TPW) return hipErrorInvalidValue;
-    const size_t lds = sizeof(float) * ((size_t)(p.K >> 5) * XH_STRIDE + (((p.K / p.gs) + 3) & ~3) + 4 + (size_t)tpw * MK_WAVES * 16 + 16);
+    const size_t lds = sizeof(float) * ((size_t)(p.K >> 5) * XH_STRIDE + (((p.K / p.gs) + 3) & ~3) + MV_ZERO + (size_t)tpw * MK_WAVES * 16 + 16);
     if (lds > DMV_MAX_LDS) return hipErrorInvalidValue;
     const bool fb4 = p.gs == 32;
     switch (mode) {

@@ -111,6 +111,7 @@ __device__ __forceinline__ f16x8_t a_operand(uint32_t w) {
 // (the masked B operand).
 constexpr int XH_STRIDE = 32;          // floats per chunk
 constexpr int XH_LO = 16;              // floats from a chunk's hi slots to its lo slots
+constexpr int MV_ZERO = 64;            // floats of zeros (a B operand read of any chunk of a group in it reads zeros)
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
@@ -125,7 +126,7 @@ struct MvLds { float* xf; float* xh; float* gsum; float* zero16; float* hown; fl
 template <typename LD>
 __device__ __forceinline__ float pack_x16_from(const LD& ld, int K, float gmax, const MvLds& L, int gsh) {
     float* xh = L.xh; float* gsum = L.gsum;
-    if (threadIdx.x < 4) L.zero16[threadIdx.x] = 0.0f;
+    if (threadIdx.x < MV_ZERO) L.zero16[threadIdx.x] = 0.0f;
     int ex = 0;
     if (gmax > 0.0f && gmax <= 3.0e38f) frexpf(gmax, &ex);
     const int e = min(max(14 - ex, -100), 100);
@@ -222,9 +223,13 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
                 };
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
+                    // one base per group (the j of a group share it), the chunk's place as a constant
+                    // offset: the group's hi slots, its lo slots, or the zero region shifted back by
+                    // the group's offset, so that every chunk of the group reads zeros there
                     const int gcol = (4 * k + j) / CPG;                        // the chunk's group column
-                    const float* bp = col == gcol ? xb + (4 * k + j) * XH_STRIDE
-                                    : col == (gcol ^ 8) ? xb + (4 * k + j) * XH_STRIDE + XH_LO : zero16;
+                    const int g0 = gcol * CPG * XH_STRIDE;                    // the group's first chunk
+                    const float* gb = col == gcol ? xb : col == (gcol ^ 8) ? xb + XH_LO : zero16 - g0;
+                    const float* bp = gb + g0 + (4 * k + j - gcol * CPG) * XH_STRIDE;
                     b[j] = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(bp));
                     if constexpr (!STRAIGHT) mfma(j, b[j]);   // each operand read right before its MFMA
                 }

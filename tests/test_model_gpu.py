@@ -383,3 +383,42 @@ def test_engine_speculative_greedy_is_identical(gpu, models):
         m.reset_write_tracking()
         ref_turn = fresh.generate(follow, p)
         assert [e[1] for e in again if e[0] == "token"] == [e[1] for e in ref_turn if e[0] == "token"]
+
+
+def test_checkpoint_layouts_load_identically(gpu, models, tmp_path):
+    """Loader parity across the checkpoint layouts MLX-community repositories use (GPU.swift:330-357,
+    Transformer.swift:48-111): the same tensors re-written by an independent writer as two shards
+    with model.safetensors.index.json, in another tensor order, with a multimodal
+    `language_model.` prefix, extra config fields and an unused extra tensor, give bit-identical
+    logits to the single-file model. (No real checkpoint is available offline: the layouts are built
+    from the synthetic model's own tensors.)"""
+    import json
+    from qfix import read_safetensors, write_safetensors
+    d = models["qwen2"]
+    src = read_safetensors(os.path.join(d, "model.safetensors"))
+    cfg = json.load(open(os.path.join(d, "config.json")))
+    dt_of = {np.uint32: "U32", np.uint16: "BF16", np.float16: "F16", np.float32: "F32"}
+    dtypes = {k: dt_of[v.dtype.type] for k, v in src.items()}
+    out = str(tmp_path / "sharded")
+    os.makedirs(out)
+    names = sorted(src, reverse=True)
+    renamed = {("language_model." + k if not k.startswith("lm_head") else "language_model." + k): k for k in names}
+    half = len(names) // 2
+    shards = {"model-00001-of-00002.safetensors": names[:half], "model-00002-of-00002.safetensors": names[half:]}
+    weight_map = {}
+    for fn, ks in shards.items():
+        tens = {[r for r, o in renamed.items() if o == k][0]: src[k] for k in ks}
+        dts = {[r for r, o in renamed.items() if o == k][0]: dtypes[k] for k in ks}
+        if fn.startswith("model-00002"):
+            tens["language_model.model.rotary_emb.inv_freq"] = np.ones(64, np.float32)
+            dts["language_model.model.rotary_emb.inv_freq"] = "F32"
+        write_safetensors(os.path.join(out, fn), tens, dts)
+        weight_map.update({k: fn for k in tens})
+    json.dump({"metadata": {"total_size": 0}, "weight_map": weight_map}, open(os.path.join(out, "model.safetensors.index.json"), "w"))
+    cfg2 = dict(cfg, architectures=["Qwen2ForCausalLM"], torch_dtype="bfloat16", transformers_version="4.51.0")
+    json.dump(cfg2, open(os.path.join(out, "config.json"), "w"))
+    toks = prompt(33, 1000, seed=44)
+    with mlxr.Transformer(d, context_length=256) as a, mlxr.Transformer(out, context_length=256) as b:
+        la, lb = a.forward(toks, 0), b.forward(toks, 0)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        assert a.generate(toks, 8, GREEDY) == b.generate(toks, 8, GREEDY)
