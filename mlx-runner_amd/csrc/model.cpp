@@ -1080,6 +1080,23 @@ int model_profile(Model* m, const char* kind_c, int iters, int context, double* 
     } else if (kind == "down") {
         b = lin_bytes_of(m->layers[0].down) + (int64_t)c.I * 4 + (int64_t)c.H * 4 * 2;
         launch = [&](int i) { const Layer& ly = m->layers[i % c.L]; return (int)launch_qmv(qmv_args(&ly.down, 1, m->mlp, nullptr, 0, m->tmp, EPI_ADD), s); };
+    } else if (kind.size() > 1 && kind[0] == 't' && (kind == "tqkv" || kind == "to" || kind == "tgateup" || kind == "tdown") &&
+               (int)m->tile_layers.size() == c.L) {
+        // the same projections on the repacked-tile matvec of the kernel-per-op step (dpack_mv_kernel)
+        const Layer& l0 = m->layers[0];
+        const std::string k = kind.substr(1);
+        b = k == "qkv" ? lin_bytes_of(l0.q) + lin_bytes_of(l0.k) + lin_bytes_of(l0.v) + (int64_t)c.H * 4 * 2 + (int64_t)m->qkv_cols * 4
+          : k == "o" ? lin_bytes_of(l0.o) + (int64_t)c.nH * c.D * 4 + (int64_t)c.H * 4 * 2
+          : k == "gateup" ? lin_bytes_of(l0.gate) + lin_bytes_of(l0.up) + (int64_t)c.H * 4 * 2 + (int64_t)c.I * 4
+          : lin_bytes_of(l0.down) + (int64_t)c.I * 4 + (int64_t)c.H * 4 * 2;
+        launch = [&, k](int i) {
+            const LayerDev& t = m->tile_layers[i % c.L];
+            const Layer& ly = m->layers[i % c.L];
+            if (k == "qkv") return (int)launch_dpack_mv(t.qkv, m->h, ly.in_norm, c.eps, m->qkv, 0, s);
+            if (k == "o") return (int)launch_dpack_mv(t.o, m->attn, nullptr, 0, m->tmp, 1, s);
+            if (k == "gateup") return (int)launch_dpack_mv(t.gu, m->h, ly.post_norm, c.eps, m->mlp, 2, s);
+            return (int)launch_dpack_mv(t.down, m->mlp, nullptr, 0, m->tmp, 1, s);
+        };
     } else if (kind == "head") {
         b = lin_bytes_of(m->head) + (int64_t)c.H * 4 * 2 + (int64_t)c.V * 4;
         launch = [&](int) { return (int)launch_qmv(qmv_args(&m->head, 1, m->h, m->final_norm, c.eps, m->logits, EPI_STORE), s); };
