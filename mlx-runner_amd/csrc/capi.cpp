@@ -288,8 +288,10 @@ int mlxr_k_qmv_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode
     MvPhaseDesc d; uint8_t* code;
     if (int rc = tiles_pack(parts, nparts, K, gs, mode == 2, d, code)) return rc;
     if (!dpack_mv_supported(d)) { hipFree(code); return set_error(MLXR_E_UNSUPPORTED, "matvec over repacked tiles: K too large"); }
+    // the scratch of the long-input split (2 * rows floats), as the model's kernel-per-op step passes it
+    if (int rc = ensure_buf(g_part, g_part_floats, (size_t)2 * d.rows)) { hipFree(code); return rc; }
     hipError_t e = hipSuccess;
-    for (int r = 0; r < reps && e == hipSuccess; r++) e = launch_dpack_mv(d, x, norm_w, eps, y, mode, g_stream);
+    for (int r = 0; r < reps && e == hipSuccess; r++) e = launch_dpack_mv(d, x, norm_w, eps, y, mode, g_stream, g_part);
     const hipError_t e2 = hipStreamSynchronize(g_stream);
     hipFree(code);
     if (e == hipSuccess) e = e2;

@@ -8,6 +8,7 @@ namespace mlxr {
 
 constexpr int DMV_MAX_K = 32768;     // input length of the standalone matvec (max)
 constexpr int DMV_MAX_LDS = 160 * 1024;
+constexpr int DMV_SPLIT_K = 16384;   // longer inputs split over two workgroups per tile (with a scratch buffer)
 
 // The matvec over the packed input and the epilogue (y = v, y += v, or SiLU(gate) * up).
 template <int FB, int MODE>
@@ -44,8 +45,8 @@ __device__ __forceinline__ void dmv_finish(const MvPhaseDesc& p, const MvLds& L,
 // and packs x straight from global memory (the norm statistics and max |x| first, then the
 // packing), so large inputs (K up to 32768) fit in LDS without an f32 copy.
 template <int FB, int MODE>
-__global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, const float* __restrict__ x,
-                                                              const float* __restrict__ nw, float eps, float* __restrict__ y, int tpw) {
+__device__ __forceinline__ void dmv_body(const MvPhaseDesc& p, const float* __restrict__ x, const float* __restrict__ nw, float eps,
+                                         float* __restrict__ y, int tpw, int wg, int nwg) {
     constexpr int GSH = FB == 4 ? 5 : 6;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int K = p.K;
@@ -56,7 +57,7 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
     L.zero16 = L.gsum + (((K >> GSH) + 3) & ~3);   // 16-byte aligned
     L.part = L.zero16 + MV_ZERO;
     float* red = L.part + tpw * MK_WAVES * 16;
-    const int wg = blockIdx.x, nwg = gridDim.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     Ring<FB> ring;
     // statistics: sum of squares of x, max |x w| (max |x| without a norm). Inputs of up to
     // 8 * XR * MK_THREADS values are read once, 8-group t = tid + MK_THREADS i into registers, and
@@ -161,6 +162,41 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
 }
 
 template <int FB, int MODE>
+__global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, const float* __restrict__ x,
+                                                              const float* __restrict__ nw, float eps, float* __restrict__ y, int tpw) {
+    dmv_body<FB, MODE>(p, x, nw, eps, y, tpw, blockIdx.x, gridDim.x);
+}
+
+// Split over the input for long inputs (no norm, not gated): workgroup (t, s) computes tile t's
+// rows over the s-th of gridDim.y contiguous runs of scale groups, from its own slice of x (the
+// f16 hi + lo image of a slice fits twice in LDS, so two workgroups share a CU), into
+// part[s][rows]; dmv_combine adds the slices in order (deterministic) and the bias.
+template <int FB>
+__global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc p, const float* __restrict__ x, float* __restrict__ part) {
+    const int t = blockIdx.x, sl = blockIdx.y, S = gridDim.y;
+    const int KBT = p.K >> 7, NF = (KBT + FB - 1) / FB;
+    const int fa = NF * sl / S, fb = NF * (sl + 1) / S;
+    MvPhaseDesc q = p;
+    q.code = p.code + ((size_t)t * NF + fa) * ((FB + 1) * 1024);
+    q.K = min(fb * FB * 128, p.K) - fa * FB * 128;
+    q.tiles = 1;
+    q.rows = min(16, p.rows - 16 * t);
+    q.o1 = q.rows; q.o2 = 0;
+    q.bias[0] = q.bias[1] = q.bias[2] = nullptr;
+    dmv_body<FB, OUT_STORE>(q, x + fa * FB * 128, nullptr, 0.0f, part + (size_t)sl * p.rows + 16 * t, 1, 0, 1);
+}
+
+// y[r] = (accumulate ? y[r] : 0) + part[0][r] + ... + part[S-1][r] + bias[r]
+__global__ void dmv_combine(MvPhaseDesc p, const float* __restrict__ part, int S, float* __restrict__ y, int accumulate) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= p.rows) return;
+    float v = 0.0f;
+    for (int sl = 0; sl < S; sl++) v += part[(size_t)sl * p.rows + r];
+    v += row_bias(p, r);
+    y[r] = accumulate ? y[r] + v : v;
+}
+
+template <int FB, int MODE>
 static hipError_t dmv_launch(const MvPhaseDesc& p, const float* x, const float* nw, float eps, float* y, int nwg, int tpw,
                              size_t lds, hipStream_t s) {
     static bool attr = false;
@@ -179,8 +215,24 @@ bool dpack_mv_supported(const MvPhaseDesc& p) {
 }
 
 hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* norm_w, float eps, float* y, int mode,
-                           hipStream_t s) {
+                           hipStream_t s, float* split) {
     if (!dpack_mv_supported(p) || mode < 0 || mode > 2) return hipErrorInvalidValue;
+    if (split && p.K > DMV_SPLIT_K && !norm_w && mode != OUT_GATED) {
+        constexpr int S = 2;   // measured on the 32B down (27648 inputs): 1 49 us, 2 31, 3 33, 4 31, 6 39
+        const int KBT = p.K >> 7, FB = p.gs >> 3, NF = (KBT + FB - 1) / FB;
+        const int kslice = (NF + S - 1) / S * FB * 128;
+        const size_t lds = sizeof(float) * ((size_t)(kslice >> 5) * XH_STRIDE + ((kslice / p.gs + 3) & ~3) + MV_ZERO + MK_WAVES * 16 + 16);
+        static bool attr = false;
+        if (!attr) {
+            for (const void* f : {(const void*)dpack_mv_split_kernel<4>, (const void*)dpack_mv_split_kernel<8>})
+                if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, DMV_MAX_LDS) != hipSuccess) return hipErrorInvalidValue;
+            attr = true;
+        }
+        if (p.gs == 32) hipLaunchKernelGGL(dpack_mv_split_kernel<4>, dim3(p.tiles, S), dim3(MK_THREADS), lds, s, p, x, split);
+        else hipLaunchKernelGGL(dpack_mv_split_kernel<8>, dim3(p.tiles, S), dim3(MK_THREADS), lds, s, p, x, split);
+        hipLaunchKernelGGL(dmv_combine, dim3((p.rows + 255) / 256), dim3(256), 0, s, p, (const float*)split, S, y, mode == OUT_ADD ? 1 : 0);
+        return hipGetLastError();
+    }
     static int cus = 0;
     if (!cus) {
         int dev = 0;

@@ -569,7 +569,7 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
         (rc = dalloc(m, &m->dpos, 64)) || (rc = dalloc(m, &m->h, (size_t)B * H)) || (rc = dalloc(m, &m->xn, (size_t)B * H)) ||
         (rc = dalloc(m, &m->tmp, (size_t)B * H)) || (rc = dalloc(m, &m->qkv, (size_t)B * m->qkv_cols)) ||
         (rc = dalloc(m, &m->attn, (size_t)B * c.nH * c.D)) || (rc = dalloc(m, &m->gu, (size_t)B * 2 * I)) ||
-        (rc = dalloc(m, &m->mlp, (size_t)B * I)) || (rc = dalloc(m, &m->logits, (size_t)8 * V)) ||
+        (rc = dalloc(m, &m->mlp, (size_t)B * I)) || (rc = dalloc(m, &m->logits, (size_t)8 * V)) || (rc = dalloc(m, &m->dmv_split, (size_t)2 * H)) ||
         (rc = dalloc(m, &m->part, partFloats)) || (rc = dalloc(m, &m->bmax, (V + 255) / 256)) ||
         (rc = dalloc(m, &m->barg, (V + 255) / 256)) || (rc = dalloc(m, &m->xbf, (size_t)B * Kmax)) || (rc = dalloc(m, &m->xsc, (size_t)B)) || (rc = dalloc(m, &m->diag, 8)))
         return fail(rc);
@@ -709,7 +709,7 @@ int encode_decode(Model* m, const mlxr_sample_params* sp, bool sparse, bool logi
         if (tl) {
             HIPCHECK(launch_dpack_mv(tl->o, m->attn, nullptr, 0, m->h, 1, s));
             HIPCHECK(launch_dpack_mv(tl->gu, m->h, ly.post_norm, c.eps, m->mlp, 2, s));
-            HIPCHECK(launch_dpack_mv(tl->down, m->mlp, nullptr, 0, m->h, 1, s));
+            HIPCHECK(launch_dpack_mv(tl->down, m->mlp, nullptr, 0, m->h, 1, s, m->dmv_split));
         } else {
             HIPCHECK(launch_qmv(qmv_args(&ly.o, 1, m->attn, nullptr, 0, m->h, EPI_ADD), s));
             HIPCHECK(launch_qmv(qmv_args(gup, 2, m->h, ly.post_norm, c.eps, m->mlp, EPI_GATED), s));
@@ -1095,7 +1095,7 @@ int model_profile(Model* m, const char* kind_c, int iters, int context, double* 
             if (k == "qkv") return (int)launch_dpack_mv(t.qkv, m->h, ly.in_norm, c.eps, m->qkv, 0, s);
             if (k == "o") return (int)launch_dpack_mv(t.o, m->attn, nullptr, 0, m->tmp, 1, s);
             if (k == "gateup") return (int)launch_dpack_mv(t.gu, m->h, ly.post_norm, c.eps, m->mlp, 2, s);
-            return (int)launch_dpack_mv(t.down, m->mlp, nullptr, 0, m->tmp, 1, s);
+            return (int)launch_dpack_mv(t.down, m->mlp, nullptr, 0, m->tmp, 1, s, m->dmv_split);
         };
     } else if (kind == "head") {
         b = lin_bytes_of(m->head) + (int64_t)c.H * 4 * 2 + (int64_t)c.V * 4;

@@ -61,6 +61,7 @@ struct Model {
     int* hist = nullptr; int* status = nullptr; uint64_t* rng = nullptr;
     int* dpos = nullptr;                 // position of the step being processed (device)
     float *h = nullptr, *xn = nullptr, *tmp = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *mlp = nullptr;
+    float* dmv_split = nullptr;      // [2][H] input-slice partials of the kernel-per-op down matvec (long inputs)
     float* logits = nullptr; float* part = nullptr; float* bmax = nullptr; int* barg = nullptr;
     uint16_t* xbf = nullptr; float* xsc = nullptr;
     int* diag = nullptr;
