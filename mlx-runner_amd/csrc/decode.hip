@@ -273,10 +273,17 @@ template <int NB = MK_LDB>
 __device__ __forceinline__ float copy_to_lds(const uint2* src, unsigned tag, const TagWait& tw, int K, const MvLds& L, int gsh,
                                              const uint2* h, unsigned htag, int H, int row0, int row1, float* red) {
     const int n = row1 - row0;
-    float hv = 0.0f;
-    if ((int)threadIdx.x < n) hv = ld_tag1(h, row0 + threadIdx.x, H, htag, tw);
+    // the residual row was written phases ago: its load is issued first and checked only after the
+    // input's loads, so it adds no round trip of its own
+    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint2*>(h), 0, H * 8, 0x00020000);
+    typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+    const int hi = min(row0 + (int)threadIdx.x, H - 1);
+    u32x2v hv = __builtin_amdgcn_raw_buffer_load_b64(hr, hi * 8, 0, 16);
     const float mx = fetch_to_lds<NB>(src, K, tag, tw, L.xf).y;
-    if ((int)threadIdx.x < n) L.hown[threadIdx.x] = hv;
+    if ((int)threadIdx.x < n) {
+        for (unsigned spins = 0; hv.y != htag && tag_spin(tw, spins);) hv = __builtin_amdgcn_raw_buffer_load_b64(hr, hi * 8, 0, 16);
+        L.hown[threadIdx.x] = __uint_as_float(hv.x);
+    }
     return pack_x16(L.xf, K, block_max(mx, red), L, gsh);
 }
 
