@@ -102,6 +102,27 @@ __device__ __forceinline__ float2 ld_tag2(const uint2* base, int i, int n, unsig
     while ((v.y != tag || v.w != tag) && tag_spin(tw, spins)) v = __builtin_amdgcn_raw_buffer_load_b128(r, i * 8, 0, 16);
     return float2{__uint_as_float(v.x), __uint_as_float(v.z)};
 }
+// N tagged values base[idx[i]] in one round trip: every load issued, then polled together until
+// all carry `tag` (the ones still missing reissued each round).
+template <int N>
+__device__ __forceinline__ void ld_tagN(const uint2* base, int n, const int* idx, unsigned tag, const TagWait& tw, float* out) {
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint2*>(base), 0, n * 8, 0x00020000);
+    typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+    u32x2v v[N];
+#pragma unroll
+    for (int q = 0; q < N; q++) v[q] = __builtin_amdgcn_raw_buffer_load_b64(r, idx[q] * 8, 0, 16);
+    for (unsigned spins = 0;;) {
+        bool ready = true;
+#pragma unroll
+        for (int q = 0; q < N; q++) ready &= v[q].y == tag;
+        if (ready || !tag_spin(tw, spins)) break;
+#pragma unroll
+        for (int q = 0; q < N; q++)
+            if (v[q].y != tag) v[q] = __builtin_amdgcn_raw_buffer_load_b64(r, idx[q] * 8, 0, 16);
+    }
+#pragma unroll
+    for (int q = 0; q < N; q++) out[q] = __uint_as_float(v[q].x);
+}
 __device__ __forceinline__ float ld_tag1(const uint2* base, int i, int n, unsigned tag, const TagWait& tw) {
     __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint2*>(base), 0, n * 8, 0x00020000);
     typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
@@ -590,7 +611,12 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     // K / V loads (issued first; the memory counter completes in order)
                     const float* nwp = isk ? ly.k_norm : ly.q_norm;
                     const float nw0 = nwp ? gload(nwp + nd0) : 1.0f, nw1 = nwp ? gload(nwp + nd1) : 1.0f;
-                    float v0 = ld_tag1(a.qkvT, col + nd0, QKV, qtag, tw), v1 = ld_tag1(a.qkvT, col + nd1, QKV, qtag, tw);
+                    // this item's two dims (and, for the new key, the value's two dims) in one round trip
+                    const int vc = (nH + nKV + kvh) * D;
+                    const int ix[4] = {col + nd0, col + nd1, isk ? vc + nd0 : col + nd0, isk ? vc + nd1 : col + nd1};
+                    float got[4];
+                    ld_tagN<4>(a.qkvT, QKV, ix, qtag, tw, got);
+                    float v0 = got[0], v1 = got[1];
                     if (nwp) {
                         const float r = 1.0f / sqrtf(wave_sum(v0 * v0 + v1 * v1) / 128.0f + a.eps);
                         v0 = v0 * r * nw0;
@@ -598,10 +624,8 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
                     }
                     const float o0 = v0 * cs.x - v1 * cs.y, o1 = v1 * cs.x + v0 * cs.y;
                     if (isk) {
-                        const int vc = (nH + nKV + kvh) * D;
                         const uint16_t k0 = f32_to_bf16(o0), k1 = f32_to_bf16(o1);
-                        const uint16_t w0 = f32_to_bf16(ld_tag1(a.qkvT, vc + nd0, QKV, qtag, tw));
-                        const uint16_t w1 = f32_to_bf16(ld_tag1(a.qkvT, vc + nd1, QKV, qtag, tw));
+                        const uint16_t w0 = f32_to_bf16(got[2]), w1 = f32_to_bf16(got[3]);
                         kn16[nd0] = k0; kn16[nd1] = k1; vn16[nd0] = w0; vn16[nd1] = w1;
                         const int64_t row = kv_row(lpt, nKV, kvh, pos_l) * 128;
                         gstore(ly.kc + row + nd0, k0); gstore(ly.kc + row + nd1, k1);
@@ -622,10 +646,11 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             // q heads (4 per pass of 512 threads), then the new k and v if this range holds pos
             const int grp = tid >> 7, i = tid & 127;
             // every value this workgroup needs from q|k|v, loaded at once
-            const float qv0 = ld_tag1(a.qkvT, (kvh * G + min(grp, G - 1)) * D + i, QKV, qtag, tw);
-            const float qv1 = ld_tag1(a.qkvT, (kvh * G + min(grp + 4, G - 1)) * D + i, QKV, qtag, tw);
-            const float kraw = ld_tag1(a.qkvT, (nH + kvh) * D + i, QKV, qtag, tw);
-            const float vraw = ld_tag1(a.qkvT, (nH + nKV + kvh) * D + i, QKV, qtag, tw);
+            const int ix[4] = {(kvh * G + min(grp, G - 1)) * D + i, (kvh * G + min(grp + 4, G - 1)) * D + i,
+                               (nH + kvh) * D + i, (nH + nKV + kvh) * D + i};
+            float got[4];
+            ld_tagN<4>(a.qkvT, QKV, ix, qtag, tw, got);
+            const float qv0 = got[0], qv1 = got[1], kraw = got[2], vraw = got[3];
             for (int base = 0; base < G; base += 4) {
                 const int g = base + grp;
                 const float v = g < G ? (base == 0 ? qv0 : qv1) : 0.0f;
