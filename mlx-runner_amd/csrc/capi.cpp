@@ -20,6 +20,7 @@ int* g_pos = nullptr;          // device scalar for kernel-level calls
 int* g_pt = nullptr;           // identity page table
 int g_pt_pages = 0;
 float* g_part = nullptr; size_t g_part_floats = 0;
+float* g_split = nullptr; size_t g_split_floats = 0;   // the long-input split matvec's scratch
 uint16_t* g_xbf = nullptr; size_t g_xbf_elems = 0;
 float* g_xsc = nullptr; size_t g_xsc_elems = 0;
 float* g_bmax = nullptr; int* g_barg = nullptr; int g_blocks = 0;
@@ -289,9 +290,13 @@ int mlxr_k_qmv_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode
     if (int rc = tiles_pack(parts, nparts, K, gs, mode == 2, d, code)) return rc;
     if (!dpack_mv_supported(d)) { hipFree(code); return set_error(MLXR_E_UNSUPPORTED, "matvec over repacked tiles: K too large"); }
     // the scratch of the long-input split (2 * rows floats), as the model's kernel-per-op step passes it
-    if (int rc = ensure_buf(g_part, g_part_floats, (size_t)2 * d.rows)) { hipFree(code); return rc; }
+    const size_t sf = dpack_mv_split_floats(d.rows);
+    if (sf > g_split_floats) {
+        if (int rc = ensure_buf(g_split, g_split_floats, sf)) { hipFree(code); return rc; }
+        CK(hipMemset(g_split, 0, sf * 4));   // tile counters start at zero and return to it
+    }
     hipError_t e = hipSuccess;
-    for (int r = 0; r < reps && e == hipSuccess; r++) e = launch_dpack_mv(d, x, norm_w, eps, y, mode, g_stream, g_part);
+    for (int r = 0; r < reps && e == hipSuccess; r++) e = launch_dpack_mv(d, x, norm_w, eps, y, mode, g_stream, g_split);
     const hipError_t e2 = hipStreamSynchronize(g_stream);
     hipFree(code);
     if (e == hipSuccess) e = e2;

@@ -31,8 +31,10 @@ hipError_t launch_tile_gemm(const MvPhaseDesc& p, const uint16_t* xh, const floa
 // Batch-1 matvec over a repacked matrix (the kernel-per-op decode step): mode 0 y = W x (+ bias),
 // 1 y += W x (+ bias), 2 y[o1] = SiLU(gate) * up; norm_w: x := RMSNorm(x) * norm_w first.
 bool dpack_mv_supported(const MvPhaseDesc& p);
-// split: optional scratch of 2 * rows floats; with it, inputs over 16384 values (no norm, not gated)
-// run as two input slices per tile plus an ordered combine.
+// split: optional scratch of dpack_mv_split_floats(rows) floats, zeroed once before its first use
+// (its tile counters return to zero after every launch); with it, inputs over 16384 values (no
+// norm, not gated) run as two input slices per tile, combined in order by the last of them.
+inline size_t dpack_mv_split_floats(int rows) { return (size_t)2 * rows + (size_t)(rows + 15) / 16 + 16; }
 hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* norm_w, float eps, float* y, int mode,
                            hipStream_t s, float* split = nullptr);
 

@@ -8,7 +8,8 @@ namespace mlxr {
 
 constexpr int DMV_MAX_K = 32768;     // input length of the standalone matvec (max)
 constexpr int DMV_MAX_LDS = 160 * 1024;
-constexpr int DMV_SPLIT_K = 16384;   // longer inputs split over two workgroups per tile (with a scratch buffer)
+constexpr int DMV_SPLIT_K = 16384;
+constexpr int DMV_OUT_PARTIAL = 5;   // dmv_finish mode: plain store, coherent across the XCDs (an input slice's partial rows)   // longer inputs split over two workgroups per tile (with a scratch buffer)
 
 // The matvec over the packed input and the epilogue (y = v, y += v, or SiLU(gate) * up).
 template <int FB, int MODE>
@@ -34,6 +35,7 @@ __device__ __forceinline__ void dmv_finish(const MvPhaseDesc& p, const MvLds& L,
         if (row >= p.rows) break;
         const float v = tile_row(L.part, i >> 4, i & 15, nfw, g.NF) * unscale + row_bias(p, row);
         if (MODE == OUT_ADD) y[row] += v;
+        else if (MODE == DMV_OUT_PARTIAL) __hip_atomic_store(y + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else y[row] = v;
     }
 }
@@ -170,9 +172,12 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
 // Split over the input for long inputs (no norm, not gated): workgroup (t, s) computes tile t's
 // rows over the s-th of gridDim.y contiguous runs of scale groups, from its own slice of x (the
 // f16 hi + lo image of a slice fits twice in LDS, so two workgroups share a CU), into
-// part[s][rows]; dmv_combine adds the slices in order (deterministic) and the bias.
+// part[s][rows] with coherent stores; the last slice of a tile to finish (a per-tile counter after
+// the partials, reset by it for the next launch) adds the slices in order, the bias and the output:
+// deterministic, and no combine launch.
 template <int FB>
-__global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc p, const float* __restrict__ x, float* __restrict__ part) {
+__global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc p, const float* __restrict__ x, float* __restrict__ part,
+                                                                    float* __restrict__ y, int accumulate) {
     const int t = blockIdx.x, sl = blockIdx.y, S = gridDim.y;
     const int KBT = p.K >> 7, NF = (KBT + FB - 1) / FB;
     const int fa = NF * sl / S, fb = NF * (sl + 1) / S;
@@ -183,17 +188,24 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc 
     q.rows = min(16, p.rows - 16 * t);
     q.o1 = q.rows; q.o2 = 0;
     q.bias[0] = q.bias[1] = q.bias[2] = nullptr;
-    dmv_body<FB, OUT_STORE>(q, x + fa * FB * 128, nullptr, 0.0f, part + (size_t)sl * p.rows + 16 * t, 1, 0, 1);
-}
-
-// y[r] = (accumulate ? y[r] : 0) + part[0][r] + ... + part[S-1][r] + bias[r]
-__global__ void dmv_combine(MvPhaseDesc p, const float* __restrict__ part, int S, float* __restrict__ y, int accumulate) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= p.rows) return;
-    float v = 0.0f;
-    for (int sl = 0; sl < S; sl++) v += part[(size_t)sl * p.rows + r];
-    v += row_bias(p, r);
-    y[r] = accumulate ? y[r] + v : v;
+    dmv_body<FB, DMV_OUT_PARTIAL>(q, x + fa * FB * 128, nullptr, 0.0f, part + (size_t)sl * p.rows + 16 * t, 1, 0, 1);
+    // the partial rows are stored (and visible at agent scope) before the tile's counter moves
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int last;
+    unsigned* cnt = reinterpret_cast<unsigned*>(part + (size_t)S * p.rows);
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(cnt + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    __syncthreads();
+    if (!last) return;
+    const int r = 16 * t + (int)threadIdx.x;
+    if (threadIdx.x < 16 && r < p.rows) {
+        float v = 0.0f;
+        for (int k = 0; k < S; k++) v += __hip_atomic_load(part + (size_t)k * p.rows + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v += row_bias(p, r);
+        y[r] = accumulate ? y[r] + v : v;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int FB, int MODE>
@@ -225,12 +237,13 @@ hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* no
         static bool attr = false;
         if (!attr) {
             for (const void* f : {(const void*)dpack_mv_split_kernel<4>, (const void*)dpack_mv_split_kernel<8>})
-                if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, DMV_MAX_LDS) != hipSuccess) return hipErrorInvalidValue;
+                if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, DMV_MAX_LDS - 1024) != hipSuccess)   // beside its static LDS
+                    return hipErrorInvalidValue;
             attr = true;
         }
-        if (p.gs == 32) hipLaunchKernelGGL(dpack_mv_split_kernel<4>, dim3(p.tiles, S), dim3(MK_THREADS), lds, s, p, x, split);
-        else hipLaunchKernelGGL(dpack_mv_split_kernel<8>, dim3(p.tiles, S), dim3(MK_THREADS), lds, s, p, x, split);
-        hipLaunchKernelGGL(dmv_combine, dim3((p.rows + 255) / 256), dim3(256), 0, s, p, (const float*)split, S, y, mode == OUT_ADD ? 1 : 0);
+        const int acc = mode == OUT_ADD ? 1 : 0;
+        if (p.gs == 32) hipLaunchKernelGGL(dpack_mv_split_kernel<4>, dim3(p.tiles, S), dim3(MK_THREADS), lds, s, p, x, split, y, acc);
+        else hipLaunchKernelGGL(dpack_mv_split_kernel<8>, dim3(p.tiles, S), dim3(MK_THREADS), lds, s, p, x, split, y, acc);
         return hipGetLastError();
     }
     static int cus = 0;

@@ -569,11 +569,12 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
         (rc = dalloc(m, &m->dpos, 64)) || (rc = dalloc(m, &m->h, (size_t)B * H)) || (rc = dalloc(m, &m->xn, (size_t)B * H)) ||
         (rc = dalloc(m, &m->tmp, (size_t)B * H)) || (rc = dalloc(m, &m->qkv, (size_t)B * m->qkv_cols)) ||
         (rc = dalloc(m, &m->attn, (size_t)B * c.nH * c.D)) || (rc = dalloc(m, &m->gu, (size_t)B * 2 * I)) ||
-        (rc = dalloc(m, &m->mlp, (size_t)B * I)) || (rc = dalloc(m, &m->logits, (size_t)8 * V)) || (rc = dalloc(m, &m->dmv_split, (size_t)2 * H)) ||
+        (rc = dalloc(m, &m->mlp, (size_t)B * I)) || (rc = dalloc(m, &m->logits, (size_t)8 * V)) || (rc = dalloc(m, &m->dmv_split, dpack_mv_split_floats(H))) ||
         (rc = dalloc(m, &m->part, partFloats)) || (rc = dalloc(m, &m->bmax, (V + 255) / 256)) ||
         (rc = dalloc(m, &m->barg, (V + 255) / 256)) || (rc = dalloc(m, &m->xbf, (size_t)B * Kmax)) || (rc = dalloc(m, &m->xsc, (size_t)B)) || (rc = dalloc(m, &m->diag, 8)))
         return fail(rc);
     HIPCHECK(hipMemset(m->hist, 0, (seq + 1) * 4));
+    HIPCHECK(hipMemset(m->dmv_split, 0, dpack_mv_split_floats(H) * 4));   // the split matvec's tile counters
     HIPCHECK(hipMemset(m->status, 0, (seq + 1) * 4));
     HIPCHECK(hipMemset(m->dpos, 0, 64 * 4));
     // sparse index (Transformer.swift:1009-1063)
