@@ -145,11 +145,12 @@ __device__ __forceinline__ void prof_mark(unsigned long long* prof, int ev) {
 // After every wave's mv_run: combines the partials and writes the phase's outputs (coherent stores
 // for data other workgroups read). ARGMAX returns the workgroup's largest row (lowest index among
 // equals; NaN rows never win) to every thread.
-template <int MODE, int FB>
+template <int MODE, int FB, bool HALF = false>
 __device__ __forceinline__ MvResult mv_finish(const MvPhase& p, float unscale, int wg, int nwg, const float* part, uint2* out,
                                               unsigned tag, float* logits, const float* hown, float* red, int* redi) {
     lds_barrier();
-    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
+    MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
+    if (HALF) g.NF *= 2;                         // the waves' ranges count half scale groups
     const int nfw = g.nt * g.NF;
     MvResult res{-INFINITY, 0x7fffffff};
     if (MODE == OUT_GATED) {
@@ -535,7 +536,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
     prof_mark(a.prof, 0);
     prof_mark(a.prof, 2 * epoch); ++epoch;
     NormW nwr = norm_w_load(ldesc[0].in_norm, H);
-    mv_prefetch<FB>(ldesc[0].qkv, wg, nwg, wave, lane, ring);
+    mvh_prefetch<FB>(ldesc[0].qkv, wg, nwg, wave, lane, ring);
     prof_mark(a.prof, 2 * epoch - 1);
 
     const int nsplit = nwg / nKV;
@@ -552,8 +553,8 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             if (li == 0 && a.stall && wg == 0) itag ^= 0x80000000u;   // test hook: a tag no launch writes
             const float us = norm_to_lds(a.hA, itag, tw, ly.in_norm, nwr, H, a.eps, ml, FB == 4 ? 5 : 6, red);
             prof_mark(a.prof, 512 + 8 * li + 0);
-            mv_run<FB, true>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
-            mv_finish<OUT_STORE, FB>(ly.qkv, us, wg, nwg, ml.part, a.qkvT, tag_of(2 + 5 * li), nullptr, nullptr, red, redi);
+            mvh_run<FB>(ly.qkv, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_finish<OUT_STORE, FB, true>(ly.qkv, us, wg, nwg, ml.part, a.qkvT, tag_of(2 + 5 * li), nullptr, nullptr, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
         // prefetch this workgroup's K/V rows (positions < pos are final)
@@ -906,7 +907,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             }
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
-        mv_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
+        mvh_prefetch<FB>(ly.o, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
 
         // ---- C: o_proj, h += W_o attn
@@ -915,8 +916,8 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
             const float us = copy_to_lds(a.attnT, tag_of(3 + 5 * li), tw, nH * D, ml, FB == 4 ? 5 : 6, a.hA,
                                          tag_of(li == 0 ? 1 : 6 + 5 * (li - 1)), H, 16 * gg.t0, min(16 * (gg.t0 + gg.nt), H), red);
             prof_mark(a.prof, 512 + 8 * li + 4);
-            mv_run<FB, true>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
-            mv_finish<OUT_ADD, FB>(ly.o, us, wg, nwg, ml.part, a.hB, tag_of(4 + 5 * li), nullptr, ml.hown, red, redi);
+            mvh_run<FB>(ly.o, ml.xh, ml.gsum, ml.zero16, wg, nwg, wave, lane, ring, ml.part);
+            mv_finish<OUT_ADD, FB, true>(ly.o, us, wg, nwg, ml.part, a.hB, tag_of(4 + 5 * li), nullptr, ml.hown, red, redi);
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
         nwr = norm_w_load(ly.post_norm, H);
@@ -947,7 +948,7 @@ __global__ __launch_bounds__(MK_THREADS, 1) void decode_step_kernel(MegaArgs a) 
         }
         prof_mark(a.prof, 2 * epoch); ++epoch;
         nwr = norm_w_load(li + 1 < a.L ? ldesc[li + 1].in_norm : a.final_norm, H);
-        if (li + 1 < a.L) mv_prefetch<FB>(ldesc[li + 1].qkv, wg, nwg, wave, lane, ring);
+        if (li + 1 < a.L) mvh_prefetch<FB>(ldesc[li + 1].qkv, wg, nwg, wave, lane, ring);
         else mv_prefetch<FB>(a.head, wg, nwg, wave, lane, ring);
         prof_mark(a.prof, 2 * epoch - 1);
     }

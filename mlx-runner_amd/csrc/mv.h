@@ -292,6 +292,110 @@ __device__ __forceinline__ float row_bias(const MvPhase& p, int vr) {
     return bf16_to_f32(gload(b + row));
 }
 
+// Half scale groups: for the phases with few scale groups per workgroup (q|k|v, o_proj: one per
+// wave or fewer), each scale group is cut into two units, its first and its second half of code
+// blocks (quantization groups 0-7 and 8-15), each with the group's scale block, so twice as many
+// waves work and each wave's chain of dependent MFMAs is half as long (the scale block is read
+// twice: 1 KB more per 9 KB). Unit u of the workgroup's tile-major order: group u >> 1, half u & 1.
+template <int FB>
+__device__ __forceinline__ void mvh_geom(const MvPhase& p, int wg, int nwg, int wave, int& NF, int& t0, int& nt, int& u0, int& u1) {
+    NF = ((p.K >> 7) + FB - 1) / FB;
+    t0 = (int)((unsigned)(p.tiles * wg) / (unsigned)nwg);
+    nt = (int)((unsigned)(p.tiles * (wg + 1)) / (unsigned)nwg) - t0;
+    const int nu = 2 * nt * NF;
+    u0 = (nu * wave) >> 3; u1 = (nu * (wave + 1)) >> 3;
+}
+// Block b (0: scales, 1..FB/2: the half's code blocks) of unit u, this lane's 16 bytes.
+template <int FB>
+__device__ __forceinline__ gptr8 mvh_block(const MvPhase& p, int NF, int t0, int u, int b, int lane) {
+    const int gi = u >> 1, h = u & 1;   // group in the workgroup's tile-major order, half
+    const int blk = b == 0 ? 0 : 1 + h * (FB / 2) + (b - 1);
+    return (gptr8)p.code + ((size_t)(unsigned)(t0 * NF + gi) * (FB + 1) + blk) * 1024 + lane * 16;
+}
+template <int FB>
+__device__ __forceinline__ void mvh_prefetch(const MvPhase p, int wg, int nwg, int wave, int lane, Ring<FB>& ring) {
+    int NF, t0, nt, u0, u1;
+    mvh_geom<FB>(p, wg, nwg, wave, NF, t0, nt, u0, u1);
+#pragma unroll
+    for (int b = 0; b <= FB; b++) ring.u[b] = uint4{0u, 0u, 0u, 0u};
+    if (u1 <= u0) return;
+#pragma unroll
+    for (int b = 0; b <= FB / 2; b++) ring.u[b] = ld_stream16(mvh_block<FB>(p, NF, t0, u0, b, lane));
+}
+// mv_run over half units (the first unit already in ring slots 0..FB/2). Partial row sums per
+// tile as mv_run leaves them; mv_finish combines them with tile_row(.., 2 * nt * NF, 2 * NF).
+template <int FB>
+__device__ __forceinline__ void mvh_run(const MvPhase p, const float* xh, const float* gsum, const float* zero16, int wg, int nwg,
+                                        int wave, int lane, Ring<FB>& ring, float* part) {
+    constexpr int GSH = FB == 4 ? 5 : 6;
+    constexpr int CPG = 1 << (GSH - 5);           // chunks per group
+    constexpr int HB = FB / 2;                     // code blocks per half
+    int NF, t0, nt, u0, u1;
+    mvh_geom<FB>(p, wg, nwg, wave, NF, t0, nt, u0, u1);
+    if (u1 <= u0) return;
+    const int gpr = p.K >> GSH;
+    const int col = lane & 15;
+    f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int u = u0; u < u1; u++) {
+        const bool more = u + 1 < u1;
+        const int gi = u >> 1, h = u & 1, tile = gi / NF, f = gi - tile * NF;
+        const uint4 sbr = ring.u[0];
+        if (more) ring.u[0] = ld_stream16(mvh_block<FB>(p, NF, t0, u + 1, 0, lane));
+        const float* xb = xh + (lane >> 4) * 4 + f * (4 * FB) * XH_STRIDE;
+        f32x4_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        // code blocks H * HB .. of the group (H a constant in each copy of the body)
+        auto body = [&](auto HC) {
+            constexpr int H = decltype(HC)::value;
+#pragma unroll
+            for (int kl = 0; kl < HB; kl++) {
+                const int k = H * HB + kl;                                 // block within the group
+                const uint4 unit = ring.u[1 + kl];
+                const uint32_t wd[4] = {unit.x, unit.y, unit.z, unit.w};
+                f16x8_t b[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int gcol = (4 * k + j) / CPG;
+                    const int g0 = gcol * CPG * XH_STRIDE;
+                    const float* gb = col == gcol ? xb : col == (gcol ^ 8) ? xb + XH_LO : zero16 - g0;
+                    const float* bp = gb + g0 + (4 * k + j - gcol * CPG) * XH_STRIDE;
+                    b[j] = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(bp));
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const f16x8_t av = a_operand(wd[j]);
+                    if (j & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[j], acc1, 0, 0, 0);
+                    else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[j], acc0, 0, 0, 0);
+                }
+                if (more) ring.u[1 + kl] = ld_stream16(mvh_block<FB>(p, NF, t0, u + 1, 1 + kl, lane));
+            }
+        };
+        if (h == 0) body(std::integral_constant<int, 0>{});
+        else body(std::integral_constant<int, 1>{});
+        acc0 += acc1;
+        // this half's groups are columns 8h .. 8h + 7 (hi), their lo parts in the other eight
+        const bool mine = (col >> 3) == h;
+        const int gi16 = 16 * f + col;
+        const bool real = mine && gi16 < gpr;
+        const float xs = gsum[real ? gi16 : 0];
+        const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float a = acc0[r] + __shfl_xor(acc0[r], 8, 64);
+            const float sc = __uint_as_float(sv[r] << 16) * 16777216.0f, bb = __uint_as_float(sv[r] & 0xffff0000u);
+            const float t = sc * a + bb * xs;
+            run[r] += real ? t : 0.0f;
+        }
+        if ((f == NF - 1 && h == 1) || !more) {    // tile done (or the wave's range): row sums to LDS
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float v = row16_sum(run[r]);
+                if (col == 0) part[(tile * MK_WAVES + wave) * 16 + 4 * (lane >> 4) + r] = v;
+            }
+            run = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+}
+
 // Row r of tile tl of this workgroup: the partial sums of the waves whose ranges meet the tile, in
 // wave order.
 __device__ __forceinline__ float tile_row(const float* part, int tl, int r, int nfw, int NF) {
