@@ -289,7 +289,7 @@ int mlxr_k_qmv_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode
     MvPhaseDesc d; uint8_t* code;
     if (int rc = tiles_pack(parts, nparts, K, gs, mode == 2, d, code)) return rc;
     if (!dpack_mv_supported(d)) { hipFree(code); return set_error(MLXR_E_UNSUPPORTED, "matvec over repacked tiles: K too large"); }
-    // the scratch of the long-input split (2 * rows floats), as the model's kernel-per-op step passes it
+    // the scratch of the input-sliced matvec, as the model's kernel-per-op step passes it
     const size_t sf = dpack_mv_split_floats(d.rows);
     if (sf > g_split_floats) {
         if (int rc = ensure_buf(g_split, g_split_floats, sf)) { hipFree(code); return rc; }

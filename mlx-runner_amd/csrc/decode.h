@@ -11,6 +11,7 @@ struct MvPhaseDesc {
     const uint8_t* code;                      // DPack stream (scale groups of scale + code blocks)
     const uint16_t* bias[3];                  // optional per-row bias of each part (bf16)
     int o1, o2, rows, K, gs, gated, tiles;
+    int tstride;   // scale groups from one tile's first to the next's when they are not contiguous (an input slice), else 0
 };
 
 // Source of a repack: the MLX layout (codes [O][K/2], bf16 scales / biases [O][K/gs]) of each part.
@@ -32,9 +33,11 @@ hipError_t launch_tile_gemm(const MvPhaseDesc& p, const uint16_t* xh, const floa
 // 1 y += W x (+ bias), 2 y[o1] = SiLU(gate) * up; norm_w: x := RMSNorm(x) * norm_w first.
 bool dpack_mv_supported(const MvPhaseDesc& p);
 // split: optional scratch of dpack_mv_split_floats(rows) floats, zeroed once before its first use
-// (its tile counters return to zero after every launch); with it, inputs over 16384 values (no
-// norm, not gated) run as two input slices per tile, combined in order by the last of them.
-inline size_t dpack_mv_split_floats(int rows) { return (size_t)2 * rows + (size_t)(rows + 15) / 16 + 16; }
+// (its tile counters return to zero after every launch); with it, a projection without norm or
+// gate whose tiles are too few to spread evenly over the CUs runs as up to DMV_MAX_SLICES input
+// slices of every tile, the slices' partials combined in order by the last of them.
+constexpr int DMV_MAX_SLICES = 8;
+inline size_t dpack_mv_split_floats(int rows) { return (size_t)DMV_MAX_SLICES * rows + (size_t)(rows + 15) / 16 + 64; }
 hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* norm_w, float eps, float* y, int mode,
                            hipStream_t s, float* split = nullptr);
 

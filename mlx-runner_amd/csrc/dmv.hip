@@ -8,14 +8,13 @@ namespace mlxr {
 
 constexpr int DMV_MAX_K = 32768;     // input length of the standalone matvec (max)
 constexpr int DMV_MAX_LDS = 160 * 1024;
-constexpr int DMV_SPLIT_K = 16384;
-constexpr int DMV_OUT_PARTIAL = 5;   // dmv_finish mode: plain store, coherent across the XCDs (an input slice's partial rows)   // longer inputs split over two workgroups per tile (with a scratch buffer)
+constexpr int DMV_OUT_PARTIAL = 5;   // dmv_finish mode: plain store, coherent across the XCDs (an input slice's partial rows)
 
 // The matvec over the packed input and the epilogue (y = v, y += v, or SiLU(gate) * up).
-template <int FB, int MODE>
+template <int FB, int MODE, bool TS>
 __device__ __forceinline__ void dmv_finish(const MvPhaseDesc& p, const MvLds& L, int wg, int nwg, int wave, int lane,
                                            Ring<FB>& ring, float unscale, float* __restrict__ y) {
-    mv_run<FB>(p, L.xh, L.gsum, L.zero16, wg, nwg, wave, lane, ring, L.part);
+    mv_run<FB, false, TS>(p, L.xh, L.gsum, L.zero16, wg, nwg, wave, lane, ring, L.part);
     lds_barrier();
     const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, 0);
     const int nfw = g.nt * g.NF;
@@ -46,7 +45,7 @@ __device__ __forceinline__ void dmv_finish(const MvPhaseDesc& p, const MvLds& L,
 // Every workgroup issues its first scale group of weights (after x when x is held in registers)
 // and packs x straight from global memory (the norm statistics and max |x| first, then the
 // packing), so large inputs (K up to 32768) fit in LDS without an f32 copy.
-template <int FB, int MODE>
+template <int FB, int MODE, bool TS = false>
 __device__ __forceinline__ void dmv_body(const MvPhaseDesc& p, const float* __restrict__ x, const float* __restrict__ nw, float eps,
                                          float* __restrict__ y, int tpw, int wg, int nwg) {
     constexpr int GSH = FB == 4 ? 5 : 6;
@@ -86,7 +85,7 @@ __device__ __forceinline__ void dmv_body(const MvPhaseDesc& p, const float* __re
         }
         // the weights' first scale group after x: the memory counter completes in order, so the
         // statistics wait for x alone while the weights stream in behind
-        mv_prefetch<FB>(p, wg, nwg, wave, lane, ring);
+        mv_prefetch<FB, TS>(p, wg, nwg, wave, lane, ring);
 #pragma unroll
         for (int i = 0; i < XR; i++)
 #pragma unroll
@@ -121,10 +120,10 @@ __device__ __forceinline__ void dmv_body(const MvPhaseDesc& p, const float* __re
                 if (i == k) { lo = xv[k][0]; hi = xv[k][1]; }
         };
         const float unscale = pack_x16_from(ld, K, gmax * inv, L, GSH);
-        dmv_finish<FB, MODE>(p, L, wg, nwg, wave, lane, ring, unscale, y);
+        dmv_finish<FB, MODE, TS>(p, L, wg, nwg, wave, lane, ring, unscale, y);
         return;
     }
-    mv_prefetch<FB>(p, wg, nwg, wave, lane, ring);
+    mv_prefetch<FB, TS>(p, wg, nwg, wave, lane, ring);
     for (int base = threadIdx.x * 4; base < K; base += MK_THREADS * 16) {
         float4 v[4], w[4];
 #pragma unroll
@@ -160,7 +159,7 @@ __device__ __forceinline__ void dmv_body(const MvPhaseDesc& p, const float* __re
         auto ld = [x, gf4](int t, float4& lo, float4& hi) { lo = gf4(x + 8 * t); hi = gf4(x + 8 * t + 4); };
         unscale = pack_x16_from(ld, K, gmax, L, GSH);
     }
-    dmv_finish<FB, MODE>(p, L, wg, nwg, wave, lane, ring, unscale, y);
+    dmv_finish<FB, MODE, TS>(p, L, wg, nwg, wave, lane, ring, unscale, y);
 }
 
 template <int FB, int MODE>
@@ -169,43 +168,46 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
     dmv_body<FB, MODE>(p, x, nw, eps, y, tpw, blockIdx.x, gridDim.x);
 }
 
-// Split over the input for long inputs (no norm, not gated): workgroup (t, s) computes tile t's
-// rows over the s-th of gridDim.y contiguous runs of scale groups, from its own slice of x (the
-// f16 hi + lo image of a slice fits twice in LDS, so two workgroups share a CU), into
-// part[s][rows] with coherent stores; the last slice of a tile to finish (a per-tile counter after
-// the partials, reset by it for the next launch) adds the slices in order, the bias and the output:
-// deterministic, and no combine launch.
+// Split over the input (no norm, not gated): workgroup (w, s) computes the rows of its share of the
+// tiles (as dpack_mv_kernel shares them over gridDim.x workgroups) over the s-th of gridDim.y
+// contiguous runs of every tile's scale groups, from its own slice of x, into part[s][rows] with
+// coherent stores; for each tile, the last slice to finish (per-tile counters at the start of the
+// scratch, part after them, so that launches of other shapes and slice counts sharing the scratch
+// never overwrite a counter; reset by that slice for the next launch) adds the slices in order,
+// the bias and the output: deterministic, and no combine launch.
 template <int FB>
-__global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc p, const float* __restrict__ x, float* __restrict__ part,
-                                                                    float* __restrict__ y, int accumulate) {
-    const int t = blockIdx.x, sl = blockIdx.y, S = gridDim.y;
-    const int KBT = p.K >> 7, NF = (KBT + FB - 1) / FB;
+__global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc p, const float* __restrict__ x, float* __restrict__ split,
+                                                                    float* __restrict__ y, int accumulate, int tpw) {
+    unsigned* cnt = reinterpret_cast<unsigned*>(split);
+    float* part = split + ((p.tiles + 63) & ~63);
+    const int w = blockIdx.x, nw = gridDim.x, sl = blockIdx.y, S = gridDim.y;
+    const int NF = ((p.K >> 7) + FB - 1) / FB;
     const int fa = NF * sl / S, fb = NF * (sl + 1) / S;
     MvPhaseDesc q = p;
-    q.code = p.code + ((size_t)t * NF + fa) * ((FB + 1) * 1024);
+    q.code = p.code + (size_t)fa * ((FB + 1) * 1024);
     q.K = min(fb * FB * 128, p.K) - fa * FB * 128;
-    q.tiles = 1;
-    q.rows = min(16, p.rows - 16 * t);
-    q.o1 = q.rows; q.o2 = 0;
+    q.tstride = NF;
     q.bias[0] = q.bias[1] = q.bias[2] = nullptr;
-    dmv_body<FB, DMV_OUT_PARTIAL>(q, x + fa * FB * 128, nullptr, 0.0f, part + (size_t)sl * p.rows + 16 * t, 1, 0, 1);
-    // the partial rows are stored (and visible at agent scope) before the tile's counter moves
+    dmv_body<FB, DMV_OUT_PARTIAL, true>(q, x + fa * FB * 128, nullptr, 0.0f, part + (size_t)sl * p.rows, tpw, w, nw);
+    // the partial rows are stored (and visible at agent scope) before the tiles' counters move
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    __shared__ int last;
-    unsigned* cnt = reinterpret_cast<unsigned*>(part + (size_t)S * p.rows);
-    if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(cnt + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    __shared__ int last[MK_TPW];
+    const MvGeom<FB> g = mv_geom<FB>(q, w, nw, 0);
+    if ((int)threadIdx.x < g.nt)
+        last[threadIdx.x] = __hip_atomic_fetch_add(cnt + g.t0 + threadIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
     __syncthreads();
-    if (!last) return;
-    const int r = 16 * t + (int)threadIdx.x;
-    if (threadIdx.x < 16 && r < p.rows) {
-        float v = 0.0f;
-        for (int k = 0; k < S; k++) v += __hip_atomic_load(part + (size_t)k * p.rows + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        v += row_bias(p, r);
-        y[r] = accumulate ? y[r] + v : v;
+    for (int i = threadIdx.x; i < g.nt * 16; i += MK_THREADS) {
+        if (!last[i >> 4]) continue;
+        const int r = 16 * g.t0 + i;
+        if (r < p.rows) {
+            float v = 0.0f;
+            for (int k = 0; k < S; k++) v += __hip_atomic_load(part + (size_t)k * p.rows + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v += row_bias(p, r);
+            y[r] = accumulate ? y[r] + v : v;
+        }
+        if ((i & 15) == 0) __hip_atomic_store(cnt + g.t0 + (i >> 4), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (threadIdx.x == 0) __hip_atomic_store(cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int FB, int MODE>
@@ -229,23 +231,6 @@ bool dpack_mv_supported(const MvPhaseDesc& p) {
 hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* norm_w, float eps, float* y, int mode,
                            hipStream_t s, float* split) {
     if (!dpack_mv_supported(p) || mode < 0 || mode > 2) return hipErrorInvalidValue;
-    if (split && p.K > DMV_SPLIT_K && !norm_w && mode != OUT_GATED) {
-        constexpr int S = 2;   // measured on the 32B down (27648 inputs): 1 49 us, 2 31, 3 33, 4 31, 6 39
-        const int KBT = p.K >> 7, FB = p.gs >> 3, NF = (KBT + FB - 1) / FB;
-        const int kslice = (NF + S - 1) / S * FB * 128;
-        const size_t lds = sizeof(float) * ((size_t)(kslice >> 5) * XH_STRIDE + ((kslice / p.gs + 3) & ~3) + MV_ZERO + MK_WAVES * 16 + 16);
-        static bool attr = false;
-        if (!attr) {
-            for (const void* f : {(const void*)dpack_mv_split_kernel<4>, (const void*)dpack_mv_split_kernel<8>})
-                if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, DMV_MAX_LDS - 1024) != hipSuccess)   // beside its static LDS
-                    return hipErrorInvalidValue;
-            attr = true;
-        }
-        const int acc = mode == OUT_ADD ? 1 : 0;
-        if (p.gs == 32) hipLaunchKernelGGL(dpack_mv_split_kernel<4>, dim3(p.tiles, S), dim3(MK_THREADS), lds, s, p, x, split, y, acc);
-        else hipLaunchKernelGGL(dpack_mv_split_kernel<8>, dim3(p.tiles, S), dim3(MK_THREADS), lds, s, p, x, split, y, acc);
-        return hipGetLastError();
-    }
     static int cus = 0;
     if (!cus) {
         int dev = 0;
@@ -257,6 +242,39 @@ hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* no
     // the 32B projections: gate|up 43 -> 36 us at 2, down 48 -> 37 us at 1)
     const int nwg = std::min(p.tiles, (p.K > 16384 ? 1 : 2) * cus);
     const int tpw = (p.tiles + nwg - 1) / nwg;
+    if (split && !norm_w && mode != OUT_GATED) {
+        // S input slices of every tile over nw = slots / S workgroups each (two per CU: a slice's
+        // f16 image fits twice in LDS); the longest workgroup streams ceil(tiles / nw) tiles x
+        // ceil(NF / S) scale groups over its 8 waves: take the S that makes the longest wave's chain
+        // shortest, if shorter than unsplit (the fewest slices among equals: each slice repacks x)
+        const int FB = p.gs >> 3, NF = ((p.K >> 7) + FB - 1) / FB;
+        auto chain = [](long groups) { return (groups + MK_WAVES - 1) / MK_WAVES; };
+        int best_s = 1, best_nw = nwg, best_tpw = tpw;
+        long best = chain((long)tpw * NF);
+        for (int S = 2; S <= DMV_MAX_SLICES; S++) {
+            const int nw = std::min(p.tiles, 2 * cus / S), t = (p.tiles + nw - 1) / nw, fs = (NF + S - 1) / S;
+            if (t > MK_TPW || (long)fs * FB * 128 * 4 > DMV_MAX_LDS / 2 - 8192) continue;
+            if (chain((long)t * fs) < best) { best = chain((long)t * fs); best_s = S; best_nw = nw; best_tpw = t; }
+        }
+        if (best_s > 1) {
+            const int kslice = (NF + best_s - 1) / best_s * FB * 128;
+            const size_t lds = sizeof(float) * ((size_t)(kslice >> 5) * XH_STRIDE + ((kslice / p.gs + 3) & ~3) + MV_ZERO +
+                                                (size_t)best_tpw * MK_WAVES * 16 + 16);
+            static bool attr = false;
+            if (!attr) {
+                for (const void* f : {(const void*)dpack_mv_split_kernel<4>, (const void*)dpack_mv_split_kernel<8>})
+                    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, DMV_MAX_LDS - 1024) != hipSuccess)   // beside its static LDS
+                        return hipErrorInvalidValue;
+                attr = true;
+            }
+            const int acc = mode == OUT_ADD ? 1 : 0;
+            if (p.gs == 32)
+                hipLaunchKernelGGL(dpack_mv_split_kernel<4>, dim3(best_nw, best_s), dim3(MK_THREADS), lds, s, p, x, split, y, acc, best_tpw);
+            else
+                hipLaunchKernelGGL(dpack_mv_split_kernel<8>, dim3(best_nw, best_s), dim3(MK_THREADS), lds, s, p, x, split, y, acc, best_tpw);
+            return hipGetLastError();
+        }
+    }
     if (tpw > MK_TPW) return hipErrorInvalidValue;
     const size_t lds = sizeof(float) * ((size_t)(p.K >> 5) * XH_STRIDE + (((p.K / p.gs) + 3) & ~3) + MV_ZERO + (size_t)tpw * MK_WAVES * 16 + 16);
     if (lds > DMV_MAX_LDS) return hipErrorInvalidValue;

@@ -75,13 +75,18 @@ __device__ __forceinline__ MvGeom<FB> mv_geom(const MvPhase& p, int wg, int nwg,
     static_assert(MK_WAVES == 8, "wave split");
     return g;
 }
-// This lane's slice of the wave's first scale group.
-template <int FB>
+// This lane's slice of the wave's first scale group (TS: tiles p.tstride scale groups apart, the
+// phase covering a run of each tile's scale groups).
+template <int FB, bool TS = false>
 __device__ __forceinline__ gptr8 mv_base(const MvPhase& p, const MvGeom<FB>& g, int lane) {
+    if constexpr (TS) {
+        const int tl = g.f0 / g.NF;
+        return (gptr8)p.code + (size_t)(unsigned)((g.t0 + tl) * p.tstride + g.f0 - tl * g.NF) * ((FB + 1) * 1024) + lane * 16;
+    }
     return (gptr8)p.code + (size_t)(unsigned)(g.t0 * g.NF + g.f0) * ((FB + 1) * 1024) + lane * 16;
 }
 
-template <int FB>
+template <int FB, bool TS = false>
 __device__ __forceinline__ void mv_prefetch(const MvPhase p, int wg, int nwg, int wave, int lane, Ring<FB>& ring) {
     const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, wave);
     if (g.f1 <= g.f0) {   // every path defines the ring, so no earlier value stays live across phases
@@ -89,7 +94,7 @@ __device__ __forceinline__ void mv_prefetch(const MvPhase p, int wg, int nwg, in
         for (int d = 0; d <= FB; d++) ring.u[d] = uint4{0u, 0u, 0u, 0u};
         return;
     }
-    const gptr8 b = mv_base<FB>(p, g, lane);
+    const gptr8 b = mv_base<FB, TS>(p, g, lane);
 #pragma unroll
     for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
 }
@@ -176,7 +181,7 @@ __device__ __forceinline__ float pack_x16(const float* xf, int K, float gmax, co
 
 // Streams the wave's scale groups (the first already in the ring), leaving per-tile partial row
 // sums in part[(tile * MK_WAVES + wave) * 16 + row] (LDS) for mv_finish.
-template <int FB, bool STRAIGHT = false>
+template <int FB, bool STRAIGHT = false, bool TS = false>
 __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const float* gsum, const float* zero16, int wg, int nwg,
                                        int wave, int lane, Ring<FB>& ring, float* part) {
     constexpr int GSH = FB == 4 ? 5 : 6;          // log2 of the group size
@@ -184,14 +189,17 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
     const int nfb = g.f1 - g.f0;
     if (nfb <= 0) return;
     const int gpr = p.K >> GSH;                   // groups per row
-    const gptr8 base = mv_base<FB>(p, g, lane);
+    const gptr8 base = mv_base<FB, TS>(p, g, lane);
     const int col = lane & 15;
     f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f};
     int tile = g.f0 / g.NF, f = g.f0 - tile * g.NF;   // scale group within the tile
+    gptr8 cur = base;                                 // TS: this scale group's address
     for (int i = 0; i < nfb; i++) {
         // the next scale group streams in behind this one (none after the last: no load is left in flight)
         const bool more = i + 1 < nfb;
-        const gptr8 nxt = base + (int64_t)(i + 1) * ((FB + 1) * 1024);
+        gptr8 nxt;
+        if constexpr (TS) nxt = cur = cur + (int64_t)(f + 1 == g.NF ? p.tstride - g.NF + 1 : 1) * ((FB + 1) * 1024);
+        else nxt = base + (int64_t)(i + 1) * ((FB + 1) * 1024);
         const uint4 sbr = ring.u[0];
         if (more) ring.u[0] = ld_stream16(nxt);
         const float* xb = xh + (lane >> 4) * 4 + f * (4 * FB) * XH_STRIDE;   // this lane's slot of the group's first chunk

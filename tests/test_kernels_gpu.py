@@ -240,6 +240,24 @@ def test_qmv_tiles_epilogues(gpu, gs):
     assert np.all(zero == 0.0)
 
 
+def test_qmv_tiles_input_slices_share_scratch(gpu):
+    """The input-sliced matvec (a projection whose tiles are too few for the CUs runs as several
+    input slices per tile, the last slice of a tile adding the partials) over one scratch shared by
+    launches of different shapes and slice counts: a small projection, a larger one whose partials
+    cover the small one's scratch, then the small one again (its per-tile counters must still read
+    zero), each against the oracle's fp64 product at the matvec gate, plain and accumulating."""
+    rng = np.random.default_rng(3)
+    cases = [(16384, 40), (12288, 1024), (16384, 40), (27648, 24), (16384, 40)]   # 2, 2, 2, 8, 2 slices
+    fx = {}
+    for K, O in cases:
+        f = fx.setdefault((K, O), QuantFixture(O, K, 4, 64, seed=K + O, fast=True))
+        x = rng.normal(0, 1, K).astype(np.float32)
+        ref = f.oracle(oracle).matmul_f64(x)[0]
+        assert max_rel_err(qmv_tiles(gpu, [f], x), ref) < TOL, (K, O)
+        y0 = rng.normal(0, 1, O).astype(np.float32)
+        assert max_rel_err(qmv_tiles(gpu, [f], x, mode=1, y0=y0), y0 + ref) < TOL, (K, O)
+
+
 def _decode_input(kind, K, rng):
     """Inputs as the decode step feeds each projection: RMSNorm'd hidden state (q|k|v, gate|up,
     lm_head: passed raw with the norm weights, the norm runs in the kernel), the attention output
