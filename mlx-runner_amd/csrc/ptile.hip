@@ -32,14 +32,15 @@ typedef uint32_t q4u4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int PT_M = 128, PT_TILES = 16, PT_KB = 128;
+constexpr int PT_M = 128, PT_KB = 128;
 constexpr int PT_XB = PT_M * 256;                   // X block
-constexpr int PT_CB = PT_TILES * 1024;              // code blocks
-constexpr int PT_SB = PT_TILES * 256;               // the scale words of one block's groups
-constexpr int PT_STAGE = PT_XB + PT_CB + PT_SB;
-constexpr int PT_NST = 3;                           // stages: copies run two blocks ahead
-constexpr int PT_LDS = PT_NST * PT_STAGE;
-constexpr int PT_WAIT_ONE_AHEAD = 0x0F77;           // s_waitcnt vmcnt(7): one block's copies still in flight
+// RT row tiles per wave (16 RT per workgroup), NST stages: (2, 3) by default; (3, 2) where a
+// launch of 16-tile workgroups would leave a round half empty (the q|k|v projection of the 8B
+// models: 384 tiles)
+template <int RT> constexpr int pt_stage() { return PT_XB + 8 * RT * 1024 + 8 * RT * 256; }
+template <int RT, int NST> constexpr int pt_lds_bytes() { return NST * pt_stage<RT>(); }
+// s_waitcnt vmcnt(n), expcnt and lgkmcnt not waited for: one block's n copies of a wave in flight
+constexpr int pt_wait_vm(int n) { return 0x0F70 | n; }
 constexpr int PT_RSRC_W3 = 0x00020000;              // raw buffer, 32-bit data format
 
 struct TileGemmArgs {
@@ -53,12 +54,16 @@ __device__ __forceinline__ half2_t bf16_half2(uint32_t raw16) {
     return half2_t{h, h};
 }
 
-template <int GATED>
+template <int GATED, int RT, int NST>
 __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
+    constexpr int PT_TILES = 8 * RT, PT_CB = PT_TILES * 1024, PT_STAGE = pt_stage<RT>();
+    constexpr int NCP = 4 + RT + 1;                 // copies a wave issues per block
+    static_assert(NCP < 16 && NST >= 2 && NST <= 3, "copy pipeline");
     extern __shared__ __attribute__((aligned(1024))) uint8_t pt_lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wq = wave & 3, kc = wave >> 2;
+    // the wave's first tile within the workgroup's
+    const int wt0 = RT == 2 ? 4 * (wave & 3) + 2 * (wave >> 2) : RT * wave;
     // tile order: XCD x runs workgroups x, x + 8, ...; give it a contiguous run of tiles, and
     // enumerate tiles in columns of 8 row-tiles so that the ~32 workgroups an XCD runs at once cover
     // 4 token tiles x 8 row tiles (X and W blocks each shared in its L2 by several workgroups)
@@ -74,18 +79,19 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
     // tiles past the matrix read out of range (zeros)
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.p.code, 0, (int)(a.p.tiles * tile_bytes),
                                                                          PT_RSRC_W3);
-    f32x4_t acc[8][2];
+    f32x4_t acc[8][RT];
 #pragma unroll
     for (int i = 0; i < 8; i++)
 #pragma unroll
-        for (int u = 0; u < 2; u++) acc[i][u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int u = 0; u < RT; u++) acc[i][u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // this wave's copies of block blk (7 per wave): X rows 16 w .. 16 w + 15 (4 x 1 KB), the code
-    // blocks of workgroup tiles 2 w, 2 w + 1, and their scale words of the block's 128 / gs groups
-    // (lanes 0-31: tile 2 w + (lane >> 4), 16-byte chunk (rows 4 rq .. 4 rq + 3, group gl) with
-    // lane & 15 = 4 rq + gl; chunks past the block's groups are loaded and never read)
+    // this wave's copies of block blk (NCP per wave): X rows 16 w .. 16 w + 15 (4 x 1 KB), the code
+    // blocks of workgroup tiles RT w .. RT w + RT - 1, and their scale words of the block's
+    // 128 / gs groups (lanes 0 .. 16 RT - 1: tile RT w + (lane >> 4), 16-byte chunk (rows 4 rq ..
+    // 4 rq + 3, group gl) with lane & 15 = 4 rq + gl; chunks past the block's groups are loaded and
+    // never read)
     auto issue = [&](int blk) {
-        uint8_t* st = pt_lds + (blk % PT_NST) * PT_STAGE;
+        uint8_t* st = pt_lds + (blk % NST) * PT_STAGE;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int qq = wave * 4 + q, r = 4 * qq + kq;
@@ -94,16 +100,16 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
         }
         const int f = blk / FB, bl = blk - f * FB;
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int tw = 2 * wave + c;
+        for (int c = 0; c < RT; c++) {
+            const int tw = RT * wave + c;
             const uint32_t base = (uint32_t)(t0 + tw) * tile_bytes + (uint32_t)f * (FB + 1) * 1024 + lane * 16;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(st + PT_XB + tw * 1024), 16, base + (bl + 1) * 1024, 0, 0, 0);
         }
-        if (lane < 32) {
-            const int tw = 2 * wave + (lane >> 4), l = lane & 15;
+        if (lane < 16 * RT) {
+            const int tw = RT * wave + (lane >> 4), l = lane & 15;
             const uint32_t off = (uint32_t)(t0 + tw) * tile_bytes + (uint32_t)f * (FB + 1) * 1024 +
                                  ((l >> 2) * 16 + bl * (PT_KB / a.p.gs) + (l & 3)) * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(st + PT_XB + PT_CB + 2 * wave * 256), 16, off, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(st + PT_XB + PT_CB + RT * wave * 256), 16, off, 0, 0, 0);
         }
     };
 
@@ -111,26 +117,26 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
     // (k = 32 j + 8 kq + 0..7) and the X fragment of the same k; step j + 1's X fragments and
     // dequantized W are produced while step j's MFMAs run.
     auto compute = [&](int blk, int pf) {
-        const uint8_t* st = pt_lds + (blk % PT_NST) * PT_STAGE;
+        const uint8_t* st = pt_lds + (blk % NST) * PT_STAGE;
         const uint8_t* sc = st + PT_XB + PT_CB;
-        q4u4_t cw[2];
+        q4u4_t cw[RT];
 #pragma unroll
-        for (int u = 0; u < 2; u++) cw[u] = *reinterpret_cast<const q4u4_t*>(st + PT_XB + (4 * wq + 2 * kc + u) * 1024 + lane * 16);
-        half2_t s2[4][2], b2[4][2];
+        for (int u = 0; u < RT; u++) cw[u] = *reinterpret_cast<const q4u4_t*>(st + PT_XB + (wt0 + u) * 1024 + lane * 16);
+        half2_t s2[4][RT], b2[4][RT];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int gl = (32 * j) / a.p.gs;                      // group within the block
             const int so = ((r16 >> 2) * 4 + gl) * 16 + (r16 & 3) * 4;
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(sc + (4 * wq + 2 * kc + u) * 256 + so);
+            for (int u = 0; u < RT; u++) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(sc + (wt0 + u) * 256 + so);
                 s2[j][u] = bf16_half2(w & 0xFFFFu);
                 b2[j][u] = bf16_half2(w >> 16);
             }
         }
         auto dequant = [&](int j, half8_t* wf) {
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
+            for (int u = 0; u < RT; u++) {
                 const uint32_t wv = cw[u][j];
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
@@ -148,7 +154,7 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
             for (int i = 0; i < 8; i++)
                 xf[i] = *reinterpret_cast<const half8_t*>(st + (16 * i + r16) * 256 + 16 * ((4 * j + kq) ^ r16));
         };
-        half8_t xf[2][8], wf[2][2];
+        half8_t xf[2][8], wf[2][RT];
         xload(0, xf[0]);
         dequant(0, wf[0]);
 #pragma unroll
@@ -159,12 +165,12 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; i++)
 #pragma unroll
-                for (int u = 0; u < 2; u++)
+                for (int u = 0; u < RT; u++)
                     acc[i][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[j & 1][u], xf[j & 1][i], acc[i][u], 0, 0, 0);
             if (j < 3) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-                for (int k = 0; k < 16; k++) {
+                for (int k = 0; k < 8 * RT; k++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
                 }
@@ -174,20 +180,21 @@ __global__ __launch_bounds__(512, 1) void tile_gemm_kernel(TileGemmArgs a) {
     };
 
     issue(0);
-    if (nb > 1) issue(1);
+    if (NST == 3 && nb > 1) issue(1);
     for (int blk = 0; blk < nb; blk++) {
-        // this wave's copies of block blk have landed (block blk + 1's may still be in flight) ...
-        if (blk + 1 < nb) __builtin_amdgcn_s_waitcnt(PT_WAIT_ONE_AHEAD);
+        // this wave's copies of block blk have landed (with three stages block blk + 1's may still
+        // be in flight) ...
+        if (NST == 3 && blk + 1 < nb) __builtin_amdgcn_s_waitcnt(pt_wait_vm(NCP));
         else __builtin_amdgcn_s_waitcnt(0);
-        // ... and every wave's; block blk - 1's stage, which block blk + 2 overwrites, is no longer
-        // read. A bare s_barrier: __syncthreads' fence adds nothing here.
+        // ... and every wave's; block blk + 1 - NST's stage, which block blk + NST - 1 overwrites,
+        // is no longer read. A bare s_barrier: __syncthreads' fence adds nothing here.
         __builtin_amdgcn_s_barrier();
-        compute(blk, blk + 2 < nb ? blk + 2 : -1);
+        compute(blk, blk + NST - 1 < nb ? blk + NST - 1 : -1);
     }
-    // lane holds, for token m0 + 16 i + r16, rows 4 kq .. 4 kq + 3 of tile t0 + 4 wq + 2 kc + u
+    // lane holds, for token m0 + 16 i + r16, rows 4 kq .. 4 kq + 3 of tile t0 + wt0 + u
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int t = t0 + 4 * wq + 2 * kc + u;
+    for (int u = 0; u < RT; u++) {
+        const int t = t0 + wt0 + u;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int m = m0 + 16 * i + r16;
@@ -236,24 +243,43 @@ bool tile_gemm_supported(const MvPhaseDesc& p) {
     return p.code && (p.gs == 32 || p.gs == 64) && p.K % PT_KB == 0 && p.tiles > 0;
 }
 
+template <int RT, int NST>
+static hipError_t tile_gemm_launch(const TileGemmArgs& a0, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        for (const void* f : {(const void*)tile_gemm_kernel<0, RT, NST>, (const void*)tile_gemm_kernel<1, RT, NST>})
+            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, pt_lds_bytes<RT, NST>()) != hipSuccess)
+                return hipErrorInvalidValue;
+        attr = true;
+    }
+    TileGemmArgs a = a0;
+    a.ntiles = a.nT * ((a.p.tiles + 8 * RT - 1) / (8 * RT));
+    constexpr int lds = pt_lds_bytes<RT, NST>();
+    if (a.p.gated) hipLaunchKernelGGL((tile_gemm_kernel<1, RT, NST>), dim3(a.ntiles), dim3(512), lds, s, a);
+    else hipLaunchKernelGGL((tile_gemm_kernel<0, RT, NST>), dim3(a.ntiles), dim3(512), lds, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_tile_gemm(const MvPhaseDesc& p, const uint16_t* xh, const float* inv, int T, float* y, int ys,
                             hipStream_t s) {
     if (!tile_gemm_supported(p) || T < 1) return hipErrorInvalidValue;
-    static bool attr = false;
-    if (!attr) {
-        if (hipFuncSetAttribute((const void*)tile_gemm_kernel<0>, hipFuncAttributeMaxDynamicSharedMemorySize, PT_LDS) != hipSuccess ||
-            hipFuncSetAttribute((const void*)tile_gemm_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, PT_LDS) != hipSuccess)
-            return hipErrorInvalidValue;
-        attr = true;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return hipErrorInvalidDevice;
     }
     TileGemmArgs a;
     a.p = p; a.xh = xh; a.inv = inv; a.y = y; a.ys = ys; a.T = T;
     a.nT = (T + PT_M - 1) / PT_M;
-    const int nO = (p.tiles + PT_TILES - 1) / PT_TILES;
-    a.ntiles = a.nT * nO;
-    if (p.gated) hipLaunchKernelGGL(tile_gemm_kernel<1>, dim3(a.ntiles), dim3(512), PT_LDS, s, a);
-    else hipLaunchKernelGGL(tile_gemm_kernel<0>, dim3(a.ntiles), dim3(512), PT_LDS, s, a);
-    return hipGetLastError();
+    // one workgroup per CU: rounds of workgroups x tiles per workgroup, the two-stage pipeline of the
+    // 24-tile workgroups costing ~4% (measured on the 16-tile ones)
+    auto cost = [&](int rt) {
+        const long wgs = (long)a.nT * ((p.tiles + 8 * rt - 1) / (8 * rt));
+        return (double)((wgs + cus - 1) / cus) * rt * (rt == 3 ? 1.04 : 1.0);
+    };
+    if (cost(3) < cost(2)) return tile_gemm_launch<3, 2>(a, s);
+    return tile_gemm_launch<2, 3>(a, s);
 }
 
 }  // namespace mlxr
