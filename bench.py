@@ -5,9 +5,10 @@ group 64 (bf16 scale/bias), bf16 KV cache; a 4096-token prompt of random ids is 
 batch-1 greedy decode. A "step" is one decode token: W untimed steps, then K timed steps issued as
 the reference's pipelined loop does (step n+1 committed before step n is read back, Engine.swift:740-763),
 bracketed by device synchronisation. value = decode tokens/s of the whole job (one GPU).
-`--mode prefill` runs configs[2] instead (Llama-3-8B shape, one 2048-token prefill per step),
-`--mode sweep` configs[3] (the matvec / GEMM sweep), `--mode long` configs[4] (Qwen2.5-32B shape,
-32K context, sparse decode attention, reused prefix).
+`--mode small` runs configs[0] instead (Qwen3-0.6B shape, 32 + 64 tokens), `--mode prefill`
+configs[2] (Llama-3-8B shape, one 2048-token prefill per step), `--mode sweep` configs[3] (the
+matvec / GEMM sweep), `--mode long` configs[4] (Qwen2.5-32B shape, 32K context, sparse decode
+attention, reused prefix).
 
 Extra objects on the JSON line:
 - roofline: the dominant kernel, the persistent decode step (one launch per token: every layer,
@@ -19,8 +20,9 @@ Extra objects on the JSON line:
 - step_roofline: the same accounting for the whole decode step (bytes per token at the mean context);
 - prefill: prompt tokens/s of the 4096-token prefill (the config's second metric), with its flops
   (prefill_flops) against the MFMA peak;
-- prefill_config3 / long_config5: the `--mode prefill` and `--mode long`
-  results, each with its own roofline, measured in the same run after the decode workload;
+- small_config1 / prefill_config3 / sweep_config4 / long_config5: the `--mode small`,
+  `--mode prefill`, `--mode sweep` and `--mode long` results,
+  each with its own roofline, measured in the same run after the decode workload;
 - cpu_baseline: the CPU oracle (C restatement of the reference's semantics, all host cores) timed on
   a bounded sample: decode steps at the same context, starting from the GPU-built KV cache.
 """
@@ -57,6 +59,59 @@ def model_dir(name, seed):
         open(marker, "w").write("ok")
         log(f"[bench] synthetic model written in {time.time() - t:.1f}s")
     return d
+
+
+def small_main(a):
+    """the Qwen3-0.6B shape, a 32-token random prompt, then 64 greedy decode steps (the
+    reference's short-context decode benchmark). The prompt and steps run once untimed, then again
+    timed from a fresh prefill; value = decode tok/s over the 64 steps (two in flight, as the main
+    line); roofline = the persistent step kernel (HIP events) against the HBM peak."""
+    cfg = configs.CONFIGS[a.config]
+    d = model_dir(a.config, a.seed)
+    n_prompt, n_steps = 32, 64
+    model = mlxr.Transformer(d, context_length=n_prompt + n_steps + a.step_iters + 16)
+    greedy = mlxr.SamplingParameters.greedy()
+    prompt = np.random.default_rng(a.seed).integers(0, model.vocab_size, n_prompt).astype(np.int32)
+
+    def run():
+        model.prefill(prompt, 0, greedy)
+        mlxr.synchronize()
+        t = time.perf_counter()
+        cur = model.begin_decode_step(n_prompt, greedy)
+        toks = []
+        for i in range(n_steps):
+            nxt = model.begin_decode_step(cur.offset + 1, greedy) if i + 1 < n_steps else None
+            toks.append(model.finish(cur))
+            cur = nxt
+        mlxr.synchronize()
+        return time.perf_counter() - t, toks
+
+    run()
+    el, toks = run()
+    tok_s = n_steps / el
+    mean_ctx = n_prompt + n_steps / 2
+    step_ms, step_b = model.profile_kernel("step", a.step_iters, n_prompt + n_steps)
+    step_gbs = step_b / (step_ms * 1e-3) / 1e9
+    log(f"[bench] {a.config} decode {n_steps} steps after {n_prompt} prompt tokens: {el * 1e3:.1f} ms, {tok_s:.1f} tok/s; "
+        f"step kernel {step_ms * 1e3:.1f} us, {step_gbs:.0f} GB/s")
+    result = {
+        "metric": "decode tok/s (bs1, 0.6B-shape 4-bit g64, 32-token prompt + 64 greedy steps) + % HBM roofline",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": n_steps, "warmup": n_steps,
+        "ms_per_step": round(el * 1e3 / n_steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u4 weights (affine g64, bf16 scale/bias); x as f16 hi+lo MFMA operands, fp32 accumulate, bf16 KV",
+        "data": "synthetic: random-init weights N(0,0.02) from a seed, uniform random prompt ids",
+        "config": {"workload": f"{a.config}: {n_prompt}-token prompt + {n_steps} greedy decode steps (configs[0])",
+                   "model": a.config, "global_batch": 1, "seq_len": n_prompt + n_steps, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "decode_step_kernel (persistent: whole token step in one launch)",
+                     "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": round(step_ms * 1e3, 2), "bytes_per_launch": int(step_b)},
+        "step_roofline": {"bytes_per_token": int(step_bytes(cfg, mean_ctx)),
+                          "frac": round(step_bytes(cfg, mean_ctx) * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
+        "first_tokens": toks[:8],
+    }
+    model.close()
+    return result
 
 
 def weight_bytes(cfg):
@@ -187,7 +242,7 @@ def sweep_main(a):
         "gemm_T512": {"best_TFLOPs": max(c["TFLOPs"] for c in gemm), "peak": MFMA_PEAK_TFS},
         "cells": cells,
     }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def long_main(a):
@@ -294,16 +349,18 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="decode only: skip the prefill_config3 and long_config5 sub-objects (configs[2] and [4])")
+                    help="decode only: skip the small_config1, prefill_config3, sweep_config4 and long_config5 "
+                         "sub-objects (configs[0], [2], [3] and [4])")
     ap.add_argument("--kernel-iters", type=int, default=360)
     ap.add_argument("--step-iters", type=int, default=64)
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch the kernel-per-op decode step kernel by kernel (profiling) instead of as a hipGraph")
     ap.add_argument("--decode-mode", type=int, default=1, choices=[0, 1, 2],
                     help="1: persistent decode step, 0: kernel per op (repacked tiles), 2: kernel per op (MLX layout)")
-    ap.add_argument("--mode", default="decode", choices=["decode", "prefill", "sweep", "long"],
-                    help="decode: configs[1] (default); prefill: configs[2] (llama3-8b, 2048 tokens unless given); "
-                         "sweep: configs[3]; long: configs[4] (qwen2.5-32b, 32768-token context, sparse)")
+    ap.add_argument("--mode", default="decode", choices=["decode", "small", "prefill", "sweep", "long"],
+                    help="decode: configs[1] (default); small: configs[0] (qwen3-0.6b, 32 + 64 tokens); prefill: "
+                         "configs[2] (llama3-8b, 2048 tokens unless given); sweep: configs[3]; long: configs[4] "
+                         "(qwen2.5-32b, 32768-token context, sparse)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run 3 device-to-device copy kernels of MB MiB each (calibrates rocprofv3 byte counters)")
     a = ap.parse_args()
@@ -335,7 +392,13 @@ def main():
         print(json.dumps(prefill_main(a)), flush=True)
         return
     if a.mode == "sweep":
-        return sweep_main(a)
+        print(json.dumps(sweep_main(a)), flush=True)
+        return
+    if a.mode == "small":
+        if "--config" not in sys.argv:
+            a.config = "qwen3-0.6b"
+        print(json.dumps(small_main(a)), flush=True)
+        return
     if a.mode == "long":
         if "--config" not in sys.argv:
             a.config = "qwen2.5-32b"
@@ -440,10 +503,14 @@ def main():
         result["cpu_baseline"] = cpu_baseline(d, model, cfg, pos + a.steps, a.cpu_tokens, a.cpu_budget)
     model.close()
     if not a.no_extra:
-        # the other two model workloads, measured in the same run (short: a few seconds of GPU time each)
+        # the other workloads, measured in the same run (short: seconds of GPU time each)
+        sa = argparse.Namespace(**vars(a))
+        sa.config, sa.step_iters = "qwen3-0.6b", 64
+        result["small_config1"] = _sub(small_main(sa))
         pa = argparse.Namespace(**vars(a))
         pa.config, pa.context, pa.steps, pa.warmup = "llama3-8b", 2048, 5, 1
         result["prefill_config3"] = _sub(prefill_main(pa))
+        result["sweep_config4"] = _sub(sweep_main(argparse.Namespace(**vars(a))))
         la = argparse.Namespace(**vars(a))
         la.config, la.context, la.steps, la.warmup = "qwen2.5-32b", 32768, 64, 4
         result["long_config5"] = _sub(long_main(la))

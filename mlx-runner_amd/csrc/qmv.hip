@@ -4,10 +4,14 @@
 // generic `qmm` (Kernels.swift:60-113): y[o] = sum over groups of s * (sum_j q_j x_j) + b * (sum_j x_j),
 // fp32 accumulation, rows of up to three matrices [A | B | C] concatenated, optional per-row bias.
 //
-// MI355X layout: a 256-thread workgroup (4 waves of 64) owns ROWS rows per wave. A lane consumes one
-// 32-code chunk of a row per step (4*BITS bytes: one 16-byte load at 4 bits), so a wave streams a
-// contiguous 64*4*BITS-byte span of the row per load instruction (fully coalesced), and every row of
-// the wave reuses the lane's 32 x values. Codes are extracted without shifts where possible: at
+// MI355X layout: a 256-thread workgroup (4 waves of 64) owns ROWS rows per wave; for inputs of at
+// least 64 chunks per wave (K >= 8192, below 8 bits) the four waves share the same ROWS rows and take a quarter of
+// K each instead (so short-N, long-K projections still spread over many workgroups, and each
+// wave's chain of loads is a quarter as long), their partial sums meeting in LDS, added in wave
+// order. A lane
+// consumes one 32-code chunk of a row per step (4*BITS bytes: one 16-byte load at 4 bits), so a
+// wave streams a contiguous 64*4*BITS-byte span of the row per load instruction (fully coalesced),
+// and every row reuses the lane's 32 x values. Codes are extracted without shifts where possible: at
 // 4 bits the dword is split into low/high nibbles of its four bytes and each byte converted with the
 // byte-to-float conversion. The workgroup can normalise x itself (RMSNorm of the residual stream
 // times the norm weight, written to LDS) so the norm needs no kernel of its own.
@@ -83,8 +87,8 @@ __device__ __forceinline__ void load_chunk(const uint8_t* p, uint32_t* w) {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
-// XNORM: x is normalised into LDS by the workgroup (K floats).
-template <int BITS, int ST, bool XNORM>
+// XNORM: x is normalised into LDS by the workgroup (K floats). KS: the waves split K over the same rows.
+template <int BITS, int ST, bool XNORM, bool KS>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
     extern __shared__ __attribute__((aligned(16))) float xs_lds[];
     __shared__ float red[QMV_WAVES];
@@ -113,8 +117,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
     }
     const bool gated = a.epi == EPI_GATED;
     const int rows_per_wave = QMV_ROWS;
-    const int slot0 = (blockIdx.x * QMV_WAVES + wave) * (gated ? rows_per_wave / 2 : rows_per_wave);
-    if (slot0 >= a.O) return;
+    const int slot0 = (KS ? blockIdx.x : blockIdx.x * QMV_WAVES + wave) * (gated ? rows_per_wave / 2 : rows_per_wave);
+    if (!KS && slot0 >= a.O) return;
     const int64_t rowBytes = (int64_t)K * BITS / 8;
     const int gpr = K / a.gs;
     const uint8_t* wp[QMV_ROWS]; const uint16_t* sp[QMV_ROWS]; const uint16_t* bp[QMV_ROWS];
@@ -145,7 +149,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
 #pragma unroll
     for (int r = 0; r < QMV_ROWS; r++) acc[r] = 0.0f;
     const int nchunks = K >> 5;
-    for (int c = lane; c < nchunks; c += 64) {
+    const int cq0 = KS ? nchunks * wave / QMV_WAVES : 0, cq1 = KS ? nchunks * (wave + 1) / QMV_WAVES : nchunks;
+    for (int c = cq0 + lane; c < cq1; c += 64) {
         const int k0 = c << 5;
         uint32_t w[QMV_ROWS][BITS];
 #pragma unroll
@@ -169,6 +174,17 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
     }
 #pragma unroll
     for (int r = 0; r < QMV_ROWS; r++) acc[r] = wave_sum(acc[r]);
+    if constexpr (KS) {
+        __shared__ float wred[QMV_WAVES][QMV_ROWS];
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < QMV_ROWS; r++) wred[wave][r] = acc[r];
+        }
+        __syncthreads();
+        if (wave != 0 || slot0 >= a.O) return;
+#pragma unroll
+        for (int r = 0; r < QMV_ROWS; r++) acc[r] = ((wred[0][r] + wred[1][r]) + wred[2][r]) + wred[3][r];
+    }
     if (lane != 0) return;
     if (gated) {
 #pragma unroll
@@ -198,15 +214,16 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
 }
 
 template <int BITS, int ST, bool XNORM>
-static hipError_t qmv_launch(const QmvDev& d, int grid, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM>), dim3(grid), dim3(256), lds, s, d);
+static hipError_t qmv_launch(const QmvDev& d, bool ks, int grid, size_t lds, hipStream_t s) {
+    if (ks) hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM, true>), dim3(grid), dim3(256), lds, s, d);
+    else hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM, false>), dim3(grid), dim3(256), lds, s, d);
     return hipGetLastError();
 }
 
 template <int BITS>
-static hipError_t qmv_dispatch_st(const QmvDev& d, int st, bool xn, int grid, size_t lds, hipStream_t s) {
-    if (st == 0) return xn ? qmv_launch<BITS, 0, true>(d, grid, lds, s) : qmv_launch<BITS, 0, false>(d, grid, lds, s);
-    return xn ? qmv_launch<BITS, 1, true>(d, grid, lds, s) : qmv_launch<BITS, 1, false>(d, grid, lds, s);
+static hipError_t qmv_dispatch_st(const QmvDev& d, int st, bool xn, bool ks, int grid, size_t lds, hipStream_t s) {
+    if (st == 0) return xn ? qmv_launch<BITS, 0, true>(d, ks, grid, lds, s) : qmv_launch<BITS, 0, false>(d, ks, grid, lds, s);
+    return xn ? qmv_launch<BITS, 1, true>(d, ks, grid, lds, s) : qmv_launch<BITS, 1, false>(d, ks, grid, lds, s);
 }
 
 hipError_t launch_qmv(const QmvArgs& a, hipStream_t s) {
@@ -218,17 +235,20 @@ hipError_t launch_qmv(const QmvArgs& a, hipStream_t s) {
     d.o1 = a.part[0].O; d.o2 = a.nparts > 1 ? a.part[1].O : 0;
     d.K = a.K; d.gs = a.gs; d.O = a.O; d.epi = a.epi; d.hasBias = a.part[0].bias != nullptr;
     d.x = a.x; d.norm_w = a.norm_w; d.eps = a.eps; d.y = a.y;
-    const int per_wg = QMV_WAVES * (a.epi == EPI_GATED ? QMV_ROWS / 2 : QMV_ROWS);
+    // measured on the 14336-input sweep cells: 3 / 4 / 6 bits 19.3 / 18.9 / 21.1 -> 12.9 / 13.5 / 15.6 us;
+    // 8-bit rows (twice the bytes per chunk, each wave's loads already busy) 18.6 -> 21.9, so not those
+    const bool ks = (a.K >> 5) >= 64 * QMV_WAVES && a.bits < 8;
+    const int per_wg = (ks ? 1 : QMV_WAVES) * (a.epi == EPI_GATED ? QMV_ROWS / 2 : QMV_ROWS);
     const int grid = (a.O + per_wg - 1) / per_wg;
     const bool xn = a.norm_w != nullptr;
     const size_t lds = xn ? (size_t)a.K * sizeof(float) : 0;
     switch (a.bits) {
-        case 2: return qmv_dispatch_st<2>(d, a.st, xn, grid, lds, s);
-        case 3: return qmv_dispatch_st<3>(d, a.st, xn, grid, lds, s);
-        case 4: return qmv_dispatch_st<4>(d, a.st, xn, grid, lds, s);
-        case 5: return qmv_dispatch_st<5>(d, a.st, xn, grid, lds, s);
-        case 6: return qmv_dispatch_st<6>(d, a.st, xn, grid, lds, s);
-        case 8: return qmv_dispatch_st<8>(d, a.st, xn, grid, lds, s);
+        case 2: return qmv_dispatch_st<2>(d, a.st, xn, ks, grid, lds, s);
+        case 3: return qmv_dispatch_st<3>(d, a.st, xn, ks, grid, lds, s);
+        case 4: return qmv_dispatch_st<4>(d, a.st, xn, ks, grid, lds, s);
+        case 5: return qmv_dispatch_st<5>(d, a.st, xn, ks, grid, lds, s);
+        case 6: return qmv_dispatch_st<6>(d, a.st, xn, ks, grid, lds, s);
+        case 8: return qmv_dispatch_st<8>(d, a.st, xn, ks, grid, lds, s);
     }
     return hipErrorInvalidValue;
 }
