@@ -254,8 +254,15 @@ hipError_t launch_qmv(const QmvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Small batch: TT tokens per wave pass (weights unpacked once, reused for every token).
-constexpr int QMM_TT = 8;
+// Small batch (T = 2..8). A lane holds x of its 32-code chunk for up to QMM_TP tokens in registers
+// and reuses it for QMM_R rows (each row's codes converted once and dotted with every token), so x
+// is loaded once per chunk per pass instead of once per row and token. More than QMM_TP tokens take
+// a second pass over the same rows (their weights then come from the caches). For inputs of at
+// least 64 chunks per wave the four waves split K over the same rows (partial sums added in LDS in
+// wave order), else each wave takes its own rows.
+constexpr int QMM_TT = 8;    // tokens (max)
+constexpr int QMM_TP = 4;    // tokens per pass
+constexpr int QMM_R = 8;     // rows per wave
 
 struct QmmDev {
     const uint8_t* w[3]; const uint16_t* s[3]; const uint16_t* b[3]; const uint16_t* bias[3];
@@ -263,74 +270,132 @@ struct QmmDev {
     const float* x; float* y;
 };
 
-template <int BITS, int ST>
+template <int BITS>
+__device__ __forceinline__ void unpack_chunk(const uint32_t* w, float* q) {
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+            q[8 * i + 0] = (float)(lo & 0xFFu);         q[8 * i + 1] = (float)(hi & 0xFFu);
+            q[8 * i + 2] = (float)((lo >> 8) & 0xFFu);  q[8 * i + 3] = (float)((hi >> 8) & 0xFFu);
+            q[8 * i + 4] = (float)((lo >> 16) & 0xFFu); q[8 * i + 5] = (float)((hi >> 16) & 0xFFu);
+            q[8 * i + 6] = (float)(lo >> 24);           q[8 * i + 7] = (float)(hi >> 24);
+        }
+    } else if constexpr (BITS == 8) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            q[4 * i + 0] = (float)(w[i] & 0xFFu);         q[4 * i + 1] = (float)((w[i] >> 8) & 0xFFu);
+            q[4 * i + 2] = (float)((w[i] >> 16) & 0xFFu); q[4 * i + 3] = (float)(w[i] >> 24);
+        }
+    } else {
+        constexpr uint32_t M = (1u << BITS) - 1u;
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const int bit = j * BITS, wi = bit >> 5, off = bit & 31;
+            uint32_t c;
+            if (off + BITS <= 32) c = (w[wi] >> off) & M;
+            else c = ((w[wi] >> off) | (w[wi + 1] << (32 - off))) & M;
+            q[j] = (float)c;
+        }
+    }
+}
+
+template <int BITS, int ST, bool KS>
 __global__ __launch_bounds__(256) void qmm_small_kernel(QmmDev a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int gr0 = (blockIdx.x * QMV_WAVES + wave) * QMV_ROWS;
-    if (gr0 >= a.O) return;
+    const int gr0 = (KS ? blockIdx.x : blockIdx.x * QMV_WAVES + wave) * QMM_R;
+    if (!KS && gr0 >= a.O) return;
     const int K = a.K;
     const int64_t rowBytes = (int64_t)K * BITS / 8;
     const int gpr = K / a.gs;
-    const uint8_t* wp[QMV_ROWS]; const uint16_t* sp[QMV_ROWS]; const uint16_t* bp[QMV_ROWS]; int gr[QMV_ROWS];
+    const uint8_t* wp[QMM_R]; const uint16_t* sp[QMM_R]; const uint16_t* bp[QMM_R]; int gr[QMM_R];
 #pragma unroll
-    for (int r = 0; r < QMV_ROWS; r++) {
-        int g = gr0 + r; gr[r] = g < a.O ? g : -1; if (g >= a.O) g = gr0;
+    for (int r = 0; r < QMM_R; r++) {
+        int g = gr0 + r; gr[r] = g < a.O ? g : -1; if (g >= a.O) g = min(gr0, a.O - 1);
         int part, row;
         if (g < a.o1) { part = 0; row = g; } else if (g < a.o1 + a.o2) { part = 1; row = g - a.o1; } else { part = 2; row = g - a.o1 - a.o2; }
         wp[r] = a.w[part] + row * rowBytes; sp[r] = a.s[part] + (int64_t)row * gpr; bp[r] = a.b[part] + (int64_t)row * gpr;
     }
-    float acc[QMV_ROWS][QMM_TT];
-#pragma unroll
-    for (int r = 0; r < QMV_ROWS; r++)
-#pragma unroll
-        for (int t = 0; t < QMM_TT; t++) acc[r][t] = 0.0f;
     const int nchunks = K >> 5;
-    for (int c = lane; c < nchunks; c += 64) {
-        const int k0 = c << 5;
-        const int g = k0 / a.gs;
-        uint32_t w[QMV_ROWS][BITS];
-        float sc[QMV_ROWS], bi[QMV_ROWS];
+    const int cq0 = KS ? nchunks * wave / QMV_WAVES : 0, cq1 = KS ? nchunks * (wave + 1) / QMV_WAVES : nchunks;
+    __shared__ float wred[QMV_WAVES][QMM_R][QMM_TP];
+    for (int t0 = 0; t0 < a.T; t0 += QMM_TP) {
+        const int nt = min(QMM_TP, a.T - t0);
+        float acc[QMM_R][QMM_TP];
 #pragma unroll
-        for (int r = 0; r < QMV_ROWS; r++) {
-            load_chunk<BITS>(wp[r] + (int64_t)c * (4 * BITS), w[r]);
-            sc[r] = ld_scale<ST>(sp[r] + g); bi[r] = ld_scale<ST>(bp[r] + g);
-        }
+        for (int r = 0; r < QMM_R; r++)
 #pragma unroll
-        for (int t = 0; t < QMM_TT; t++) {
-            if (t >= a.T) break;
-            float x[32];
-            const float* xp = a.x + (int64_t)t * a.xs + k0;
+            for (int t = 0; t < QMM_TP; t++) acc[r][t] = 0.0f;
+        for (int c = cq0 + lane; c < cq1; c += 64) {
+            const int k0 = c << 5, g = k0 / a.gs;
+            float x[QMM_TP][32], xsum[QMM_TP];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 v = *reinterpret_cast<const float4*>(xp + 4 * i);
-                x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+            for (int t = 0; t < QMM_TP; t++) {
+                const float* xp = a.x + (int64_t)(t0 + min(t, nt - 1)) * a.xs + k0;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float4 v = *reinterpret_cast<const float4*>(xp + 4 * i);
+                    x[t][4 * i] = v.x; x[t][4 * i + 1] = v.y; x[t][4 * i + 2] = v.z; x[t][4 * i + 3] = v.w;
+                }
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 32; j++) sum += x[t][j];
+                xsum[t] = sum;
             }
-            float xsum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 32; j++) xsum += x[j];
+            for (int r = 0; r < QMM_R; r++) {
+                uint32_t w[BITS];
+                load_chunk<BITS>(wp[r] + (int64_t)c * (4 * BITS), w);
+                const float sc = ld_scale<ST>(sp[r] + g), bi = ld_scale<ST>(bp[r] + g);
+                float q[32];
+                unpack_chunk<BITS>(w, q);
 #pragma unroll
-            for (int r = 0; r < QMV_ROWS; r++) acc[r][t] += sc[r] * chunk_dot<BITS>(w[r], x) + bi[r] * xsum;
+                for (int t = 0; t < QMM_TP; t++) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 32; j++) d = fmaf(q[j], x[t][j], d);
+                    acc[r][t] += sc * d + bi * xsum[t];
+                }
+            }
         }
-    }
 #pragma unroll
-    for (int r = 0; r < QMV_ROWS; r++)
+        for (int r = 0; r < QMM_R; r++)
 #pragma unroll
-        for (int t = 0; t < QMM_TT; t++) {
-            if (t >= a.T) break;
-            const float v0 = wave_sum(acc[r][t]);
-            if (lane == 0 && gr[r] >= 0) {
-                float v = v0;
+            for (int t = 0; t < QMM_TP; t++) acc[r][t] = wave_sum(acc[r][t]);
+        if constexpr (KS) {
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < QMM_R; r++)
+#pragma unroll
+                    for (int t = 0; t < QMM_TP; t++) wred[wave][r][t] = acc[r][t];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < QMM_R; r++)
+#pragma unroll
+                for (int t = 0; t < QMM_TP; t++) acc[r][t] = ((wred[0][r][t] + wred[1][r][t]) + wred[2][r][t]) + wred[3][r][t];
+            __syncthreads();   // wred is reused by the next pass
+        }
+        if (lane == 0 && (!KS || wave == 0)) {
+#pragma unroll
+            for (int r = 0; r < QMM_R; r++) {
+                if (gr[r] < 0) continue;
+                float bv = 0.0f;
                 if (a.hasBias) {
                     const int g = gr[r]; int part, row;
                     if (g < a.o1) { part = 0; row = g; } else if (g < a.o1 + a.o2) { part = 1; row = g - a.o1; } else { part = 2; row = g - a.o1 - a.o2; }
-                    v += ld_scale<ST>(a.bias[part] + row);
+                    bv = ld_scale<ST>(a.bias[part] + row);
                 }
-                a.y[(int64_t)t * a.ys + gr[r]] = v;
+#pragma unroll
+                for (int t = 0; t < QMM_TP; t++)
+                    if (t < nt) a.y[(int64_t)(t0 + t) * a.ys + gr[r]] = acc[r][t] + bv;
             }
         }
+    }
 }
 
 hipError_t launch_qmm_small(const QmmSmallArgs& a, hipStream_t s) {
+    if (a.T < 1 || a.T > QMM_TT) return hipErrorInvalidValue;
     QmmDev d{};
     for (int i = 0; i < 3; i++) {
         const QMat& m = a.part[i < a.nparts ? i : a.nparts - 1];
@@ -339,10 +404,14 @@ hipError_t launch_qmm_small(const QmmSmallArgs& a, hipStream_t s) {
     d.o1 = a.part[0].O; d.o2 = a.nparts > 1 ? a.part[1].O : 0;
     d.K = a.K; d.gs = a.gs; d.O = a.O; d.T = a.T; d.hasBias = a.part[0].bias != nullptr;
     d.xs = a.x_stride; d.ys = a.y_stride; d.x = a.x; d.y = a.y;
-    const int grid = (a.O + QMV_WAVES * QMV_ROWS - 1) / (QMV_WAVES * QMV_ROWS);
+    const bool ks = (a.K >> 5) >= 64 * QMV_WAVES;
+    const int per_wg = (ks ? 1 : QMV_WAVES) * QMM_R;
+    const int grid = (a.O + per_wg - 1) / per_wg;
 #define QMM_CASE(B) case B: \
-    if (a.st == 0) hipLaunchKernelGGL((qmm_small_kernel<B, 0>), dim3(grid), dim3(256), 0, s, d); \
-    else hipLaunchKernelGGL((qmm_small_kernel<B, 1>), dim3(grid), dim3(256), 0, s, d); \
+    if (ks) { if (a.st == 0) hipLaunchKernelGGL((qmm_small_kernel<B, 0, true>), dim3(grid), dim3(256), 0, s, d); \
+              else hipLaunchKernelGGL((qmm_small_kernel<B, 1, true>), dim3(grid), dim3(256), 0, s, d); } \
+    else { if (a.st == 0) hipLaunchKernelGGL((qmm_small_kernel<B, 0, false>), dim3(grid), dim3(256), 0, s, d); \
+           else hipLaunchKernelGGL((qmm_small_kernel<B, 1, false>), dim3(grid), dim3(256), 0, s, d); } \
     return hipGetLastError();
     switch (a.bits) { QMM_CASE(2) QMM_CASE(3) QMM_CASE(4) QMM_CASE(5) QMM_CASE(6) QMM_CASE(8) }
 #undef QMM_CASE
