@@ -8,7 +8,8 @@
 // Tiling: a 256-thread workgroup owns a 128-token x 128-row output tile; each wave a 64 x 64
 // quarter (4 x 4 MFMA tiles of 16 x 16). K advances 64 at a time: the X tile (bf16) and the
 // dequantized W tile are staged in LDS with a padded row stride (72 bf16) so the 16-byte fragment
-// reads of 16 consecutive rows fall in different banks.
+// reads of 16 consecutive rows fall in different banks; the next step's global loads are issued
+// into registers before the current step's MFMAs.
 #include "kernels.h"
 
 namespace mlxr {
@@ -80,25 +81,35 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QGemmDev a) {
     const uint16_t* sp = a.s + (int64_t)wrow * gpr;
     const uint16_t* bp = a.b + (int64_t)wrow * gpr;
     const bool xvalid = xm < a.T;
+    // step k0's global data in registers: X (4 x 16 bytes), the row's 32 codes and their group's
+    // scale / bias. The next step's loads are issued before this step's MFMAs, so their latency
+    // hides behind the compute.
+    uint4 xr[4];
+    uint32_t wr[BITS];
+    float sr, br;
+    auto fetch = [&](int k0) {
+        const uint4* src = reinterpret_cast<const uint4*>(xrow + k0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) xr[v] = xvalid ? src[v] : uint4{0, 0, 0, 0};
+        load_codes32<BITS>(wptr + (int64_t)(k0 / 32) * (4 * BITS), wr);
+        const int g = (k0 + lh * 32) / a.gs;
+        sr = ld_scale<ST>(sp + g); br = ld_scale<ST>(bp + g);
+    };
+    fetch(0);
     for (int k0 = 0; k0 < K; k0 += GB_K) {
         // X tile
         {
-            const uint4* src = reinterpret_cast<const uint4*>(xrow + k0);
             uint4* dst = reinterpret_cast<uint4*>(Xs + lr * GB_LD + lh * 32);
 #pragma unroll
-            for (int v = 0; v < 4; v++) dst[v] = xvalid ? src[v] : uint4{0, 0, 0, 0};
+            for (int v = 0; v < 4; v++) dst[v] = xr[v];
         }
         // W tile: 32 codes of row lr, dequantized in fp32, rounded to bf16
         {
-            uint32_t w[BITS];
-            load_codes32<BITS>(wptr + (int64_t)(k0 / 32) * (4 * BITS), w);
-            const int g = (k0 + lh * 32) / a.gs;
-            const float s = ld_scale<ST>(sp + g), b = ld_scale<ST>(bp + g);
             uint32_t packed[16];
 #pragma unroll
             for (int j = 0; j < 16; j++) {
-                const float v0 = (float)code_of<BITS>(w, 2 * j) * s + b;
-                const float v1 = (float)code_of<BITS>(w, 2 * j + 1) * s + b;
+                const float v0 = (float)code_of<BITS>(wr, 2 * j) * sr + br;
+                const float v1 = (float)code_of<BITS>(wr, 2 * j + 1) * sr + br;
                 packed[j] = (uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16);
             }
             uint4* dst = reinterpret_cast<uint4*>(Ws + lr * GB_LD + lh * 32);
@@ -106,6 +117,7 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QGemmDev a) {
             for (int v = 0; v < 4; v++) dst[v] = uint4{packed[4 * v], packed[4 * v + 1], packed[4 * v + 2], packed[4 * v + 3]};
         }
         __syncthreads();
+        if (k0 + GB_K < K) fetch(k0 + GB_K);
 #pragma unroll
         for (int kk = 0; kk < 2; kk++) {
             bf16x8_t af[4], bf[4];
