@@ -20,6 +20,7 @@ int* g_pos = nullptr;          // device scalar for kernel-level calls
 int* g_pt = nullptr;           // identity page table
 int g_pt_pages = 0;
 float* g_part = nullptr; size_t g_part_floats = 0;
+float* g_qsplit = nullptr; size_t g_qsplit_floats = 0;   // the GEMM's split-over-K scratch (counters kept at zero)
 float* g_split = nullptr; size_t g_split_floats = 0;   // the long-input split matvec's scratch
 uint16_t* g_xbf = nullptr; size_t g_xbf_elems = 0;
 float* g_xsc = nullptr; size_t g_xsc_elems = 0;
@@ -230,8 +231,13 @@ int mlxr_k_qgemm(const mlxr_qmat* mat, int K, int bits, int gs, int st, int T, c
     if (T < 1 || !x || !y || x_stride < K || y_stride < mat->O || x_stride % 4) return set_error(MLXR_E_INVALID_ARG, "T / strides");
     if (int rc = ensure_buf(g_xbf, g_xbf_elems, (size_t)T * K)) return rc;
     if (int rc = ensure_buf(g_xsc, g_xsc_elems, (size_t)T)) return rc;
+    if (!g_qsplit) {
+        if (int rc = ensure_buf(g_qsplit, g_qsplit_floats, QGEMM_SPLIT_FLOATS)) return rc;
+        CK(hipMemset(g_qsplit, 0, QGEMM_SPLIT_FLOATS * 4));
+    }
     QGemmArgs a; a.m = qmat(*mat); a.K = K; a.bits = bits; a.gs = gs; a.st = st; a.O = mat->O; a.T = T;
     a.x = x; a.x_stride = x_stride; a.y = y; a.y_stride = y_stride; a.xbf = g_xbf; a.xsc = g_xsc;
+    a.split = g_qsplit; a.split_floats = g_qsplit_floats;
     return done(launch_qgemm(a, g_stream));
 }
 

@@ -35,6 +35,7 @@ struct QGemmDev {
     const uint8_t* w; const uint16_t* s; const uint16_t* b; const uint16_t* bias;
     int K, gs, O, T, ys;
     const uint16_t* xbf; float* y;
+    float* split;             // split over K (gridDim.z slices): tile counters, then the slices' partial tiles
 };
 
 template <int BITS>
@@ -58,7 +59,10 @@ __device__ __forceinline__ uint32_t code_of(const uint32_t* w, int j) {
     return ((w[wi] >> off) | (w[wi + 1] << (32 - off))) & M;
 }
 
-template <int BITS, int ST>
+// K slices of the bf16 GEMM: 4 (of at least 32 steps) for inputs of 8192 or more, else 1.
+__host__ __device__ constexpr int qgemm_slices(int K) { return K / GB_K >= 128 ? 4 : 1; }
+
+template <int BITS, int ST, int SF>
 __global__ __launch_bounds__(256) void qgemm_kernel(QGemmDev a) {
     __shared__ __attribute__((aligned(16))) uint16_t Xs[GB_M * GB_LD];
     __shared__ __attribute__((aligned(16))) uint16_t Ws[GB_N * GB_LD];
@@ -81,6 +85,13 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QGemmDev a) {
     const uint16_t* sp = a.s + (int64_t)wrow * gpr;
     const uint16_t* bp = a.b + (int64_t)wrow * gpr;
     const bool xvalid = xm < a.T;
+    // K in SF fixed slices (whole GB_K steps, SF set by K alone), each accumulated from zero and the
+    // slices added in order: the same arithmetic whether one workgroup walks them in turn
+    // (gridDim.z == 1) or SF workgroups take one each (gridDim.z == SF, the last adding the
+    // partials), so a token's result never depends on T (nor on the launch's split)
+    const int nsteps = K / GB_K, z = blockIdx.z, S = gridDim.z;
+    const int sl0 = z * SF / S, sl1 = (z + 1) * SF / S;
+    f32x4_t tot[4][4];
     // step k0's global data in registers: X (4 x 16 bytes), the row's 32 codes and their group's
     // scale / bias. The next step's loads are issued before this step's MFMAs, so their latency
     // hides behind the compute.
@@ -95,44 +106,96 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QGemmDev a) {
         const int g = (k0 + lh * 32) / a.gs;
         sr = ld_scale<ST>(sp + g); br = ld_scale<ST>(bp + g);
     };
-    fetch(0);
-    for (int k0 = 0; k0 < K; k0 += GB_K) {
-        // X tile
-        {
-            uint4* dst = reinterpret_cast<uint4*>(Xs + lr * GB_LD + lh * 32);
+    for (int sl = sl0; sl < sl1; sl++) {
+        const int kb = nsteps * sl / SF * GB_K, ke = nsteps * (sl + 1) / SF * GB_K;
 #pragma unroll
-            for (int v = 0; v < 4; v++) dst[v] = xr[v];
-        }
-        // W tile: 32 codes of row lr, dequantized in fp32, rounded to bf16
-        {
-            uint32_t packed[16];
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float v0 = (float)code_of<BITS>(wr, 2 * j) * sr + br;
-                const float v1 = (float)code_of<BITS>(wr, 2 * j + 1) * sr + br;
-                packed[j] = (uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16);
+            for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        fetch(kb);
+        for (int k0 = kb; k0 < ke; k0 += GB_K) {
+            // X tile
+            {
+                uint4* dst = reinterpret_cast<uint4*>(Xs + lr * GB_LD + lh * 32);
+#pragma unroll
+                for (int v = 0; v < 4; v++) dst[v] = xr[v];
             }
-            uint4* dst = reinterpret_cast<uint4*>(Ws + lr * GB_LD + lh * 32);
+            // W tile: 32 codes of row lr, dequantized in fp32, rounded to bf16
+            {
+                uint32_t packed[16];
 #pragma unroll
-            for (int v = 0; v < 4; v++) dst[v] = uint4{packed[4 * v], packed[4 * v + 1], packed[4 * v + 2], packed[4 * v + 3]};
+                for (int j = 0; j < 16; j++) {
+                    const float v0 = (float)code_of<BITS>(wr, 2 * j) * sr + br;
+                    const float v1 = (float)code_of<BITS>(wr, 2 * j + 1) * sr + br;
+                    packed[j] = (uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16);
+                }
+                uint4* dst = reinterpret_cast<uint4*>(Ws + lr * GB_LD + lh * 32);
+#pragma unroll
+                for (int v = 0; v < 4; v++) dst[v] = uint4{packed[4 * v], packed[4 * v + 1], packed[4 * v + 2], packed[4 * v + 3]};
+            }
+            __syncthreads();
+            if (k0 + GB_K < ke) fetch(k0 + GB_K);
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                bf16x8_t af[4], bf[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    af[i] = *reinterpret_cast<const bf16x8_t*>(Xs + (wm * 64 + i * 16 + (lane & 15)) * GB_LD + kk * 32 + (lane >> 4) * 8);
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    bf[j] = *reinterpret_cast<const bf16x8_t*>(Ws + (wn * 64 + j * 16 + (lane & 15)) * GB_LD + kk * 32 + (lane >> 4) * 8);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+            __syncthreads();
         }
-        __syncthreads();
-        if (k0 + GB_K < K) fetch(k0 + GB_K);
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-            bf16x8_t af[4], bf[4];
+        if constexpr (SF > 1) {
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                af[i] = *reinterpret_cast<const bf16x8_t*>(Xs + (wm * 64 + i * 16 + (lane & 15)) * GB_LD + kk * 32 + (lane >> 4) * 8);
+#pragma unroll
+                for (int j = 0; j < 4; j++) tot[i][j] = sl == sl0 ? acc[i][j] : tot[i][j] + acc[i][j];
+        }
+    }
+    if constexpr (SF > 1) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = tot[i][j];
+    }
+    if (S > 1) {
+        // this slice's partial tile (coherent stores), then the tile's counter; the last slice adds
+        // the slices in order (deterministic) and writes the output
+        const int tile = blockIdx.y * gridDim.x + blockIdx.x, ntiles = gridDim.x * gridDim.y;
+        unsigned* cnt = reinterpret_cast<unsigned*>(a.split);
+        float* part = a.split + QGEMM_SPLIT_TILES;
+        auto pidx = [&](int zz, int i, int j, int r) {   // [slice][tile][16 KB: this thread's 64 values]
+            return (((size_t)zz * ntiles + tile) * 256 + tid) * 64 + (i * 4 + j) * 4 + r;
+        };
+#pragma unroll
+        for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                bf[j] = *reinterpret_cast<const bf16x8_t*>(Ws + (wn * 64 + j * 16 + (lane & 15)) * GB_LD + kk * 32 + (lane >> 4) * 8);
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
+                for (int r = 0; r < 4; r++) __hip_atomic_store(part + pidx(z, i, j, r), acc[i][j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        __shared__ int last;
+        if (tid == 0) last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+        __syncthreads();
+        if (!last) return;
+        if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float v = __hip_atomic_load(part + pidx(0, i, j, r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    for (int zz = 1; zz < S; zz++) v += __hip_atomic_load(part + pidx(zz, i, j, r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    acc[i][j][r] = v;
+                }
     }
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -456,11 +519,26 @@ hipError_t launch_qgemm(const QGemmArgs& a, hipStream_t s) {
     }
     const int64_t n = (int64_t)a.T * a.K;
     hipLaunchKernelGGL(to_bf16_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, a.x, a.x_stride, a.K, a.T, a.xbf);
-    QGemmDev d{a.m.w, a.m.s, a.m.b, a.m.bias, a.K, a.gs, a.O, a.T, a.y_stride, a.xbf, a.y};
+    QGemmDev d{a.m.w, a.m.s, a.m.b, a.m.bias, a.K, a.gs, a.O, a.T, a.y_stride, a.xbf, a.y, a.split};
     dim3 grid((a.O + GB_N - 1) / GB_N, (a.T + GB_M - 1) / GB_M);
+    {   // under one round of workgroups: the K slices on workgroups of their own (at most two
+        // workgroups per CU), when a scratch is given
+        static int cus = 0;
+        if (!cus) {
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+                return hipErrorInvalidDevice;
+        }
+        const int tiles = (int)(grid.x * grid.y), SF = qgemm_slices(a.K);
+        if (SF > 1 && tiles * SF <= 2 * cus && (size_t)tiles * SF <= QGEMM_SPLIT_TILES && a.split && a.split_floats >= QGEMM_SPLIT_FLOATS)
+            grid.z = SF;
+    }
+    const bool sf4 = qgemm_slices(a.K) == 4;
 #define GEMM_CASE(B) case B: \
-    if (a.st == 0) hipLaunchKernelGGL((qgemm_kernel<B, 0>), grid, dim3(256), 0, s, d); \
-    else hipLaunchKernelGGL((qgemm_kernel<B, 1>), grid, dim3(256), 0, s, d); \
+    if (sf4) { if (a.st == 0) hipLaunchKernelGGL((qgemm_kernel<B, 0, 4>), grid, dim3(256), 0, s, d); \
+               else hipLaunchKernelGGL((qgemm_kernel<B, 1, 4>), grid, dim3(256), 0, s, d); } \
+    else { if (a.st == 0) hipLaunchKernelGGL((qgemm_kernel<B, 0, 1>), grid, dim3(256), 0, s, d); \
+           else hipLaunchKernelGGL((qgemm_kernel<B, 1, 1>), grid, dim3(256), 0, s, d); } \
     return hipGetLastError();
     switch (a.bits) { GEMM_CASE(2) GEMM_CASE(3) GEMM_CASE(4) GEMM_CASE(5) GEMM_CASE(6) GEMM_CASE(8) }
 #undef GEMM_CASE

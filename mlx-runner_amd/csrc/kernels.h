@@ -50,7 +50,14 @@ struct QGemmArgs {
     uint16_t* xbf = nullptr;              // scratch: T*K 16-bit (x rounded once per call)
     float* xsc = nullptr;                 // scratch: T floats (per-row power-of-two scales); null = bf16 path
     bool x_ready = false;                 // xbf / xsc already hold this x (same K): skip the pre-pass
+    // optional scratch for the other widths' GEMM split over K when its grid is under one round:
+    // QGEMM_SPLIT_FLOATS floats, zero before first use (its tile counters return to zero)
+    float* split = nullptr; size_t split_floats = 0;
 };
+// tile counters for up to 512 tiles, then at most 512 partial 128 x 128 tiles (slices x tiles stay
+// within two workgroups per CU of a 256-CU device)
+constexpr size_t QGEMM_SPLIT_TILES = 512;
+constexpr size_t QGEMM_SPLIT_FLOATS = QGEMM_SPLIT_TILES + QGEMM_SPLIT_TILES * 128 * 128;
 hipError_t launch_qgemm(const QGemmArgs& a, hipStream_t s);
 // The 4-bit GEMM pre-pass: row t of x scaled by the power of two that puts max|x| in [2^13, 2^14),
 // rounded to f16 (each 8-group stored as 0,4,1,5,2,6,3,7), inv[t] = the inverse scale.

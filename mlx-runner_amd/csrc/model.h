@@ -63,6 +63,7 @@ struct Model {
     float *h = nullptr, *xn = nullptr, *tmp = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *mlp = nullptr;
     float* dmv_split = nullptr;      // [2][H] input-slice partials of the kernel-per-op down matvec (long inputs)
     float* logits = nullptr; float* part = nullptr; float* bmax = nullptr; int* barg = nullptr;
+    float* qsplit = nullptr;            // the other widths' prefill GEMM split over K (QGEMM_SPLIT_FLOATS, counters at zero)
     uint16_t* xbf = nullptr; float* xsc = nullptr;
     int* diag = nullptr;
     // sparse

@@ -323,6 +323,23 @@ def test_qgemm_batch_invariant(gpu):
         assert np.array_equal(qgemm(gpu, fx, x[:T]).view(np.uint32), full[:T].view(np.uint32)), T
 
 
+@pytest.mark.parametrize("bits,gs", [(3, 32), (8, 64)])
+def test_qgemm_split_k_batch_invariant(gpu, bits, gs):
+    """The other widths' GEMM over a long input (128 K steps: four fixed K slices added in order):
+    a launch of few tiles runs the slices on workgroups of their own (9 tokens x 40 row tiles), a
+    launch of many does not (512 tokens x 40), and a token's result is bit-identical either way
+    (prefillTilesAgreeBitwise, KernelTests.swift:168-184), and matches the oracle in the GEMM's
+    precision; repeated, so the split's tile counters are back at zero."""
+    O, K = 5120, 8192
+    fx = QuantFixture(O, K, bits, gs, seed=bits, fast=True)
+    x = np.random.default_rng(bits).uniform(-1, 1, (512, K)).astype(np.float32)
+    full = qgemm(gpu, fx, x)
+    for _ in range(2):
+        few = qgemm(gpu, fx, x[:9])
+        assert np.array_equal(few.view(np.uint32), full[:9].view(np.uint32))
+    assert max_rel_err(few, fx.oracle(oracle).matmul_prefill(x[:9])) < TOL
+
+
 def test_qembed(gpu):
     """quantizedEmbeddingLookup (KernelTests.swift:287-296), tol 1e-5."""
     K, V = 128, 16
