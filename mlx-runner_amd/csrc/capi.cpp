@@ -309,6 +309,23 @@ int mlxr_k_qmv_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode
     return done(e);
 }
 
+int mlxr_k_qmm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int gated, int T, const float* x, int x_stride,
+                     float* y, int y_stride) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (int rc = ensure_stream()) return rc;
+    if (T < 1 || T > 8 || !x || !y || x_stride < K || x_stride % 4) return set_error(MLXR_E_INVALID_ARG, "T 1..8 / pointers / strides");
+    MvPhaseDesc d; uint8_t* code;
+    if (int rc = tiles_pack(parts, nparts, K, gs, gated, d, code)) return rc;
+    const int cols = gated ? d.o1 : d.rows;
+    if (y_stride < cols) { hipFree(code); return set_error(MLXR_E_INVALID_ARG, "y_stride"); }
+    hipError_t e = launch_dpack_mm(d, x, x_stride, y, y_stride, T, g_stream);
+    const hipError_t e2 = hipStreamSynchronize(g_stream);
+    hipFree(code);
+    if (e == hipSuccess) e = e2;
+    if (e == hipErrorInvalidValue) return set_error(MLXR_E_UNSUPPORTED, "small-batch matvec over repacked tiles: shape");
+    return done(e);
+}
+
 int mlxr_k_qembed(const mlxr_qmat* mat, int K, int bits, int gs, int st, const int32_t* ids, int T, float* out) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (int rc = ensure_stream()) return rc;

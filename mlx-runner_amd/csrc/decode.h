@@ -40,6 +40,9 @@ constexpr int DMV_MAX_SLICES = 8;
 inline size_t dpack_mv_split_floats(int rows) { return (size_t)DMV_MAX_SLICES * rows + (size_t)(rows + 15) / 16 + 64; }
 hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* norm_w, float eps, float* y, int mode,
                            hipStream_t s, float* split = nullptr);
+// The same matrices for T = 1..8 tokens (x[t] at x + t * xs, y[t] at y + t * ys): y = W x (+ bias),
+// or for a gated phase y[o1] = SiLU(gate) * up.
+hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, float* y, int ys, int T, hipStream_t s);
 
 struct LayerDev {
     MvPhaseDesc qkv, o, gu, down;

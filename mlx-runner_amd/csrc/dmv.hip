@@ -210,6 +210,148 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc 
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Small batch over the repacked tiles: Y[t] = W x[t] (+ bias), or SiLU(gate) * up, for up to 8
+// tokens at once (the speculative verify batch). The tokens ride in the MFMA B columns (token c & 7,
+// its hi part in column c, lo part in column c + 8), so the A operands (codes) are built once for
+// every token, and each quantization group of a scale group accumulates in its own registers and is
+// scaled after its MFMAs (the decode matvec separates groups by column instead). x of each token is
+// packed as the decode matvec packs it (its own power-of-two scale, f16 hi + lo); `nt` tokens per
+// launch, as many as fit in LDS.
+constexpr int DMM_TOK = 8;
+
+template <int FB>
+__device__ __forceinline__ void mvt_run(const MvPhase p, const float* xh, int img, const float* gsum, int gstride, int nt,
+                                        int wg, int nwg, int wave, int lane, Ring<FB>& ring, float* part) {
+    constexpr int GSH = FB == 4 ? 5 : 6, CPG = 1 << (GSH - 5);   // chunks of 32 per quantization group
+    const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, wave);
+    const int nfb = g.f1 - g.f0;
+    if (nfb <= 0) return;
+    const int gpr = p.K >> GSH;
+    const gptr8 base = mv_base<FB>(p, g, lane);
+    const int col = lane & 15, tok = col & 7, kq = lane >> 4;
+    // B operand: the token's image (image 0 for the unused columns: read, never written), hi or lo
+    // slots, slot kq of each chunk
+    const float* xb = xh + (tok < nt ? tok : 0) * img + kq * 4 + (col >= 8 ? XH_LO : 0);
+    const float* gs_t = gsum + (tok < nt ? tok : 0) * gstride;
+    f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f};
+    int tile = g.f0 / g.NF, f = g.f0 - tile * g.NF;
+    for (int i = 0; i < nfb; i++) {
+        const bool more = i + 1 < nfb;
+        const gptr8 nxt = base + (int64_t)(i + 1) * ((FB + 1) * 1024);
+        const uint4 sbr = ring.u[0];
+        if (more) ring.u[0] = ld_stream16(nxt);
+        f32x4_t acc[16];
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc[q] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < FB; k++) {
+            const uint4 unit = ring.u[k + 1];
+            const uint32_t wd[4] = {unit.x, unit.y, unit.z, unit.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int chunk = (f * FB + k) * 4 + j;
+                const f16x8_t bv = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(xb + chunk * XH_STRIDE));
+                const int gl = (4 * k + j) / CPG;
+                acc[gl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_operand(wd[j]), bv, acc[gl], 0, 0, 0);
+            }
+            if (more) ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
+        }
+        // each group: hi + lo columns, then scale * D + bias * Xs with the group's word for this
+        // lane's rows (held by the scale block's lane of column gl in the same row quarter)
+        const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
+#pragma unroll
+        for (int gl = 0; gl < 16; gl++) {
+            const int gi = 16 * f + gl;
+            const bool real = gi < gpr;
+            const float xs = gs_t[real ? gi : 0];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float v = acc[gl][r] + __shfl_xor(acc[gl][r], 8, 64);
+                const uint32_t w = __shfl(sv[r], (lane & 0x30) | gl, 64);
+                const float sc = __uint_as_float(w << 16) * 16777216.0f, bb = __uint_as_float(w & 0xffff0000u);
+                run[r] += real ? sc * v + bb * xs : 0.0f;
+            }
+        }
+        if (f == g.NF - 1 || i == nfb - 1) {     // tile done (or the wave's range): its rows to LDS
+            if (col < DMM_TOK) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) part[((tile * MK_WAVES + wave) * 16 + 4 * kq + r) * DMM_TOK + col] = run[r];
+            }
+            run = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (++f == g.NF) { f = 0; tile++; }
+    }
+}
+
+// Tokens t0 .. t0 + nt - 1 of x (rows xs floats apart) -> y (rows ys floats apart).
+template <int FB>
+__global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MvPhaseDesc p, const float* __restrict__ x, int xs, float* __restrict__ y,
+                                                              int ys, int t0, int nt, int tpw) {
+    constexpr int GSH = FB == 4 ? 5 : 6;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int K = p.K, wg = blockIdx.x, nwg = gridDim.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int img = K, gstride = ((K >> GSH) + 3) & ~3;
+    float* xh = lds;                                        // nt images of K floats (hi + lo halves)
+    float* gsum = xh + (size_t)nt * img;                    // nt x gstride group sums
+    float* zero = gsum + (size_t)nt * gstride;              // MV_ZERO (pack_x16_from clears it)
+    float* part = zero + MV_ZERO;                           // [tpw][waves][16][DMM_TOK]
+    float* red = part + (size_t)tpw * MK_WAVES * 16 * DMM_TOK;   // 16 + DMM_TOK floats
+    Ring<FB> ring;
+    mv_prefetch<FB>(p, wg, nwg, wave, lane, ring);
+    // the finish sums every wave's slot of a tile, and a wave whose range misses the tile writes none
+    for (int i = threadIdx.x; i < tpw * MK_WAVES * 16 * DMM_TOK; i += MK_THREADS) part[i] = 0.0f;
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    typedef const __attribute__((address_space(1))) f4v* gf4p;
+    auto gf4 = [](const float* q) { const f4v v = *(gf4p)q; return float4{v.x, v.y, v.z, v.w}; };
+    for (int tk = 0; tk < nt; tk++) {
+        const float* xt = x + (int64_t)(t0 + tk) * xs;
+        float mx = 0.0f;
+        for (int i = threadIdx.x * 4; i < K; i += MK_THREADS * 4) {
+            const float4 v = gf4(xt + i);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+        mx = wave_max(mx);
+        if (lane == 0) red[wave] = mx;
+        lds_barrier();
+        float gmax = 0.0f;
+        for (int w = 0; w < MK_WAVES; w++) gmax = fmaxf(gmax, red[w]);
+        MvLds L;
+        L.xf = nullptr; L.hown = nullptr; L.part = nullptr;
+        L.xh = xh + (size_t)tk * img; L.gsum = gsum + (size_t)tk * gstride; L.zero16 = zero;
+        auto ld = [xt, gf4](int t, float4& lo, float4& hi) { lo = gf4(xt + 8 * t); hi = gf4(xt + 8 * t + 4); };
+        const float us = pack_x16_from(ld, K, gmax, L, GSH);   // ends with a barrier (red reusable)
+        if (threadIdx.x == 0) red[16 + tk] = us;
+    }
+    lds_barrier();
+    mvt_run<FB>(p, xh, img, gsum, gstride, nt, wg, nwg, wave, lane, ring, part);
+    lds_barrier();
+    const MvGeom<FB> gg = mv_geom<FB>(p, wg, nwg, 0);
+    for (int i = threadIdx.x; i < gg.nt * 16 * nt; i += MK_THREADS) {
+        const int tk = i % nt, rr = i / nt, tl = rr >> 4, row = rr & 15;
+        float v = 0.0f;
+        for (int w = 0; w < MK_WAVES; w++) v += part[((tl * MK_WAVES + w) * 16 + row) * DMM_TOK + tk];
+        v *= red[16 + tk];
+        float* yt = y + (int64_t)(t0 + tk) * ys;
+        if (p.gated) {
+            // tile rows 0-7: gate of outputs 8 t + row, rows 8-15 the matching up values
+            if (row >= 8) continue;
+            const int o = 8 * (gg.t0 + tl) + row;
+            if (o >= p.o1) continue;
+            float u = 0.0f;
+            for (int w = 0; w < MK_WAVES; w++) u += part[((tl * MK_WAVES + w) * 16 + row + 8) * DMM_TOK + tk];
+            u *= red[16 + tk];
+            const float gv = v + (p.bias[0] ? bf16_to_f32(p.bias[0][o]) : 0.0f);
+            const float uv = u + (p.bias[1] ? bf16_to_f32(p.bias[1][o]) : 0.0f);
+            yt[o] = (gv / (1.0f + expf(-gv))) * uv;
+        } else {
+            const int r = 16 * (gg.t0 + tl) + row;
+            if (r < p.rows) yt[r] = v + row_bias(p, r);
+        }
+    }
+}
+
 template <int FB, int MODE>
 static hipError_t dmv_launch(const MvPhaseDesc& p, const float* x, const float* nw, float eps, float* y, int nwg, int tpw,
                              size_t lds, hipStream_t s) {
@@ -287,6 +429,53 @@ hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* no
         default: return fb4 ? dmv_launch<4, OUT_GATED>(p, x, norm_w, eps, y, nwg, tpw, lds, s)
                             : dmv_launch<8, OUT_GATED>(p, x, norm_w, eps, y, nwg, tpw, lds, s);
     }
+}
+
+hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, float* y, int ys, int T, hipStream_t s) {
+    if (!dpack_mv_supported(p) || T < 1 || T > DMM_TOK) return hipErrorInvalidValue;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return hipErrorInvalidDevice;
+    }
+    static bool attr = false;
+    if (!attr) {
+        for (const void* f : {(const void*)dpack_mm_kernel<4>, (const void*)dpack_mm_kernel<8>})
+            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, DMV_MAX_LDS) != hipSuccess) return hipErrorInvalidValue;
+        attr = true;
+    }
+    // a single-part, ungated phase of many tiles (the lm_head) runs in row chunks of at most
+    // DMM_TPW tiles per workgroup: every wave's partial rows of a tile sit in LDS
+    constexpr int DMM_TPW = 4;
+    const int FB = p.gs >> 3, NF = ((p.K >> 7) + FB - 1) / FB;
+    const size_t tile_bytes = (size_t)NF * (FB + 1) * 1024;
+    const int chunk = !p.gated && p.o2 == 0 ? DMM_TPW * cus : p.tiles;
+    for (int c0 = 0; c0 < p.tiles; c0 += chunk) {
+        MvPhaseDesc q = p;
+        q.tiles = std::min(chunk, p.tiles - c0);
+        if (c0 > 0) {
+            q.code = p.code + (size_t)c0 * tile_bytes;
+            q.rows = p.rows - 16 * c0; q.o1 = q.rows;
+            if (p.bias[0]) q.bias[0] = p.bias[0] + 16 * c0;
+        }
+        float* yc = y + (c0 > 0 ? 16 * c0 : 0);
+        const int nwg = std::min(q.tiles, cus);
+        const int tpw = (q.tiles + nwg - 1) / nwg;
+        if (tpw > MK_TPW) return hipErrorInvalidValue;
+        const int gstride = ((q.K / q.gs) + 3) & ~3;
+        const size_t fixed = sizeof(float) * ((size_t)MV_ZERO + (size_t)tpw * MK_WAVES * 16 * DMM_TOK + 16 + DMM_TOK);
+        const size_t per_tok = sizeof(float) * ((size_t)q.K + gstride);
+        if (fixed + per_tok > DMV_MAX_LDS) return hipErrorInvalidValue;
+        const int tp = (int)std::min<size_t>(DMM_TOK, (DMV_MAX_LDS - fixed) / per_tok);
+        for (int t0 = 0; t0 < T; t0 += tp) {   // tokens per launch: as many as fit in LDS
+            const int nt = std::min(tp, T - t0);
+            const size_t lds = fixed + per_tok * nt;
+            if (q.gs == 32) hipLaunchKernelGGL(dpack_mm_kernel<4>, dim3(nwg), dim3(MK_THREADS), lds, s, q, x, xs, yc, ys, t0, nt, tpw);
+            else hipLaunchKernelGGL(dpack_mm_kernel<8>, dim3(nwg), dim3(MK_THREADS), lds, s, q, x, xs, yc, ys, t0, nt, tpw);
+        }
+    }
+    return hipGetLastError();
 }
 
 }  // namespace mlxr

@@ -742,8 +742,10 @@ int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
     hipStream_t s = m->stream;
     const int H = c.H, I = c.I;
     // prefill chunks on the repacked tiles when the model has them (fused q|k|v and gate|up, SiLU
-    // in the gate|up epilogue); verify batches (T <= 8) keep the small-batch kernels
+    // in the gate|up epilogue); verify batches (T <= 8) run the tiles' small-batch matvec (tokens in
+    // the matrix cores' columns), else the MLX-layout small-batch kernels
     const bool tiles = T > 8 && (int)m->tile_layers.size() == c.L;
+    const bool small_tiles = T <= 8 && (int)m->tile_layers.size() == c.L && m->decode_mode != 2;
     HIPCHECK(launch_qembed(m->embed.m, H, m->embed.bits, m->embed.gs, m->embed.st, m->hist, m->dpos, T, m->h, s));
     if (tiles) HIPCHECK(launch_rms_norm_f16(m->h, m->layers[0].in_norm, H, T, H, c.eps, m->xbf, m->xsc, s));
     else HIPCHECK(launch_rms_norm(m->h, m->xn, m->layers[0].in_norm, H, T, H, c.eps, s));
@@ -751,8 +753,10 @@ int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
         Layer& ly = m->layers[li];
         const Lin qkvp[3] = {ly.q, ly.k, ly.v};
         const LayerDev* tl = tiles ? &m->tile_layers[li] : nullptr;
-        if (int rc = tl ? project_tiles(m, tl->qkv, nullptr, H, m->qkv, m->qkv_cols, T)
-                        : project(m, qkvp, 3, m->xn, H, m->qkv, m->qkv_cols, T)) return rc;
+        const LayerDev* st = small_tiles ? &m->tile_layers[li] : nullptr;
+        if (st) HIPCHECK(launch_dpack_mm(st->qkv, m->xn, H, m->qkv, m->qkv_cols, T, s));
+        else if (int rc = tl ? project_tiles(m, tl->qkv, nullptr, H, m->qkv, m->qkv_cols, T)
+                             : project(m, qkvp, 3, m->xn, H, m->qkv, m->qkv_cols, T)) return rc;
         QkvPostArgs pa; pa.qkv = m->qkv; pa.row_stride = m->qkv_cols; pa.inv_freq = m->inv_freq; pa.kc = ly.kc; pa.vc = ly.vc;
         pa.pt = m->page_table; pa.qn = ly.q_norm; pa.kn = ly.k_norm; pa.D = c.D; pa.nH = c.nH; pa.nKV = c.nKV;
         pa.rot_dim = c.rot_dim; pa.traditional = c.traditional; pa.T = T; pa.dpos = m->dpos; pa.eps = c.eps;
@@ -770,26 +774,34 @@ int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
             aa.nsplit = m->nsplit_dec; aa.dpos = m->dpos; aa.scale = scale;
             HIPCHECK(launch_attn_decode(aa, s));
         }
-        if (int rc = tl ? project_tiles(m, tl->o, m->attn, c.nH * c.D, m->tmp, H, T)
-                        : project(m, &ly.o, 1, m->attn, c.nH * c.D, m->tmp, H, T)) return rc;
+        if (st) HIPCHECK(launch_dpack_mm(st->o, m->attn, c.nH * c.D, m->tmp, H, T, s));
+        else if (int rc = tl ? project_tiles(m, tl->o, m->attn, c.nH * c.D, m->tmp, H, T)
+                             : project(m, &ly.o, 1, m->attn, c.nH * c.D, m->tmp, H, T)) return rc;
         if (tl) {
             HIPCHECK(launch_add_rms_norm_f16(m->h, m->tmp, ly.post_norm, H, T, c.eps, m->xbf, m->xsc, s));
             if (int rc = project_tiles(m, tl->gu, nullptr, H, m->mlp, I, T)) return rc;
         } else {
             HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, ly.post_norm, H, T, c.eps, s));
-            const Lin gup[2] = {ly.gate, ly.up};
-            if (int rc = project(m, gup, 2, m->xn, H, m->gu, 2 * I, T)) return rc;
-            HIPCHECK(launch_silu_mul(m->gu, m->mlp, I, T, s));
+            if (st) {
+                HIPCHECK(launch_dpack_mm(st->gu, m->xn, H, m->mlp, I, T, s));   // SiLU(gate) * up
+            } else {
+                const Lin gup[2] = {ly.gate, ly.up};
+                if (int rc = project(m, gup, 2, m->xn, H, m->gu, 2 * I, T)) return rc;
+                HIPCHECK(launch_silu_mul(m->gu, m->mlp, I, T, s));
+            }
         }
-        if (int rc = tl ? project_tiles(m, tl->down, m->mlp, I, m->tmp, H, T)
-                        : project(m, &ly.down, 1, m->mlp, I, m->tmp, H, T)) return rc;
+        if (st) HIPCHECK(launch_dpack_mm(st->down, m->mlp, I, m->tmp, H, T, s));
+        else if (int rc = tl ? project_tiles(m, tl->down, m->mlp, I, m->tmp, H, T)
+                             : project(m, &ly.down, 1, m->mlp, I, m->tmp, H, T)) return rc;
         const bool last = li + 1 == c.L;
         if (last && !want_logits) continue;
         if (tl && !last) HIPCHECK(launch_add_rms_norm_f16(m->h, m->tmp, m->layers[li + 1].in_norm, H, T, c.eps, m->xbf, m->xsc, s));
         else HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, last ? m->final_norm : m->layers[li + 1].in_norm, H, T, c.eps, s));
     }
     if (!want_logits) return MLXR_OK;
-    if (all_logits) {
+    if (all_logits && small_tiles && m->tile_head.code) {
+        HIPCHECK(launch_dpack_mm(m->tile_head, m->xn, H, m->logits, c.V, T, s));
+    } else if (all_logits) {
         for (int t = 0; t < T; t++)
             HIPCHECK(launch_qmv(qmv_args(&m->head, 1, m->xn + (size_t)t * H, nullptr, 0, m->logits + (size_t)t * c.V, EPI_STORE), s));
     } else {

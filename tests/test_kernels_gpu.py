@@ -228,6 +228,10 @@ def test_qmv_tiles_epilogues(gpu, gs):
         tiny = (h * 1e-20).astype(np.float32)   # scaled up by 2^e before rounding: no f16 underflow
         ref_tiny = np.concatenate([f.oracle(oracle).matmul_f64(tiny)[0] for f in fxs])
         assert max_rel_err(qmv_tiles(gpu, fxs, tiny) * 1e20, ref_tiny * 1e20) < TOL, K
+    # a single part of more tiles than four per workgroup (the lm_head: row chunks of its own)
+    f = QuantFixture(16 * 4 * 256 * 2 + 40, 256, 4, gs, seed=7, fast=True)
+    x = rng.normal(0, 1, (2, 256)).astype(np.float32)
+    assert max_rel_err(qmm_tiles(gpu, [f], x), f.oracle(oracle).matmul_f64(x)) < TOL
     K, I = 2048, 200
     g, u = (QuantFixture(I, K, 4, gs, seed=s, fast=True) for s in (5, 6))
     h = rng.normal(0, 1, K).astype(np.float32)
@@ -256,6 +260,46 @@ def test_qmv_tiles_input_slices_share_scratch(gpu):
         assert max_rel_err(qmv_tiles(gpu, [f], x), ref) < TOL, (K, O)
         y0 = rng.normal(0, 1, O).astype(np.float32)
         assert max_rel_err(qmv_tiles(gpu, [f], x, mode=1, y0=y0), y0 + ref) < TOL, (K, O)
+
+
+def qmm_tiles(mlxr, fxs, x, gated=False):
+    T, K = x.shape
+    qm = (mlxr.QMat * len(fxs))(*[f.device(mlxr) for f in fxs])
+    cols = fxs[0].O if gated else sum(f.O for f in fxs)
+    dx = mlxr.DeviceArray.from_numpy(np.ascontiguousarray(x))
+    dy = mlxr.DeviceArray.from_numpy(np.full((T, cols), np.nan, np.float32))
+    mlxr.check(mlxr.lib.mlxr_k_qmm_tiles(qm, len(fxs), K, fxs[0].gs, int(gated), T, dx.ptr, K, dy.ptr, cols))
+    mlxr.synchronize()
+    return dy.numpy()
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_qmm_tiles_small_batch(gpu, gs):
+    """The verify batch's projections over the repacked tiles (qmm / qmvx4, Kernels.swift:60-113,
+    518-622): T = 1..8 tokens in the matrix cores' B columns, every token against the oracle's fp64
+    product at the 1e-3 matvec gate: fused parts with bias and ragged rows, inputs from one scale
+    group to 12288 values (several launches of fewer tokens when x does not fit in LDS at once),
+    rows of very different magnitude, and the gated MLP form."""
+    rng = np.random.default_rng(gs)
+    for K, Os in ((128, (40,)), (1024, (264, 40, 88)), (4096, (72,)), (12288, (24,))):
+        fxs = [QuantFixture(O, K, 4, gs, seed=O + K, with_bias=len(Os) > 1, fast=True) for O in Os]
+        for T in (1, 3, 8):
+            x = rng.normal(0, 1, (T, K)).astype(np.float32) * (10.0 ** np.linspace(-3, 3, T)).astype(np.float32)[:, None]
+            ref = np.concatenate([f.oracle(oracle).matmul_f64(x) for f in fxs], axis=1)
+            got = qmm_tiles(gpu, fxs, x)
+            for t in range(T):
+                assert max_rel_err(got[t] / np.float32(10.0 ** np.linspace(-3, 3, T)[t]),
+                                   ref[t] / 10.0 ** np.linspace(-3, 3, T)[t]) < TOL, (K, T, t)
+    # a single part of more tiles than four per workgroup (the lm_head: row chunks of its own)
+    f = QuantFixture(16 * 4 * 256 * 2 + 40, 256, 4, gs, seed=7, fast=True)
+    x = rng.normal(0, 1, (2, 256)).astype(np.float32)
+    assert max_rel_err(qmm_tiles(gpu, [f], x), f.oracle(oracle).matmul_f64(x)) < TOL
+    K, I = 2048, 200
+    g, u = (QuantFixture(I, K, 4, gs, seed=s, fast=True) for s in (5, 6))
+    x = rng.normal(0, 1, (5, K)).astype(np.float32)
+    gr, ur = g.oracle(oracle).matmul_f64(x), u.oracle(oracle).matmul_f64(x)
+    gated = np.array([[oracle.lib.orc_silu_mul(float(a), float(b)) for a, b in zip(gr[t], ur[t])] for t in range(5)], np.float32)
+    assert max_rel_err(qmm_tiles(gpu, [g, u], x, gated=True), gated) < TOL
 
 
 def _decode_input(kind, K, rng):
