@@ -215,10 +215,12 @@ int mlxr_k_qgemm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int ga
 int mlxr_k_qmv_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode, const float* x, const float* norm_w,
                      float eps, float* y, int reps);
 /* The small-batch form over the same tiles (the verify batch's projections, `qmm` / `qmvx4`,
- * Kernels.swift:60-113, 518-622): T = 1..8 tokens, y[t] = W x[t] (+ bias), or gated (two parts of
- * equal O) y[t][o] = silu(A x_t)[o] * (B x_t)[o]. Same quantization limits as mlxr_k_qmv_tiles. */
-int mlxr_k_qmm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int gated, int T, const float* x, int x_stride,
-                     float* y, int y_stride);
+ * Kernels.swift:60-113, 518-622): T = 1..8 tokens (x[t] at x + t * x_stride, y[t] at
+ * y + t * y_stride), mode 0 y[t] = W x[t] (+ bias), 1 y[t] += W x[t] (+ bias), 2 (two parts of
+ * equal O) y[t][o] = silu(A x_t)[o] * (B x_t)[o]; norm_w (or NULL) first replaces each x[t] by
+ * RMSNorm(x[t]) * norm_w (eps). Same quantization limits as mlxr_k_qmv_tiles. */
+int mlxr_k_qmm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode, int T, const float* x, int x_stride,
+                     const float* norm_w, float eps, float* y, int y_stride);
 /* Quantized embedding rows (`qembed`, Kernels.swift:1002-1023): ids device int32 [T]. */
 int mlxr_k_qembed(const mlxr_qmat* mat, int K, int bits, int gs, int st, const int32_t* ids, int T, float* out);
 /* RMSNorm rows (`rms_norm`, Kernels.swift:1037-1070), fp32 weights; add_rms_norm with r != NULL. */

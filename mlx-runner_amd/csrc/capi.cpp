@@ -309,16 +309,23 @@ int mlxr_k_qmv_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode
     return done(e);
 }
 
-int mlxr_k_qmm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int gated, int T, const float* x, int x_stride,
-                     float* y, int y_stride) {
+int mlxr_k_qmm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode, int T, const float* x, int x_stride,
+                     const float* norm_w, float eps, float* y, int y_stride) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (int rc = ensure_stream()) return rc;
-    if (T < 1 || T > 8 || !x || !y || x_stride < K || x_stride % 4) return set_error(MLXR_E_INVALID_ARG, "T 1..8 / pointers / strides");
+    if (T < 1 || T > 8 || mode < 0 || mode > 2 || !x || !y || x_stride < K || x_stride % 4)
+        return set_error(MLXR_E_INVALID_ARG, "T 1..8 / mode / pointers / strides");
     MvPhaseDesc d; uint8_t* code;
-    if (int rc = tiles_pack(parts, nparts, K, gs, gated, d, code)) return rc;
-    const int cols = gated ? d.o1 : d.rows;
+    if (int rc = tiles_pack(parts, nparts, K, gs, mode == 2, d, code)) return rc;
+    const int cols = mode == 2 ? d.o1 : d.rows;
     if (y_stride < cols) { hipFree(code); return set_error(MLXR_E_INVALID_ARG, "y_stride"); }
-    hipError_t e = launch_dpack_mm(d, x, x_stride, y, y_stride, T, g_stream);
+    // the input-slice scratch, as the model passes it (tile counters start at zero and return to it)
+    const size_t sf = dpack_mm_split_floats(d);
+    if (sf > g_split_floats) {
+        if (int rc = ensure_buf(g_split, g_split_floats, sf)) { hipFree(code); return rc; }
+        CK(hipMemset(g_split, 0, sf * 4));
+    }
+    hipError_t e = launch_dpack_mm(d, x, x_stride, norm_w, eps, y, y_stride, mode == 1, T, g_split, g_split_floats, g_stream);
     const hipError_t e2 = hipStreamSynchronize(g_stream);
     hipFree(code);
     if (e == hipSuccess) e = e2;

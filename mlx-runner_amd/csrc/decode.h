@@ -41,8 +41,13 @@ inline size_t dpack_mv_split_floats(int rows) { return (size_t)DMV_MAX_SLICES * 
 hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* norm_w, float eps, float* y, int mode,
                            hipStream_t s, float* split = nullptr);
 // The same matrices for T = 1..8 tokens (x[t] at x + t * xs, y[t] at y + t * ys): y = W x (+ bias),
-// or for a gated phase y[o1] = SiLU(gate) * up.
-hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, float* y, int ys, int T, hipStream_t s);
+// y += W x (accumulate), or for a gated phase y[o1] = SiLU(gate) * up; x := RMSNorm(x) * norm_w
+// first when norm_w is given. Inputs too long for all T tokens' images in LDS run in input slices
+// and need `split`: dpack_mm_split_floats(p) floats, zeroed once before the first use (tile
+// counters that every launch leaves at zero); launches sharing it must not overlap.
+size_t dpack_mm_split_floats(const MvPhaseDesc& p);
+hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, const float* norm_w, float eps, float* y, int ys,
+                           bool accumulate, int T, float* split, size_t split_floats, hipStream_t s);
 
 struct LayerDev {
     MvPhaseDesc qkv, o, gu, down;

@@ -211,24 +211,43 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Small batch over the repacked tiles: Y[t] = W x[t] (+ bias), or SiLU(gate) * up, for up to 8
-// tokens at once (the speculative verify batch). The tokens ride in the MFMA B columns (token c & 7,
-// its hi part in column c, lo part in column c + 8), so the A operands (codes) are built once for
-// every token, and each quantization group of a scale group accumulates in its own registers and is
-// scaled after its MFMAs (the decode matvec separates groups by column instead). x of each token is
-// packed as the decode matvec packs it (its own power-of-two scale, f16 hi + lo); `nt` tokens per
-// launch, as many as fit in LDS.
+// Small batch over the repacked tiles: Y[t] = W x[t] (+ bias), Y[t] += W x[t], or SiLU(gate) * up,
+// for up to 8 tokens at once (the speculative verify batch), x optionally RMSNorm(x) * w first.
+// The tokens ride in the MFMA B columns (token c & 7, its hi part in column c, lo part in column
+// c + 8), so the A operands (codes) are built once for every token, and each quantization group of
+// a scale group accumulates in its own registers and is scaled after its MFMAs (the decode matvec
+// separates groups by column instead). x of each token is packed as the decode matvec packs it
+// (its own power-of-two scale, f16 hi + lo), every token's statistics in one pass over registers.
+// Inputs too long for every token's image in LDS run as S input slices (grid.y) of each tile, the
+// slices' partial rows summed in slice order by the tile's last workgroup (per-tile counters), so
+// the result does not depend on arrival order.
 constexpr int DMM_TOK = 8;
+constexpr int DMM_MAX_S = 8;                               // input slices (max)
+constexpr int DMM_XR = 2;                                  // 8-groups of x per thread and token (slices of <= 8192 values)
+constexpr int DMM_SLOTS = MK_WAVES * 2 * 16 * DMM_TOK;     // floats: each wave's first and last tile rows, when shared
+constexpr int DMM_RED = 2 * MK_WAVES * DMM_TOK + DMM_TOK;  // per-wave max |x w| and sum of squares per token; unscales
 
-template <int FB>
+struct MmArgs {
+    MvPhaseDesc p;                       // the whole phase (parts, bias, rows)
+    const float* x; int xs;              // token t's input at x + t * xs
+    const float* nw; float eps;          // optional RMSNorm weights
+    float* y; int ys; int accumulate;    // token t's output at y + t * ys
+    int t0, nt;                          // the launch's tokens
+    unsigned* cnt; float* part;          // S > 1: tile counters (zero between launches), partials [S][nt][tiles * 16]
+};
+
+// Streams the wave's scale groups. A tile the wave covers whole goes to emit(tile, rows) at once
+// (lane (c, q): token c & 7, rows 4q .. 4q + 3); the wave's first and last tile, when other waves
+// share them, leave their rows in slots[wave][0 / 1][row][token].
+template <int FB, bool TS, typename EMIT>
 __device__ __forceinline__ void mvt_run(const MvPhase p, const float* xh, int img, const float* gsum, int gstride, int nt,
-                                        int wg, int nwg, int wave, int lane, Ring<FB>& ring, float* part) {
+                                        int wg, int nwg, int wave, int lane, Ring<FB>& ring, float* slots, const EMIT& emit) {
     constexpr int GSH = FB == 4 ? 5 : 6, CPG = 1 << (GSH - 5);   // chunks of 32 per quantization group
     const MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, wave);
     const int nfb = g.f1 - g.f0;
     if (nfb <= 0) return;
     const int gpr = p.K >> GSH;
-    const gptr8 base = mv_base<FB>(p, g, lane);
+    const gptr8 base = mv_base<FB, TS>(p, g, lane);
     const int col = lane & 15, tok = col & 7, kq = lane >> 4;
     // B operand: the token's image (image 0 for the unused columns: read, never written), hi or lo
     // slots, slot kq of each chunk
@@ -236,9 +255,14 @@ __device__ __forceinline__ void mvt_run(const MvPhase p, const float* xh, int im
     const float* gs_t = gsum + (tok < nt ? tok : 0) * gstride;
     f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f};
     int tile = g.f0 / g.NF, f = g.f0 - tile * g.NF;
+    const int first = tile;
+    bool fresh = f == 0;                 // the wave holds the tile from its first scale group
+    gptr8 cur = base;
     for (int i = 0; i < nfb; i++) {
         const bool more = i + 1 < nfb;
-        const gptr8 nxt = base + (int64_t)(i + 1) * ((FB + 1) * 1024);
+        gptr8 nxt;
+        if constexpr (TS) nxt = cur = cur + (int64_t)(f + 1 == g.NF ? p.tstride - g.NF + 1 : 1) * ((FB + 1) * 1024);
+        else nxt = base + (int64_t)(i + 1) * ((FB + 1) * 1024);
         const uint4 sbr = ring.u[0];
         if (more) ring.u[0] = ld_stream16(nxt);
         f32x4_t acc[16];
@@ -273,83 +297,217 @@ __device__ __forceinline__ void mvt_run(const MvPhase p, const float* xh, int im
                 run[r] += real ? sc * v + bb * xs : 0.0f;
             }
         }
-        if (f == g.NF - 1 || i == nfb - 1) {     // tile done (or the wave's range): its rows to LDS
-            if (col < DMM_TOK) {
+        if (f == g.NF - 1 || i == nfb - 1) {     // tile done (or the wave's range)
+            if (fresh && f == g.NF - 1) {
+                emit(tile, run);
+            } else if (col < DMM_TOK) {
+                const int slot = tile == first ? 0 : 1;
 #pragma unroll
-                for (int r = 0; r < 4; r++) part[((tile * MK_WAVES + wave) * 16 + 4 * kq + r) * DMM_TOK + col] = run[r];
+                for (int r = 0; r < 4; r++) slots[((wave * 2 + slot) * 16 + 4 * kq + r) * DMM_TOK + col] = run[r];
             }
             run = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        if (++f == g.NF) { f = 0; tile++; }
+        if (++f == g.NF) { f = 0; tile++; fresh = true; }
     }
 }
 
-// Tokens t0 .. t0 + nt - 1 of x (rows xs floats apart) -> y (rows ys floats apart).
-template <int FB>
-__global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MvPhaseDesc p, const float* __restrict__ x, int xs, float* __restrict__ y,
-                                                              int ys, int t0, int nt, int tpw) {
+// grid (workgroups, S). Slice blockIdx.y of every tile: scale groups [NF y / S, NF (y + 1) / S).
+template <int FB, bool TS>
+__global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MmArgs a) {
     constexpr int GSH = FB == 4 ? 5 : 6;
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    const int K = p.K, wg = blockIdx.x, nwg = gridDim.x;
+    const MvPhaseDesc& p = a.p;
+    const int wg = blockIdx.x, nwg = gridDim.x, sl = blockIdx.y, S = gridDim.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int img = K, gstride = ((K >> GSH) + 3) & ~3;
-    float* xh = lds;                                        // nt images of K floats (hi + lo halves)
+    const int NF = ((p.K >> 7) + FB - 1) / FB;
+    const int fa = NF * sl / S, fb = NF * (sl + 1) / S;
+    const int k0 = fa * FB * 128, Ks = min(fb * FB * 128, p.K) - k0;
+    MvPhaseDesc q = p;
+    if constexpr (TS) { q.code = p.code + (size_t)fa * ((FB + 1) * 1024); q.K = Ks; q.tstride = NF; }
+    const int nt = a.nt, img = Ks, gstride = ((Ks >> GSH) + 3) & ~3;
+    float* xh = lds;                                        // nt images of Ks floats (hi + lo halves)
     float* gsum = xh + (size_t)nt * img;                    // nt x gstride group sums
-    float* zero = gsum + (size_t)nt * gstride;              // MV_ZERO (pack_x16_from clears it)
-    float* part = zero + MV_ZERO;                           // [tpw][waves][16][DMM_TOK]
-    float* red = part + (size_t)tpw * MK_WAVES * 16 * DMM_TOK;   // 16 + DMM_TOK floats
-    Ring<FB> ring;
-    mv_prefetch<FB>(p, wg, nwg, wave, lane, ring);
-    // the finish sums every wave's slot of a tile, and a wave whose range misses the tile writes none
-    for (int i = threadIdx.x; i < tpw * MK_WAVES * 16 * DMM_TOK; i += MK_THREADS) part[i] = 0.0f;
+    float* zero = gsum + (size_t)nt * gstride;              // MV_ZERO (the packing clears it)
+    float* slots = zero + MV_ZERO;                          // DMM_SLOTS
+    float* red = slots + DMM_SLOTS;                         // max [wave][tok], sum of squares [wave][tok], unscale [tok]
     typedef float f4v __attribute__((ext_vector_type(4)));
     typedef const __attribute__((address_space(1))) f4v* gf4p;
-    auto gf4 = [](const float* q) { const f4v v = *(gf4p)q; return float4{v.x, v.y, v.z, v.w}; };
-    for (int tk = 0; tk < nt; tk++) {
-        const float* xt = x + (int64_t)(t0 + tk) * xs;
-        float mx = 0.0f;
-        for (int i = threadIdx.x * 4; i < K; i += MK_THREADS * 4) {
-            const float4 v = gf4(xt + i);
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    auto gf4 = [](const float* v) { const f4v u = *(gf4p)v; return float4{u.x, u.y, u.z, u.w}; };
+    // every token's slice of x (8-groups t = tid + MK_THREADS i) and the norm weights into registers,
+    // then the weights' first scale group: the memory counter completes in order, so the statistics
+    // wait for x alone while the weights stream in behind
+    float4 xv[DMM_TOK][DMM_XR][2], wv[DMM_XR][2];
+#pragma unroll
+    for (int i = 0; i < DMM_XR; i++) {
+        const int t = threadIdx.x + i * MK_THREADS;
+        const bool in = 8 * t < Ks;
+        wv[i][0] = wv[i][1] = float4{1.0f, 1.0f, 1.0f, 1.0f};
+        if (a.nw && in) { wv[i][0] = gf4(a.nw + k0 + 8 * t); wv[i][1] = gf4(a.nw + k0 + 8 * t + 4); }
+#pragma unroll
+        for (int tk = 0; tk < DMM_TOK; tk++) {
+            xv[tk][i][0] = xv[tk][i][1] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (tk < nt && in) {
+                const float* xt = a.x + (int64_t)(a.t0 + tk) * a.xs + k0 + 8 * t;
+                xv[tk][i][0] = gf4(xt); xv[tk][i][1] = gf4(xt + 4);
+            }
         }
-        mx = wave_max(mx);
-        if (lane == 0) red[wave] = mx;
-        lds_barrier();
-        float gmax = 0.0f;
-        for (int w = 0; w < MK_WAVES; w++) gmax = fmaxf(gmax, red[w]);
-        MvLds L;
-        L.xf = nullptr; L.hown = nullptr; L.part = nullptr;
-        L.xh = xh + (size_t)tk * img; L.gsum = gsum + (size_t)tk * gstride; L.zero16 = zero;
-        auto ld = [xt, gf4](int t, float4& lo, float4& hi) { lo = gf4(xt + 8 * t); hi = gf4(xt + 8 * t + 4); };
-        const float us = pack_x16_from(ld, K, gmax, L, GSH);   // ends with a barrier (red reusable)
-        if (threadIdx.x == 0) red[16 + tk] = us;
+    }
+    Ring<FB> ring;
+    mv_prefetch<FB, TS>(q, wg, nwg, wave, lane, ring);
+#pragma unroll
+    for (int tk = 0; tk < DMM_TOK; tk++) {
+        if (tk >= nt) break;
+        float ss = 0.0f, mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DMM_XR; i++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const float4 v = xv[tk][i][c], w = wv[i][c];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                const float4 u = float4{v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w};
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+            }
+        if (a.nw && S > 1) {   // the norm's statistics cover the whole input, not the slice
+            ss = 0.0f;
+            const float* xt = a.x + (int64_t)(a.t0 + tk) * a.xs;
+            for (int i = threadIdx.x * 4; i < p.K; i += MK_THREADS * 4) {
+                const float4 v = gf4(xt + i);
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+        }
+        ss = wave_sum(ss); mx = wave_max(mx);
+        if (lane == 0) { red[wave * DMM_TOK + tk] = mx; red[(MK_WAVES + wave) * DMM_TOK + tk] = ss; }
     }
     lds_barrier();
-    mvt_run<FB>(p, xh, img, gsum, gstride, nt, wg, nwg, wave, lane, ring, part);
+    MvLds L;
+    L.xf = nullptr; L.hown = nullptr; L.part = nullptr; L.zero16 = zero;
+#pragma unroll
+    for (int tk = 0; tk < DMM_TOK; tk++) {
+        if (tk >= nt) break;
+        float tot = 0.0f, gmax = 0.0f;
+        for (int w = 0; w < MK_WAVES; w++) { tot += red[(MK_WAVES + w) * DMM_TOK + tk]; gmax = fmaxf(gmax, red[w * DMM_TOK + tk]); }
+        const float inv = a.nw ? 1.0f / sqrtf(tot / (float)p.K + a.eps) : 1.0f;
+        if (a.nw) {
+#pragma unroll
+            for (int i = 0; i < DMM_XR; i++)
+#pragma unroll
+                for (int c = 0; c < 2; c++) {
+                    float4& v = xv[tk][i][c];
+                    const float4 w = wv[i][c];
+                    v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
+                }
+        }
+        L.xh = xh + (size_t)tk * img; L.gsum = gsum + (size_t)tk * gstride;
+        // the packing visits t = tid + MK_THREADS i in order of i
+        auto ld = [&](int t, float4& lo, float4& hi) {
+            const bool second = DMM_XR > 1 && t >= MK_THREADS;
+            lo = second ? xv[tk][DMM_XR - 1][0] : xv[tk][0][0];
+            hi = second ? xv[tk][DMM_XR - 1][1] : xv[tk][0][1];
+        };
+        const float us = pack_x16_from<decltype(ld), false>(ld, Ks, gmax * inv, L, GSH);
+        if (threadIdx.x == 0) red[2 * MK_WAVES * DMM_TOK + tk] = us;
+    }
     lds_barrier();
-    const MvGeom<FB> gg = mv_geom<FB>(p, wg, nwg, 0);
-    for (int i = threadIdx.x; i < gg.nt * 16 * nt; i += MK_THREADS) {
+    const float* unscale = red + 2 * MK_WAVES * DMM_TOK;
+    const MvGeom<FB> g0 = mv_geom<FB>(q, wg, nwg, 0);
+    const int T0 = g0.t0, R = p.tiles * 16;
+    const bool gated = p.gated != 0, direct = S == 1;
+    // a finished row: to y (one slice) or to the slice's partials
+    auto put = [&](int tl, int row, int tk, float v) {
+        if (!direct) {
+            __hip_atomic_store(a.part + ((size_t)sl * nt + tk) * R + 16 * (T0 + tl) + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        const int r = 16 * (T0 + tl) + row;
+        if (r >= p.rows) return;
+        float* yr = a.y + (int64_t)(a.t0 + tk) * a.ys + r;
+        const float o = v + row_bias(p, r);
+        *yr = a.accumulate ? *yr + o : o;
+    };
+    // tile rows 0-7: gate of outputs 8 t + row, rows 8-15 the matching up values
+    auto put_gated = [&](int tl, int row, int tk, float gv, float uv) {
+        const int o = 8 * (T0 + tl) + row;
+        if (o >= p.o1) return;
+        gv += p.bias[0] ? bf16_to_f32(p.bias[0][o]) : 0.0f;
+        uv += p.bias[1] ? bf16_to_f32(p.bias[1][o]) : 0.0f;
+        a.y[(int64_t)(a.t0 + tk) * a.ys + o] = (gv / (1.0f + expf(-gv))) * uv;
+    };
+    auto emit = [&](int tl, const f32x4_t& run) {   // the whole wave
+        const int col = lane & 15, kq = lane >> 4;
+        const float us = unscale[col & 7];
+        if (gated && direct) {
+            f32x4_t up;
+#pragma unroll
+            for (int r = 0; r < 4; r++) up[r] = __shfl_xor(run[r], 32, 64);
+            if (col < nt && kq < 2)
+#pragma unroll
+                for (int r = 0; r < 4; r++) put_gated(tl, 4 * kq + r, col, run[r] * us, up[r] * us);
+        } else if (col < nt) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) put(tl, 4 * kq + r, col, run[r] * us);
+        }
+    };
+    mvt_run<FB, TS>(q, xh, img, gsum, gstride, nt, wg, nwg, wave, lane, ring, slots, emit);
+    lds_barrier();
+    // tiles shared between waves: their slots summed in wave order
+    const int nfw = g0.nt * g0.NF;
+    for (int i = threadIdx.x; i < g0.nt * 16 * nt; i += MK_THREADS) {
         const int tk = i % nt, rr = i / nt, tl = rr >> 4, row = rr & 15;
+        if (gated && direct && row >= 8) continue;
+        const int lo = tl * g0.NF, hi = lo + g0.NF;
+        float v = 0.0f, u = 0.0f;
+        bool whole = false;
+        for (int w = 0; w < MK_WAVES; w++) {
+            const int f0 = (nfw * w) >> 3, f1 = (nfw * (w + 1)) >> 3;
+            if (f1 <= f0 || f1 <= lo || f0 >= hi) continue;
+            if (f0 <= lo && f1 >= hi) { whole = true; break; }
+            const int slot = f0 / g0.NF == tl ? 0 : 1;
+            v += slots[((w * 2 + slot) * 16 + row) * DMM_TOK + tk];
+            if (gated && direct) u += slots[((w * 2 + slot) * 16 + row + 8) * DMM_TOK + tk];
+        }
+        if (whole) continue;
+        if (gated && direct) put_gated(tl, row, tk, v * unscale[tk], u * unscale[tk]);
+        else put(tl, row, tk, v * unscale[tk]);
+    }
+    if (direct) return;
+    // the slices' partials are stored (and visible at agent scope) before the tiles' counters move;
+    // the tile's last workgroup sums them in slice order
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int* last = reinterpret_cast<int*>(slots);
+    if ((int)threadIdx.x < g0.nt)
+        last[threadIdx.x] = __hip_atomic_fetch_add(a.cnt + T0 + threadIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    __syncthreads();
+    auto partial = [&](int tl, int row, int tk) {
         float v = 0.0f;
-        for (int w = 0; w < MK_WAVES; w++) v += part[((tl * MK_WAVES + w) * 16 + row) * DMM_TOK + tk];
-        v *= red[16 + tk];
-        float* yt = y + (int64_t)(t0 + tk) * ys;
-        if (p.gated) {
-            // tile rows 0-7: gate of outputs 8 t + row, rows 8-15 the matching up values
-            if (row >= 8) continue;
-            const int o = 8 * (gg.t0 + tl) + row;
-            if (o >= p.o1) continue;
-            float u = 0.0f;
-            for (int w = 0; w < MK_WAVES; w++) u += part[((tl * MK_WAVES + w) * 16 + row + 8) * DMM_TOK + tk];
-            u *= red[16 + tk];
-            const float gv = v + (p.bias[0] ? bf16_to_f32(p.bias[0][o]) : 0.0f);
-            const float uv = u + (p.bias[1] ? bf16_to_f32(p.bias[1][o]) : 0.0f);
-            yt[o] = (gv / (1.0f + expf(-gv))) * uv;
+        for (int k = 0; k < S; k++)
+            v += __hip_atomic_load(a.part + ((size_t)k * nt + tk) * R + 16 * (T0 + tl) + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return v;
+    };
+    for (int i = threadIdx.x; i < g0.nt * 16 * nt; i += MK_THREADS) {
+        const int tk = i % nt, rr = i / nt, tl = rr >> 4, row = rr & 15;
+        if (!last[tl]) continue;
+        if (gated) {
+            if (row < 8) {
+                const float gv = partial(tl, row, tk), uv = partial(tl, row + 8, tk);
+                const int o = 8 * (T0 + tl) + row;
+                if (o < p.o1) {
+                    const float gb = gv + (p.bias[0] ? bf16_to_f32(p.bias[0][o]) : 0.0f);
+                    const float ub = uv + (p.bias[1] ? bf16_to_f32(p.bias[1][o]) : 0.0f);
+                    a.y[(int64_t)(a.t0 + tk) * a.ys + o] = (gb / (1.0f + expf(-gb))) * ub;
+                }
+            }
         } else {
-            const int r = 16 * (gg.t0 + tl) + row;
-            if (r < p.rows) yt[r] = v + row_bias(p, r);
+            const int r = 16 * (T0 + tl) + row;
+            if (r < p.rows) {
+                float* yr = a.y + (int64_t)(a.t0 + tk) * a.ys + r;
+                const float o = partial(tl, row, tk) + row_bias(p, r);
+                *yr = a.accumulate ? *yr + o : o;
+            }
         }
     }
+    if ((int)threadIdx.x < g0.nt && last[threadIdx.x])
+        __hip_atomic_store(a.cnt + T0 + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int FB, int MODE>
@@ -431,8 +589,31 @@ hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* no
     }
 }
 
-hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, float* y, int ys, int T, hipStream_t s) {
-    if (!dpack_mv_supported(p) || T < 1 || T > DMM_TOK) return hipErrorInvalidValue;
+// Input slices of a small-batch launch of nt tokens: the fewest whose longest slice fits the
+// registers' share and whose nt images fit in LDS (0: none); *lds = the launch's dynamic LDS.
+static int mm_slices(const MvPhaseDesc& p, int nt, size_t* lds) {
+    const int FB = p.gs >> 3, GSH = FB == 4 ? 5 : 6, NF = ((p.K >> 7) + FB - 1) / FB;
+    for (int S = 1; S <= DMM_MAX_S && S <= NF; S++) {
+        int ks = 0;
+        for (int sl = 0; sl < S; sl++)
+            ks = std::max(ks, std::min(NF * (sl + 1) / S * FB * 128, p.K) - NF * sl / S * FB * 128);
+        if (ks > DMM_XR * 8 * MK_THREADS) continue;
+        const size_t b = sizeof(float) * ((size_t)nt * (ks + (((ks >> GSH) + 3) & ~3)) + MV_ZERO + DMM_SLOTS + DMM_RED);
+        if (b <= (size_t)DMV_MAX_LDS) { *lds = b; return S; }
+    }
+    return 0;
+}
+
+size_t dpack_mm_split_floats(const MvPhaseDesc& p) {
+    size_t lds = 0;
+    const int S = dpack_mv_supported(p) ? mm_slices(p, DMM_TOK, &lds) : 0;   // the most slices: at the most tokens
+    if (S <= 1) return 0;
+    return (size_t)(p.tiles + 63) / 64 * 64 + (size_t)S * DMM_TOK * 16 * p.tiles;
+}
+
+hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, const float* norm_w, float eps, float* y, int ys,
+                           bool accumulate, int T, float* split, size_t split_floats, hipStream_t s) {
+    if (!dpack_mv_supported(p) || T < 1 || T > DMM_TOK || (p.gated && accumulate)) return hipErrorInvalidValue;
     static int cus = 0;
     if (!cus) {
         int dev = 0;
@@ -441,39 +622,29 @@ hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, float* 
     }
     static bool attr = false;
     if (!attr) {
-        for (const void* f : {(const void*)dpack_mm_kernel<4>, (const void*)dpack_mm_kernel<8>})
+        for (const void* f : {(const void*)dpack_mm_kernel<4, false>, (const void*)dpack_mm_kernel<8, false>,
+                              (const void*)dpack_mm_kernel<4, true>, (const void*)dpack_mm_kernel<8, true>})
             if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, DMV_MAX_LDS) != hipSuccess) return hipErrorInvalidValue;
         attr = true;
     }
-    // a single-part, ungated phase of many tiles (the lm_head) runs in row chunks of at most
-    // DMM_TPW tiles per workgroup: every wave's partial rows of a tile sit in LDS
-    constexpr int DMM_TPW = 4;
-    const int FB = p.gs >> 3, NF = ((p.K >> 7) + FB - 1) / FB;
-    const size_t tile_bytes = (size_t)NF * (FB + 1) * 1024;
-    const int chunk = !p.gated && p.o2 == 0 ? DMM_TPW * cus : p.tiles;
-    for (int c0 = 0; c0 < p.tiles; c0 += chunk) {
-        MvPhaseDesc q = p;
-        q.tiles = std::min(chunk, p.tiles - c0);
-        if (c0 > 0) {
-            q.code = p.code + (size_t)c0 * tile_bytes;
-            q.rows = p.rows - 16 * c0; q.o1 = q.rows;
-            if (p.bias[0]) q.bias[0] = p.bias[0] + 16 * c0;
-        }
-        float* yc = y + (c0 > 0 ? 16 * c0 : 0);
-        const int nwg = std::min(q.tiles, cus);
-        const int tpw = (q.tiles + nwg - 1) / nwg;
-        if (tpw > MK_TPW) return hipErrorInvalidValue;
-        const int gstride = ((q.K / q.gs) + 3) & ~3;
-        const size_t fixed = sizeof(float) * ((size_t)MV_ZERO + (size_t)tpw * MK_WAVES * 16 * DMM_TOK + 16 + DMM_TOK);
-        const size_t per_tok = sizeof(float) * ((size_t)q.K + gstride);
-        if (fixed + per_tok > DMV_MAX_LDS) return hipErrorInvalidValue;
-        const int tp = (int)std::min<size_t>(DMM_TOK, (DMV_MAX_LDS - fixed) / per_tok);
-        for (int t0 = 0; t0 < T; t0 += tp) {   // tokens per launch: as many as fit in LDS
-            const int nt = std::min(tp, T - t0);
-            const size_t lds = fixed + per_tok * nt;
-            if (q.gs == 32) hipLaunchKernelGGL(dpack_mm_kernel<4>, dim3(nwg), dim3(MK_THREADS), lds, s, q, x, xs, yc, ys, t0, nt, tpw);
-            else hipLaunchKernelGGL(dpack_mm_kernel<8>, dim3(nwg), dim3(MK_THREADS), lds, s, q, x, xs, yc, ys, t0, nt, tpw);
-        }
+    size_t lds = 0;
+    const int S = mm_slices(p, T, &lds);
+    if (S == 0) return hipErrorInvalidValue;
+    const size_t tiles_al = (size_t)(p.tiles + 63) / 64 * 64;
+    if (S > 1 && (!split || split_floats < tiles_al + (size_t)S * T * 16 * p.tiles)) return hipErrorInvalidValue;
+    MmArgs a;
+    a.p = p; a.x = x; a.xs = xs; a.nw = norm_w; a.eps = eps; a.y = y; a.ys = ys; a.accumulate = accumulate ? 1 : 0;
+    a.t0 = 0; a.nt = T;
+    a.cnt = reinterpret_cast<unsigned*>(split); a.part = split ? split + tiles_al : nullptr;
+    // one workgroup per CU over all slices (the images fill most of the LDS)
+    const int nwg = std::min(p.tiles, std::max(1, cus / S));
+    const bool fb4 = p.gs == 32;
+    if (S == 1) {
+        if (fb4) hipLaunchKernelGGL((dpack_mm_kernel<4, false>), dim3(nwg), dim3(MK_THREADS), lds, s, a);
+        else hipLaunchKernelGGL((dpack_mm_kernel<8, false>), dim3(nwg), dim3(MK_THREADS), lds, s, a);
+    } else {
+        if (fb4) hipLaunchKernelGGL((dpack_mm_kernel<4, true>), dim3(nwg, S), dim3(MK_THREADS), lds, s, a);
+        else hipLaunchKernelGGL((dpack_mm_kernel<8, true>), dim3(nwg, S), dim3(MK_THREADS), lds, s, a);
     }
     return hipGetLastError();
 }

@@ -368,6 +368,16 @@ static int tiles_setup(Model* m) {
     }
     if (repackable(m->head)) m->tile_head = repack_phase(m, &m->head, 1, false, rc);
     if (rc) return rc;
+    // the verify batch's input-slice scratch: the largest any phase needs (counters zeroed once)
+    size_t mm = 0;
+    for (const LayerDev& d : host)
+        for (const MvPhaseDesc* p : {&d.qkv, &d.o, &d.gu, &d.down}) mm = std::max(mm, dpack_mm_split_floats(*p));
+    if (m->tile_head.code) mm = std::max(mm, dpack_mm_split_floats(m->tile_head));
+    if (mm) {
+        if ((rc = dalloc(m, &m->mm_split, mm))) return rc;
+        HIPCHECK(hipMemset(m->mm_split, 0, mm * 4));
+        m->mm_split_floats = mm;
+    }
     HIPCHECK(hipStreamSynchronize(m->stream));
     m->tile_layers = host;
     return MLXR_OK;
@@ -737,6 +747,64 @@ int project_tiles(Model* m, const MvPhaseDesc& p, const float* x, int xs, float*
     return MLXR_OK;
 }
 
+// Attention of a batch's T queries (positions *dpos .. *dpos + T - 1) after their q|k|v: QK norms,
+// RoPE and the cache write, then flash attention (prefill chunks) or the decode attention per
+// query (verify batches, T <= 8).
+int attend(Model* m, int li, int T) {
+    const Config& c = m->cfg;
+    hipStream_t s = m->stream;
+    Layer& ly = m->layers[li];
+    QkvPostArgs pa; pa.qkv = m->qkv; pa.row_stride = m->qkv_cols; pa.inv_freq = m->inv_freq; pa.kc = ly.kc; pa.vc = ly.vc;
+    pa.pt = m->page_table; pa.qn = ly.q_norm; pa.kn = ly.k_norm; pa.D = c.D; pa.nH = c.nH; pa.nKV = c.nKV;
+    pa.rot_dim = c.rot_dim; pa.traditional = c.traditional; pa.T = T; pa.dpos = m->dpos; pa.eps = c.eps;
+    HIPCHECK(launch_qkv_post(pa, s));
+    if (m->sparse_alloc) HIPCHECK(launch_sparse_index(ly.kc, m->page_table, ly.idx, c.nKV, c.D, m->dpos, 0, T, s));
+    const float scale = c.query_scale * c.rope_attention_factor * c.rope_attention_factor;
+    if (T > 8) {   // prefill chunk: flash attention on the matrix cores
+        FlashArgs fa; fa.q = m->qkv; fa.q_stride = m->qkv_cols; fa.kc = ly.kc; fa.vc = ly.vc; fa.pt = m->page_table;
+        fa.out = m->attn; fa.out_stride = c.nH * c.D; fa.D = c.D; fa.nH = c.nH; fa.nKV = c.nKV; fa.T = T;
+        fa.dpos = m->dpos; fa.scale = scale;
+        HIPCHECK(launch_flash_prefill(fa, s));
+    } else {       // verify batch: the decode attention per query
+        AttnArgs aa; aa.q = m->qkv; aa.q_stride = m->qkv_cols; aa.kc = ly.kc; aa.vc = ly.vc; aa.pt = m->page_table;
+        aa.out = m->attn; aa.out_stride = c.nH * c.D; aa.part = m->part; aa.D = c.D; aa.nH = c.nH; aa.nKV = c.nKV; aa.T = T;
+        aa.nsplit = m->nsplit_dec; aa.dpos = m->dpos; aa.scale = scale;
+        HIPCHECK(launch_attn_decode(aa, s));
+    }
+    return MLXR_OK;
+}
+
+// A verify batch (T <= 8) over the repacked tiles: every projection is one small-batch launch with
+// the tokens in the matrix cores' columns, the RMSNorms fused into the launches that read the
+// residual stream and the residual adds into the ones that write it (o_proj, down: h += W x).
+int encode_verify(Model* m, int T, bool want_logits, bool all_logits) {
+    const Config& c = m->cfg;
+    hipStream_t s = m->stream;
+    const int H = c.H, I = c.I;
+    auto mm = [&](const MvPhaseDesc& p, const float* x, int xs, const float* nw, float* y, int ys, bool acc, int n) {
+        return launch_dpack_mm(p, x, xs, nw, c.eps, y, ys, acc, n, m->mm_split, m->mm_split_floats, s);
+    };
+    for (int li = 0; li < c.L; li++) {
+        const Layer& ly = m->layers[li];
+        const LayerDev& d = m->tile_layers[li];
+        HIPCHECK(mm(d.qkv, m->h, H, ly.in_norm, m->qkv, m->qkv_cols, false, T));
+        if (int rc = attend(m, li, T)) return rc;
+        HIPCHECK(mm(d.o, m->attn, c.nH * c.D, nullptr, m->h, H, true, T));
+        HIPCHECK(mm(d.gu, m->h, H, ly.post_norm, m->mlp, I, false, T));   // SiLU(gate) * up
+        HIPCHECK(mm(d.down, m->mlp, I, nullptr, m->h, H, true, T));
+    }
+    if (!want_logits) return MLXR_OK;
+    const int r0 = all_logits ? 0 : T - 1, n = all_logits ? T : 1;
+    if (m->tile_head.code) {
+        HIPCHECK(mm(m->tile_head, m->h + (size_t)r0 * H, H, m->final_norm, m->logits, c.V, false, n));
+        return MLXR_OK;
+    }
+    HIPCHECK(launch_rms_norm(m->h, m->xn, m->final_norm, H, T, H, c.eps, s));
+    for (int t = 0; t < n; t++)
+        HIPCHECK(launch_qmv(qmv_args(&m->head, 1, m->xn + (size_t)(r0 + t) * H, nullptr, 0, m->logits + (size_t)t * c.V, EPI_STORE), s));
+    return MLXR_OK;
+}
+
 int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
     const Config& c = m->cfg;
     hipStream_t s = m->stream;
@@ -747,61 +815,36 @@ int encode_batch(Model* m, int T, bool want_logits, bool all_logits) {
     const bool tiles = T > 8 && (int)m->tile_layers.size() == c.L;
     const bool small_tiles = T <= 8 && (int)m->tile_layers.size() == c.L && m->decode_mode != 2;
     HIPCHECK(launch_qembed(m->embed.m, H, m->embed.bits, m->embed.gs, m->embed.st, m->hist, m->dpos, T, m->h, s));
+    if (small_tiles) return encode_verify(m, T, want_logits, all_logits);
     if (tiles) HIPCHECK(launch_rms_norm_f16(m->h, m->layers[0].in_norm, H, T, H, c.eps, m->xbf, m->xsc, s));
     else HIPCHECK(launch_rms_norm(m->h, m->xn, m->layers[0].in_norm, H, T, H, c.eps, s));
     for (int li = 0; li < c.L; li++) {
         Layer& ly = m->layers[li];
         const Lin qkvp[3] = {ly.q, ly.k, ly.v};
         const LayerDev* tl = tiles ? &m->tile_layers[li] : nullptr;
-        const LayerDev* st = small_tiles ? &m->tile_layers[li] : nullptr;
-        if (st) HIPCHECK(launch_dpack_mm(st->qkv, m->xn, H, m->qkv, m->qkv_cols, T, s));
-        else if (int rc = tl ? project_tiles(m, tl->qkv, nullptr, H, m->qkv, m->qkv_cols, T)
-                             : project(m, qkvp, 3, m->xn, H, m->qkv, m->qkv_cols, T)) return rc;
-        QkvPostArgs pa; pa.qkv = m->qkv; pa.row_stride = m->qkv_cols; pa.inv_freq = m->inv_freq; pa.kc = ly.kc; pa.vc = ly.vc;
-        pa.pt = m->page_table; pa.qn = ly.q_norm; pa.kn = ly.k_norm; pa.D = c.D; pa.nH = c.nH; pa.nKV = c.nKV;
-        pa.rot_dim = c.rot_dim; pa.traditional = c.traditional; pa.T = T; pa.dpos = m->dpos; pa.eps = c.eps;
-        HIPCHECK(launch_qkv_post(pa, s));
-        if (m->sparse_alloc) HIPCHECK(launch_sparse_index(ly.kc, m->page_table, ly.idx, c.nKV, c.D, m->dpos, 0, T, s));
-        const float scale = c.query_scale * c.rope_attention_factor * c.rope_attention_factor;
-        if (T > 8) {   // prefill chunk: flash attention on the matrix cores
-            FlashArgs fa; fa.q = m->qkv; fa.q_stride = m->qkv_cols; fa.kc = ly.kc; fa.vc = ly.vc; fa.pt = m->page_table;
-            fa.out = m->attn; fa.out_stride = c.nH * c.D; fa.D = c.D; fa.nH = c.nH; fa.nKV = c.nKV; fa.T = T;
-            fa.dpos = m->dpos; fa.scale = scale;
-            HIPCHECK(launch_flash_prefill(fa, s));
-        } else {       // verify batch: the decode attention per query
-            AttnArgs aa; aa.q = m->qkv; aa.q_stride = m->qkv_cols; aa.kc = ly.kc; aa.vc = ly.vc; aa.pt = m->page_table;
-            aa.out = m->attn; aa.out_stride = c.nH * c.D; aa.part = m->part; aa.D = c.D; aa.nH = c.nH; aa.nKV = c.nKV; aa.T = T;
-            aa.nsplit = m->nsplit_dec; aa.dpos = m->dpos; aa.scale = scale;
-            HIPCHECK(launch_attn_decode(aa, s));
-        }
-        if (st) HIPCHECK(launch_dpack_mm(st->o, m->attn, c.nH * c.D, m->tmp, H, T, s));
-        else if (int rc = tl ? project_tiles(m, tl->o, m->attn, c.nH * c.D, m->tmp, H, T)
-                             : project(m, &ly.o, 1, m->attn, c.nH * c.D, m->tmp, H, T)) return rc;
+        if (int rc = tl ? project_tiles(m, tl->qkv, nullptr, H, m->qkv, m->qkv_cols, T)
+                        : project(m, qkvp, 3, m->xn, H, m->qkv, m->qkv_cols, T)) return rc;
+        if (int rc = attend(m, li, T)) return rc;
+        if (int rc = tl ? project_tiles(m, tl->o, m->attn, c.nH * c.D, m->tmp, H, T)
+                        : project(m, &ly.o, 1, m->attn, c.nH * c.D, m->tmp, H, T)) return rc;
         if (tl) {
             HIPCHECK(launch_add_rms_norm_f16(m->h, m->tmp, ly.post_norm, H, T, c.eps, m->xbf, m->xsc, s));
             if (int rc = project_tiles(m, tl->gu, nullptr, H, m->mlp, I, T)) return rc;
         } else {
             HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, ly.post_norm, H, T, c.eps, s));
-            if (st) {
-                HIPCHECK(launch_dpack_mm(st->gu, m->xn, H, m->mlp, I, T, s));   // SiLU(gate) * up
-            } else {
-                const Lin gup[2] = {ly.gate, ly.up};
-                if (int rc = project(m, gup, 2, m->xn, H, m->gu, 2 * I, T)) return rc;
-                HIPCHECK(launch_silu_mul(m->gu, m->mlp, I, T, s));
-            }
+            const Lin gup[2] = {ly.gate, ly.up};
+            if (int rc = project(m, gup, 2, m->xn, H, m->gu, 2 * I, T)) return rc;
+            HIPCHECK(launch_silu_mul(m->gu, m->mlp, I, T, s));
         }
-        if (st) HIPCHECK(launch_dpack_mm(st->down, m->mlp, I, m->tmp, H, T, s));
-        else if (int rc = tl ? project_tiles(m, tl->down, m->mlp, I, m->tmp, H, T)
-                             : project(m, &ly.down, 1, m->mlp, I, m->tmp, H, T)) return rc;
+        if (int rc = tl ? project_tiles(m, tl->down, m->mlp, I, m->tmp, H, T)
+                        : project(m, &ly.down, 1, m->mlp, I, m->tmp, H, T)) return rc;
         const bool last = li + 1 == c.L;
         if (last && !want_logits) continue;
         if (tl && !last) HIPCHECK(launch_add_rms_norm_f16(m->h, m->tmp, m->layers[li + 1].in_norm, H, T, c.eps, m->xbf, m->xsc, s));
         else HIPCHECK(launch_add_rms_norm(m->h, m->tmp, m->xn, last ? m->final_norm : m->layers[li + 1].in_norm, H, T, c.eps, s));
     }
     if (!want_logits) return MLXR_OK;
-    if (all_logits && small_tiles && m->tile_head.code) {
-        HIPCHECK(launch_dpack_mm(m->tile_head, m->xn, H, m->logits, c.V, T, s));
-    } else if (all_logits) {
+    if (all_logits) {
         for (int t = 0; t < T; t++)
             HIPCHECK(launch_qmv(qmv_args(&m->head, 1, m->xn + (size_t)t * H, nullptr, 0, m->logits + (size_t)t * c.V, EPI_STORE), s));
     } else {

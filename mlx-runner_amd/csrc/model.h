@@ -61,6 +61,8 @@ struct Model {
     int* hist = nullptr; int* status = nullptr; uint64_t* rng = nullptr;
     int* dpos = nullptr;                 // position of the step being processed (device)
     float *h = nullptr, *xn = nullptr, *tmp = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *mlp = nullptr;
+    float* mm_split = nullptr;       // input-slice scratch of the verify batch's small-batch matvec (dpack_mm_split_floats)
+    size_t mm_split_floats = 0;
     float* dmv_split = nullptr;      // [2][H] input-slice partials of the kernel-per-op down matvec (long inputs)
     float* logits = nullptr; float* part = nullptr; float* bmax = nullptr; int* barg = nullptr;
     float* qsplit = nullptr;            // the other widths' prefill GEMM split over K (QGEMM_SPLIT_FLOATS, counters at zero)

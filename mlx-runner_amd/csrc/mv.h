@@ -127,8 +127,9 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 // LDS of a matvec phase (the attention phase reuses the same memory, so every phase rebuilds it).
 struct MvLds { float* xf; float* xh; float* gsum; float* zero16; float* hown; float* part; };
 
-// LD(t, lo, hi) yields values 8t..8t+7 of x.
-template <typename LD>
+// LD(t, lo, hi) yields values 8t..8t+7 of x. BAR: end with a barrier (the packed x readable by
+// every wave); without it the caller places one after packing several inputs.
+template <typename LD, bool BAR = true>
 __device__ __forceinline__ float pack_x16_from(const LD& ld, int K, float gmax, const MvLds& L, int gsh) {
     float* xh = L.xh; float* gsum = L.gsum;
     if (threadIdx.x < MV_ZERO) L.zero16[threadIdx.x] = 0.0f;
@@ -167,7 +168,7 @@ __device__ __forceinline__ float pack_x16_from(const LD& ld, int K, float gmax, 
         if (gsh == 6) xsum += __shfl_xor(xsum, 4, 64);
         if ((t & ((1 << (gsh - 3)) - 1)) == 0) gsum[t >> (gsh - 3)] = xsum;
     }
-    lds_barrier();
+    if constexpr (BAR) lds_barrier();
     return 1.0f / up;
 }
 __device__ __forceinline__ float pack_x16(const float* xf, int K, float gmax, const MvLds& L, int gsh) {

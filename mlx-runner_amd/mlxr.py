@@ -95,7 +95,7 @@ def _load():
         "mlxr_k_qgemm": (I, [C.POINTER(QMat), I, I, I, I, I, P, I, P, I]),
         "mlxr_k_qgemm_tiles": (I, [C.POINTER(QMat), I, I, I, I, I, P, I, P, I]),
         "mlxr_k_qmv_tiles": (I, [C.POINTER(QMat), I, I, I, I, P, P, C.c_float, P, I]),
-        "mlxr_k_qmm_tiles": (I, [C.POINTER(QMat), I, I, I, I, I, P, I, P, I]),
+        "mlxr_k_qmm_tiles": (I, [C.POINTER(QMat), I, I, I, I, I, P, I, P, F, P, I]),
         "mlxr_k_qembed": (I, [C.POINTER(QMat), I, I, I, I, P, I, P]),
         "mlxr_k_rms_norm": (I, [P, P, P, P, I, I, F]),
         "mlxr_k_qkv_post": (I, [P, I, P, P, P, I, P, P, I, I, I, I, I, I, I, F]),

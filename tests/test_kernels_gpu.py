@@ -262,15 +262,23 @@ def test_qmv_tiles_input_slices_share_scratch(gpu):
         assert max_rel_err(qmv_tiles(gpu, [f], x, mode=1, y0=y0), y0 + ref) < TOL, (K, O)
 
 
-def qmm_tiles(mlxr, fxs, x, gated=False):
+def qmm_tiles(mlxr, fxs, x, mode=0, norm_w=None, eps=1e-6, y0=None):
     T, K = x.shape
     qm = (mlxr.QMat * len(fxs))(*[f.device(mlxr) for f in fxs])
-    cols = fxs[0].O if gated else sum(f.O for f in fxs)
+    cols = fxs[0].O if mode == 2 else sum(f.O for f in fxs)
     dx = mlxr.DeviceArray.from_numpy(np.ascontiguousarray(x))
-    dy = mlxr.DeviceArray.from_numpy(np.full((T, cols), np.nan, np.float32))
-    mlxr.check(mlxr.lib.mlxr_k_qmm_tiles(qm, len(fxs), K, fxs[0].gs, int(gated), T, dx.ptr, K, dy.ptr, cols))
+    dy = mlxr.DeviceArray.from_numpy(np.full((T, cols), np.nan, np.float32) if y0 is None else np.asarray(y0, np.float32))
+    dn = mlxr.DeviceArray.from_numpy(np.asarray(norm_w, np.float32)) if norm_w is not None else None
+    mlxr.check(mlxr.lib.mlxr_k_qmm_tiles(qm, len(fxs), K, fxs[0].gs, mode, T, dx.ptr, K, dn.ptr if dn else None, eps,
+                                         dy.ptr, cols))
     mlxr.synchronize()
     return dy.numpy()
+
+
+def _gated_ref(g, u, x):
+    gr, ur = g.oracle(oracle).matmul_f64(x), u.oracle(oracle).matmul_f64(x)
+    return np.array([[oracle.lib.orc_silu_mul(float(a), float(b)) for a, b in zip(gr[t], ur[t])] for t in range(len(x))],
+                    np.float32)
 
 
 @pytest.mark.parametrize("gs", [32, 64])
@@ -278,28 +286,47 @@ def test_qmm_tiles_small_batch(gpu, gs):
     """The verify batch's projections over the repacked tiles (qmm / qmvx4, Kernels.swift:60-113,
     518-622): T = 1..8 tokens in the matrix cores' B columns, every token against the oracle's fp64
     product at the 1e-3 matvec gate: fused parts with bias and ragged rows, inputs from one scale
-    group to 12288 values (several launches of fewer tokens when x does not fit in LDS at once),
-    rows of very different magnitude, and the gated MLP form."""
+    group to 12288 values (the long ones in input slices summed across workgroups), rows of very
+    different magnitude, a single part of many tiles per workgroup (the lm_head), and the gated
+    form."""
     rng = np.random.default_rng(gs)
     for K, Os in ((128, (40,)), (1024, (264, 40, 88)), (4096, (72,)), (12288, (24,))):
         fxs = [QuantFixture(O, K, 4, gs, seed=O + K, with_bias=len(Os) > 1, fast=True) for O in Os]
         for T in (1, 3, 8):
-            x = rng.normal(0, 1, (T, K)).astype(np.float32) * (10.0 ** np.linspace(-3, 3, T)).astype(np.float32)[:, None]
+            mag = (10.0 ** np.linspace(-3, 3, T)).astype(np.float32)
+            x = rng.normal(0, 1, (T, K)).astype(np.float32) * mag[:, None]
             ref = np.concatenate([f.oracle(oracle).matmul_f64(x) for f in fxs], axis=1)
             got = qmm_tiles(gpu, fxs, x)
             for t in range(T):
-                assert max_rel_err(got[t] / np.float32(10.0 ** np.linspace(-3, 3, T)[t]),
-                                   ref[t] / 10.0 ** np.linspace(-3, 3, T)[t]) < TOL, (K, T, t)
-    # a single part of more tiles than four per workgroup (the lm_head: row chunks of its own)
-    f = QuantFixture(16 * 4 * 256 * 2 + 40, 256, 4, gs, seed=7, fast=True)
+                assert max_rel_err(got[t] / mag[t], ref[t] / mag[t]) < TOL, (K, T, t)
+    f = QuantFixture(16 * 40 * 256 + 40, 256, 4, gs, seed=7, fast=True)
     x = rng.normal(0, 1, (2, 256)).astype(np.float32)
     assert max_rel_err(qmm_tiles(gpu, [f], x), f.oracle(oracle).matmul_f64(x)) < TOL
-    K, I = 2048, 200
-    g, u = (QuantFixture(I, K, 4, gs, seed=s, fast=True) for s in (5, 6))
-    x = rng.normal(0, 1, (5, K)).astype(np.float32)
-    gr, ur = g.oracle(oracle).matmul_f64(x), u.oracle(oracle).matmul_f64(x)
-    gated = np.array([[oracle.lib.orc_silu_mul(float(a), float(b)) for a, b in zip(gr[t], ur[t])] for t in range(5)], np.float32)
-    assert max_rel_err(qmm_tiles(gpu, [g, u], x, gated=True), gated) < TOL
+    # gated: one slice, and two slices summed before the SiLU (x scaled so that gate and up stay
+    # O(10): the product's rounding grows with |gate| * |up|, not with the result)
+    for K, T in ((2048, 5), (8192, 8)):
+        g, u = (QuantFixture(200, K, 4, gs, seed=s + K, fast=True) for s in (5, 6))
+        x = rng.normal(0, 1, (T, K)).astype(np.float32) / np.float32(np.sqrt(K / 64))
+        assert max_rel_err(qmm_tiles(gpu, [g, u], x, mode=2), _gated_ref(g, u, x)) < TOL, K
+
+
+@pytest.mark.parametrize("K,T", [(4096, 5), (12288, 8)])
+def test_qmm_tiles_norm_and_accumulate(gpu, K, T):
+    """The verify batch's fused forms: x[t] := RMSNorm(x[t]) * w inside the launch (the statistics
+    over the whole input also when it runs in slices), and the residual add y[t] += W x[t]."""
+    rng = np.random.default_rng(K + T)
+    fxs = [QuantFixture(O, K, 4, 64, seed=O, with_bias=True, fast=True) for O in (136, 56)]
+    h = rng.normal(0, 3, (T, K)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    xn = oracle.rms_norm(h, w, 1e-6)
+    ref = np.concatenate([f.oracle(oracle).matmul_f64(xn) for f in fxs], axis=1)
+    assert max_rel_err(qmm_tiles(gpu, fxs, h, norm_w=w), ref) < TOL
+    y0 = rng.normal(0, 1, ref.shape).astype(np.float32)
+    assert max_rel_err(qmm_tiles(gpu, fxs, h, mode=1, y0=y0), y0 + np.concatenate(
+        [f.oracle(oracle).matmul_f64(h) for f in fxs], axis=1)) < TOL
+    g, u = (QuantFixture(96, K, 4, 64, seed=s, fast=True) for s in (8, 9))
+    w = w / np.float32(np.sqrt(K / 64))   # gate and up O(10), as in the gated small-batch check
+    assert max_rel_err(qmm_tiles(gpu, [g, u], h, mode=2, norm_w=w), _gated_ref(g, u, oracle.rms_norm(h, w, 1e-6))) < TOL
 
 
 def _decode_input(kind, K, rng):
