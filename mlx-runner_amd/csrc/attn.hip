@@ -220,6 +220,229 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a) {
     a.out[(int64_t)t * a.out_stride + (int64_t)h * D + d] = o / Ls;
 }
 
+// Verify batch (T = 2..8 queries at positions *dpos .. *dpos + T - 1, dense keys): grid (nKV,
+// nsplit); block 256. One workgroup per (KV head, key range) serves all G x T query rows of the head
+// (row r = t G + g), so each K and V row is read from memory once for the whole batch rather than
+// once per query. Every K and V load of the range is issued at once, after the row offsets (one
+// memory round trip for the range), into LDS; each wave's q rows load straight
+// into registers meanwhile. Both products run on the bf16 matrix cores
+// (v_mfma_f32_16x16x32_bf16), 16 x 16 output tiles spread over the waves:
+//   S^T = K Q^T    A = K rows, B = q * scale as bf16 hi + lo (the persistent decode step's split)
+//   O = P V        A = P as three bf16 terms (hi + mid + lo = p to ~2^-24), B = V through the LDS
+//                  transpose read (lane j of a 16-lane group reads key base + (j >> 2), dims
+//                  4 (j & 3) .. + 3; lane i receives dim i of keys base .. base + 3)
+// K and V are bf16 in the cache, so the only roundings are the splits'. Keys past a row's own
+// position are masked (its softmax covers keys 0 .. *dpos + t). Rows and keys past the batch read
+// copies of the last row / key (finite) and their results are dropped. Writes the same partials
+// [t][h][split] as attn_split_kernel for attn_combine_kernel.
+constexpr int ATT_MC = 128;                  // keys per workgroup (max; the host sets a.cap >= ceil(count / nsplit))
+constexpr int ATT_VR = ATT_MC / 16;          // K / V staging: 16 rows per pass of 256 threads (16 bytes each)
+constexpr int ATT_RS = ATT_D + 8;            // bf16 row stride of the K image (16 rows of a read: distinct banks)
+typedef float f32x4_att __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_att __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4_att att_mfma(const uint4 a, const uint4 b, f32x4_att c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_att, a), __builtin_bit_cast(bf16x8_att, b), c, 0, 0, 0);
+}
+// The LDS layout of one workgroup (byte offsets, 16-byte aligned). The K image is dead once the
+// scores are in, so the probabilities' bf16 terms take its place.
+struct AttMultiLds {
+    int GP, KQ, PS, scs;
+    size_t ks, pb, vs, sc, rowi, ro, mx, ls, bytes;
+    __host__ __device__ AttMultiLds(int GT, int cap) {
+        GP = (GT + 15) / 16 * 16;            // query rows, padded to whole tiles
+        KQ = (cap + 31) / 32 * 32;           // keys, padded to whole 32-key steps
+        PS = KQ + 8; scs = KQ + 4;
+        ks = pb = 0;                                     // [KQ][ATT_RS] bf16 K | [3][GP][PS] bf16 p terms
+        const size_t kb = (size_t)KQ * ATT_RS * 2, pbb = (size_t)3 * GP * PS * 2;
+        vs = kb > pbb ? kb : pbb;                        // [KQ][128] bf16 V, 16-byte chunk c of key k at c ^ (k & 15)
+        sc = vs + (size_t)KQ * ATT_D * 2;                // [GP][scs] f32 scores
+        rowi = sc + (size_t)GP * scs * 4;                // [KQ] cache rows
+        ro = rowi + (size_t)KQ * 4;                      // [GP] int2: a row's token base and (head, split) row in the partials
+        mx = ro + (size_t)GP * 8;                        // [GP] row max
+        ls = mx + (size_t)GP * 4;                        // [GP] row sum
+        bytes = ls + (size_t)GP * 4;
+    }
+};
+// (x0, x1) -> packed bf16 pair (hardware round to nearest even)
+__device__ __forceinline__ uint32_t att_pk(float x0, float x1) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    const bf2 h = {(__bf16)x0, (__bf16)x1};
+    return __builtin_bit_cast(uint32_t, h);
+}
+typedef short att_v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) att_v4s* att_lv4;
+__global__ __launch_bounds__(256) void attn_multi_kernel(AttnArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_b[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvh = blockIdx.x, split = blockIdx.y, D = ATT_D;
+    const int G = a.nH / a.nKV, T = a.T, GT = G * T, cap = a.cap;
+    const int pos0 = *a.dpos, count = pos0 + T;
+    const int c = (count + a.nsplit - 1) / a.nsplit;
+    const int n0 = min(count, split * c), n1 = min(count, n0 + min(c, cap)), nk = n1 - n0;
+    const int rows = a.nH * a.nsplit;
+    if (nk <= 0) {   // a range past the batch's last key: empty partials
+        for (int r = wave; r < GT; r += 4) {
+            const int t = r / G, g = r % G, rr = (kvh * G + g) * a.nsplit + split;
+            float* pt_ = a.part + (int64_t)t * rows * (D + 2);
+            *reinterpret_cast<float2*>(pt_ + 2 * rows + (int64_t)rr * D + 2 * lane) = float2{0.0f, 0.0f};
+            if (lane == 0) { pt_[rr] = -1e30f; pt_[rows + rr] = 0.0f; }
+        }
+        return;
+    }
+    const AttMultiLds L(GT, cap);
+    uint16_t* ks = reinterpret_cast<uint16_t*>(lds_b + L.ks);
+    uint16_t* pb = reinterpret_cast<uint16_t*>(lds_b + L.pb);
+    uint8_t* vs = lds_b + L.vs;
+    float* sc = reinterpret_cast<float*>(lds_b + L.sc);
+    int* rowi = reinterpret_cast<int*>(lds_b + L.rowi);
+    int2* ro = reinterpret_cast<int2*>(lds_b + L.ro);
+    float* mx = reinterpret_cast<float*>(lds_b + L.mx);
+    float* lsum = reinterpret_cast<float*>(lds_b + L.ls);
+    const int GP = L.GP, nkq = (nk + 31) / 32 * 32;
+    const int l16 = lane & 15, l4 = lane >> 4;
+    const int nrt = GP / 16, nkt = (nk + 15) / 16;
+    // this wave's q rows (row tile rt: rows 16 rt + l16, dims 8 l4 + 32 s .. + 7) as the B operand,
+    // scaled and split into bf16 hi + lo
+    uint4 bh[4], bl[4];
+    auto load_q = [&](int rt) {
+        const int r = min(16 * rt + l16, GT - 1), t = r / G, g = r - t * G;
+        const float* qr = a.q + (int64_t)t * a.q_stride + (int64_t)(kvh * G + g) * D + 8 * l4;
+        float4 v[8];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; s4++) { v[2 * s4] = *reinterpret_cast<const float4*>(qr + 32 * s4); v[2 * s4 + 1] = *reinterpret_cast<const float4*>(qr + 32 * s4 + 4); }
+#pragma unroll
+        for (int s4 = 0; s4 < 4; s4++) {
+            const float x[8] = {v[2 * s4].x, v[2 * s4].y, v[2 * s4].z, v[2 * s4].w, v[2 * s4 + 1].x, v[2 * s4 + 1].y, v[2 * s4 + 1].z, v[2 * s4 + 1].w};
+            uint32_t h[4], lo[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float x0 = x[2 * j] * a.scale, x1 = x[2 * j + 1] * a.scale;
+                h[j] = att_pk(x0, x1);
+                lo[j] = att_pk(x0 - __uint_as_float(h[j] << 16), x1 - __uint_as_float(h[j] & 0xffff0000u));
+            }
+            bh[s4] = uint4{h[0], h[1], h[2], h[3]}; bl[s4] = uint4{lo[0], lo[1], lo[2], lo[3]};
+        }
+    };
+    int cur_rt = wave % nrt;
+    load_q(cur_rt);
+    if (tid < nk) rowi[tid] = (int)kv_row(a.pt, a.nKV, kvh, n0 + tid);   // ATT_MC <= 256 keys
+    if (tid < GT) {   // partials of row r = t G + g: [t][(head, split)], below 2^31 floats
+        const int t = tid / G, g = tid - t * G;
+        ro[tid] = int2{t * rows * (D + 2), (kvh * G + g) * a.nsplit + split};
+    }
+    __syncthreads();
+    {   // K and V rows to LDS: every load issued before the first store (unconditional: keys
+        // past the range read the last key, and their rows, up to the image's edge, hold copies of it)
+        const int vrow = tid >> 4, vd = tid & 15;
+        uint4 kv[ATT_VR], vv[ATT_VR];
+#pragma unroll
+        for (int i = 0; i < ATT_VR; i++) {
+            const int64_t row = rowi[min(vrow + 16 * i, nk - 1)];
+            kv[i] = reinterpret_cast<const uint4*>(a.kc + row * D)[vd];
+            vv[i] = reinterpret_cast<const uint4*>(a.vc + row * D)[vd];
+        }
+#pragma unroll
+        for (int i = 0; i < ATT_VR; i++) {
+            const int r = min(vrow + 16 * i, L.KQ - 1);
+            *reinterpret_cast<uint4*>(ks + r * ATT_RS + 8 * vd) = kv[i];
+            *reinterpret_cast<uint4*>(vs + r * 256 + 16 * (vd ^ (r & 15))) = vv[i];
+        }
+    }
+    __syncthreads();
+    // scores S^T: tile (kt, rt) = keys 16 kt.., rows 16 rt..; lane: keys 16 kt + 4 l4 + i, row l16
+    for (int tI = wave; tI < nrt * nkt; tI += 4) {
+        const int rt = tI % nrt, kt = tI / nrt;
+        if (rt != cur_rt) { cur_rt = rt; load_q(rt); }
+        const uint16_t* ka = ks + (16 * kt + l16) * ATT_RS + 8 * l4;
+        uint4 av[4];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; s4++) av[s4] = *reinterpret_cast<const uint4*>(ka + 32 * s4);
+        f32x4_att s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s4 = 0; s4 < 4; s4++) { s0 = att_mfma(av[s4], bh[s4], s0); s1 = att_mfma(av[s4], bl[s4], s1); }
+        const int r = 16 * rt + l16, key = 16 * kt + 4 * l4;
+        if (r < GT) *reinterpret_cast<float4*>(sc + r * L.scs + key) = float4{s0[0] + s1[0], s0[1] + s1[1], s0[2] + s1[2], s0[3] + s1[3]};
+    }
+    __syncthreads();
+    // per-row max and exp over the row's own keys (n0 .. min(n1, *dpos + t + 1)), lane: keys 2 lane,
+    // 2 lane + 1 (nkq <= 128); p as three bf16 terms over the dead K image, zeros up to the 32-key
+    // step edge. Padded rows stay as they are: an MFMA output row reads only its own A row.
+    for (int r = wave; r < GT; r += 4) {
+        const int nv = max(0, min(nk, pos0 + r / G + 1 - n0));
+        const int k2 = 2 * lane;
+        const float2 v = k2 < nkq ? *reinterpret_cast<const float2*>(sc + r * L.scs + k2) : float2{0.0f, 0.0f};
+        float m = fmaxf(k2 < nv ? v.x : -1e30f, k2 + 1 < nv ? v.y : -1e30f);
+        m = wave_max(m);
+        const float p0 = k2 < nv ? expf(v.x - m) : 0.0f, p1 = k2 + 1 < nv ? expf(v.y - m) : 0.0f;
+        const float l = wave_sum(p0 + p1);
+        if (k2 < nkq) {
+            const uint32_t h = att_pk(p0, p1);
+            const float r0 = p0 - __uint_as_float(h << 16), r1 = p1 - __uint_as_float(h & 0xffff0000u);
+            const uint32_t md = att_pk(r0, r1);
+            const uint32_t lo = att_pk(r0 - __uint_as_float(md << 16), r1 - __uint_as_float(md & 0xffff0000u));
+            *reinterpret_cast<uint32_t*>(pb + r * L.PS + k2) = h;
+            *reinterpret_cast<uint32_t*>(pb + (GP + r) * L.PS + k2) = md;
+            *reinterpret_cast<uint32_t*>(pb + (2 * GP + r) * L.PS + k2) = lo;
+        }
+        if (lane == 0) { mx[r] = nv > 0 ? m : -1e30f; lsum[r] = l; }
+    }
+    __syncthreads();
+    // O = P V: tile (rt, dt) = rows 16 rt.., dims 16 dt..; lane: row 16 rt + 4 l4 + i, dim 16 dt + l16
+    for (int tI = wave; tI < nrt * (ATT_D / 16); tI += 4) {
+        const int rt = tI >> 3, dt = tI & 7;
+        // k-slots of a 32-key step: 0..3 = keys 4 l4 + (0..3), 4..7 = keys 16 + 4 l4 + (0..3) (the
+        // transpose read's order), P read to match
+        const uint16_t* p0 = pb + (16 * rt + l16) * L.PS + 4 * l4;
+        const int c = 2 * dt + ((l16 & 3) >> 1);
+        f32x4_att o0 = {0.0f, 0.0f, 0.0f, 0.0f}, o1 = {0.0f, 0.0f, 0.0f, 0.0f}, o2 = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < nkq; k += 32) {
+            att_v4s vv[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int key = k + 16 * h + 4 * l4 + (l16 >> 2);
+                vv[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((att_lv4)(vs + key * 256 + 16 * (c ^ (key & 15)) + 8 * (l16 & 1)));
+            }
+            const uint4 bv = __builtin_bit_cast(uint4, __builtin_shufflevector(vv[0], vv[1], 0, 1, 2, 3, 4, 5, 6, 7));
+            uint4 pt3[3];
+#pragma unroll
+            for (int tm = 0; tm < 3; tm++) {
+                const uint2 x0 = *reinterpret_cast<const uint2*>(p0 + tm * GP * L.PS + k);
+                const uint2 x1 = *reinterpret_cast<const uint2*>(p0 + tm * GP * L.PS + k + 16);
+                pt3[tm] = uint4{x0.x, x0.y, x1.x, x1.y};
+            }
+            o0 = att_mfma(pt3[0], bv, o0); o1 = att_mfma(pt3[1], bv, o1); o2 = att_mfma(pt3[2], bv, o2);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 16 * rt + 4 * l4 + i;
+            if (r >= GT) break;
+            const int2 o = ro[r];
+            const int rr = o.y;
+            float* pt_ = a.part + o.x;
+            const bool any = mx[r] > -1e30f;
+            pt_[2 * rows + (int64_t)rr * D + 16 * dt + l16] = any ? (o0[i] + o1[i]) + o2[i] : 0.0f;
+            if (dt == 0 && l16 == 0) { pt_[rr] = mx[r]; pt_[rows + rr] = any ? lsum[r] : 0.0f; }
+        }
+    }
+}
+
+hipError_t launch_attn_verify(const AttnArgs& a, hipStream_t s) {
+    const int G = a.D == ATT_D && a.nKV > 0 && a.nH % a.nKV == 0 ? a.nH / a.nKV : 0, GT = G * a.T;
+    if (G == 0 || a.T < 2 || GT > 64 || a.nsplit < 1 || a.nsplit > ATT_MAXS || a.lists || a.cap < 1 || a.cap > ATT_MC)
+        return hipErrorInvalidValue;
+    const AttMultiLds L(GT, a.cap);
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute((const void*)attn_multi_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+            return hipErrorInvalidValue;
+        attr = true;
+    }
+    if (L.bytes > 160 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attn_multi_kernel, dim3(a.nKV, a.nsplit), dim3(256), L.bytes, s, a);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nH, a.T), dim3(ATT_D), 0, s, a);
+    return hipGetLastError();
+}
+
 static hipError_t attn_launch(const AttnArgs& a, const SparsePlanDev* plan, hipStream_t s) {
     if (a.D != ATT_D || a.nH % a.nKV || a.nH / a.nKV > ATT_MAXG || a.nsplit < 1 || a.nsplit > ATT_MAXS) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attn_split_kernel, dim3(a.nKV * a.T, a.nsplit), dim3(256), 0, s, a, plan);

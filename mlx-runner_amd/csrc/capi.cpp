@@ -380,7 +380,10 @@ int mlxr_k_attention(const float* q, int q_stride, const void* kcache, const voi
     if (lists && (T != 1 || count < 1 || count > max_seq || list_stride < 0)) return set_error(MLXR_E_INVALID_ARG, "sparse lists: T 1, count");
     const int maxCount = lists ? count : offset + T;
     if (nsplit <= 0) nsplit = 32;
-    if ((maxCount + nsplit - 1) / nsplit > 512) nsplit = (maxCount + 511) / 512;
+    // several dense queries share each key range (the verify batch's kernel: 128 keys per range at most)
+    const bool multi = !lists && T > 1 && (nH / nKV) * T <= 64 && q_stride % 4 == 0;
+    const int per = multi ? 128 : 512;
+    if ((maxCount + nsplit - 1) / nsplit > per) nsplit = (maxCount + per - 1) / per;
     if (int rc = ensure_pt(max_seq)) return rc;
     if (int rc = ensure_buf(g_part, g_part_floats, (size_t)T * nH * nsplit * (D + 2))) return rc;
     if (int rc = set_pos(offset)) return rc;
@@ -394,7 +397,8 @@ int mlxr_k_attention(const float* q, int q_stride, const void* kcache, const voi
     AttnArgs a; a.q = q; a.q_stride = q_stride; a.kc = (const uint16_t*)kcache; a.vc = (const uint16_t*)vcache; a.pt = g_pt;
     a.out = out; a.out_stride = out_stride; a.part = g_part; a.D = D; a.nH = nH; a.nKV = nKV; a.T = T; a.nsplit = nsplit;
     a.dpos = g_pos; a.scale = scale; a.lists = lists; a.list_stride = list_stride; a.splan = plan;
-    return done(launch_attn_decode(a, g_stream));
+    a.cap = (maxCount + nsplit - 1) / nsplit;
+    return done(multi ? launch_attn_verify(a, g_stream) : launch_attn_decode(a, g_stream));
 }
 
 int mlxr_k_flash_prefill(const float* q, int q_stride, const void* kcache, const void* vcache, int max_seq, int D, int nH, int nKV,

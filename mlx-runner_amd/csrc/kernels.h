@@ -106,8 +106,12 @@ struct AttnArgs {
     float scale = 1.0f;
     const int* lists = nullptr; int list_stride = 0;
     const int* splan = nullptr;                   // sparse plan (device, written by launch_sparse_plan)
+    int cap = 0;                                  // verify batch: keys per range (max), >= ceil((*dpos + T) / nsplit), <= 128
 };
 hipError_t launch_attn_decode(const AttnArgs& a, hipStream_t s);
+// Verify batch (T = 2..8, G T <= 64, dense keys): one workgroup per (KV head, key range) for all T
+// queries, each masked at its own position; a.cap >= ceil((*dpos + T) / nsplit), at most 128.
+hipError_t launch_attn_verify(const AttnArgs& a, hipStream_t s);
 
 // Causal prefill attention (flash, bf16 MFMA for QK^T and PV) over the cache (queries at
 // positions *dpos + t for t < T, keys 0..pos).

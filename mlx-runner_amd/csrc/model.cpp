@@ -572,7 +572,9 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
     const int B = m->max_batch, H = c.H, I = c.I, V = c.V;
     m->qkv_cols = (c.nH + 2 * c.nKV) * c.D;
     m->nsplit_dec = std::max((seq + 511) / 512, std::min(64, (512 + c.nKV - 1) / c.nKV));
-    const size_t partFloats = (size_t)8 * c.nH * m->nsplit_dec * (c.D + 2);   // split-attention partials (T <= 8)
+    // verify batches: key ranges of at most 128 keys for the multi-query kernel
+    m->nsplit_ver = std::max(m->nsplit_dec, (seq + 127) / 128);
+    const size_t partFloats = (size_t)8 * c.nH * m->nsplit_ver * (c.D + 2);   // split-attention partials (T <= 8)
     int Kmax = std::max(c.I, std::max(c.H, c.nH * c.D));
     int rc;
     if ((rc = dalloc(m, &m->hist, seq + 1)) || (rc = dalloc(m, &m->status, seq + 1)) || (rc = dalloc(m, &m->rng, 2)) ||
@@ -748,8 +750,8 @@ int project_tiles(Model* m, const MvPhaseDesc& p, const float* x, int xs, float*
 }
 
 // Attention of a batch's T queries (positions *dpos .. *dpos + T - 1) after their q|k|v: QK norms,
-// RoPE and the cache write, then flash attention (prefill chunks) or the decode attention per
-// query (verify batches, T <= 8).
+// RoPE and the cache write, then flash attention (prefill chunks) or the split attention (verify
+// batches, T <= 8).
 int attend(Model* m, int li, int T) {
     const Config& c = m->cfg;
     hipStream_t s = m->stream;
@@ -765,11 +767,12 @@ int attend(Model* m, int li, int T) {
         fa.out = m->attn; fa.out_stride = c.nH * c.D; fa.D = c.D; fa.nH = c.nH; fa.nKV = c.nKV; fa.T = T;
         fa.dpos = m->dpos; fa.scale = scale;
         HIPCHECK(launch_flash_prefill(fa, s));
-    } else {       // verify batch: the decode attention per query
+    } else {       // verify batch: every query of a KV head in one pass over each key range
         AttnArgs aa; aa.q = m->qkv; aa.q_stride = m->qkv_cols; aa.kc = ly.kc; aa.vc = ly.vc; aa.pt = m->page_table;
         aa.out = m->attn; aa.out_stride = c.nH * c.D; aa.part = m->part; aa.D = c.D; aa.nH = c.nH; aa.nKV = c.nKV; aa.T = T;
-        aa.nsplit = m->nsplit_dec; aa.dpos = m->dpos; aa.scale = scale;
-        HIPCHECK(launch_attn_decode(aa, s));
+        aa.nsplit = T > 1 ? m->nsplit_ver : m->nsplit_dec; aa.dpos = m->dpos; aa.scale = scale;
+        aa.cap = (m->max_seq + aa.nsplit - 1) / aa.nsplit;   // positions stay below the context length
+        HIPCHECK(T > 1 ? launch_attn_verify(aa, s) : launch_attn_decode(aa, s));
     }
     return MLXR_OK;
 }

@@ -83,7 +83,7 @@ struct Model {
     static constexpr int RING = 64;
 
     hipStream_t stream = nullptr;
-    int qkv_cols = 0, nsplit_dec = 32;
+    int qkv_cols = 0, nsplit_dec = 32, nsplit_ver = 32;
     int max_batch = MLXR_PREFILL_CHUNK;                // prefill chunk (tokens per batched pass)
     int dev_pos_known = -1;              // value *dpos will hold once queued work completes
     int written_high = 0;

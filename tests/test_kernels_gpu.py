@@ -533,6 +533,28 @@ def test_attention_decode_and_split(gpu, nH, nKV):
     del rng
 
 
+@pytest.mark.parametrize("nH,nKV,offset,T,nsplit", [(32, 8, 700, 8, 3), (40, 8, 300, 8, 1), (4, 2, 100, 5, 64),
+                                                   (8, 1, 37, 2, 32), (64, 8, 511, 8, 5)])
+def test_attention_verify_batch(gpu, nH, nKV, offset, T, nsplit):
+    """The verify batch's attention (attention_split + attention_combine per query, Kernels.swift:
+    1317-1374): the T queries of a KV head share one pass over each key range, query t masked past
+    its own position offset + t. Every query against the reference attention at its position; keys
+    past the batch's last position are NaN (never read); ranges past a query's position (nsplit 64
+    over 105 keys), ranges raised to 256 keys at most (nsplit 1 over 308 keys), and G T up to 64."""
+    D, S = 128, 1024
+    kc = bf16_to_f32(bf16_round(np.random.default_rng(nH + T).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
+    vc = bf16_to_f32(bf16_round(np.random.default_rng(nH + T + 1).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
+    kc[:, offset + T:] = np.nan
+    vc[:, offset + T:] = np.nan
+    q = np.random.default_rng(nH + T + 2).uniform(-1, 1, (T, nH, D)).astype(np.float32)
+    scale = 3 / np.sqrt(D)
+    got = run_attention(gpu, q, kc, vc, nH, nKV, offset, T, scale, nsplit=nsplit)
+    assert np.all(np.isfinite(got))
+    kref, vref = np.nan_to_num(kc), np.nan_to_num(vc)
+    for t in range(T):
+        assert max_rel_err(got[t], oracle.attention(q[t], kref, vref, nH, nKV, offset + t, scale)) < 2e-5, t
+
+
 def run_flash(mlxr, q, kc, vc, nH, nKV, offset, T, scale):
     D = q.shape[-1]
     S = kc.shape[1]
