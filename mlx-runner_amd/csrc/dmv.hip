@@ -222,8 +222,14 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc 
 // slices' partial rows summed in slice order by the tile's last workgroup (per-tile counters), so
 // the result does not depend on arrival order.
 constexpr int DMM_TOK = 8;
+// f(std::integral_constant<int, I>) for I = B .. E - 1, in order
+template <int B, int E> struct StaticFor {
+    template <typename F> __device__ __forceinline__ static void run(F& f) {
+        if constexpr (B < E) { f(std::integral_constant<int, B>{}); StaticFor<B + 1, E>::run(f); }
+    }
+};
 constexpr int DMM_MAX_S = 8;                               // input slices (max)
-constexpr int DMM_XR = 2;                                  // 8-groups of x per thread and token (slices of <= 8192 values)
+constexpr int DMM_XR = 2;                                  // 8-groups of x per thread and token (max: slices of <= 8192 values)
 constexpr int DMM_SLOTS = MK_WAVES * 2 * 16 * DMM_TOK;     // floats: each wave's first and last tile rows, when shared
 constexpr int DMM_RED = 2 * MK_WAVES * DMM_TOK + DMM_TOK;  // per-wave max |x w| and sum of squares per token; unscales
 
@@ -284,19 +290,22 @@ __device__ __forceinline__ void mvt_run(const MvPhase p, const float* xh, int im
         // each group: hi + lo columns, then scale * D + bias * Xs with the group's word for this
         // lane's rows (held by the scale block's lane of column gl in the same row quarter)
         const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
-#pragma unroll
-        for (int gl = 0; gl < 16; gl++) {
+        // group gl (a compile-time constant: it selects the lane move)
+        auto group = [&](auto glc) {
+            constexpr int gl = decltype(glc)::value;
             const int gi = 16 * f + gl;
             const bool real = gi < gpr;
             const float xs = gs_t[real ? gi : 0];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float v = acc[gl][r] + __shfl_xor(acc[gl][r], 8, 64);
-                const uint32_t w = __shfl(sv[r], (lane & 0x30) | gl, 64);
+                // hi + lo columns (lane c ^ 8: row rotation by 8), the word of lane gl of this row
+                const float v = acc[gl][r] + dpp<0x128>(acc[gl][r]);
+                const uint32_t w = __float_as_uint(dpp<0x150 + gl>(__uint_as_float(sv[r])));
                 const float sc = __uint_as_float(w << 16) * 16777216.0f, bb = __uint_as_float(w & 0xffff0000u);
                 run[r] += real ? sc * v + bb * xs : 0.0f;
             }
-        }
+        };
+        StaticFor<0, 16>::run(group);
         if (f == g.NF - 1 || i == nfb - 1) {     // tile done (or the wave's range)
             if (fresh && f == g.NF - 1) {
                 emit(tile, run);
@@ -312,7 +321,8 @@ __device__ __forceinline__ void mvt_run(const MvPhase p, const float* xh, int im
 }
 
 // grid (workgroups, S). Slice blockIdx.y of every tile: scale groups [NF y / S, NF (y + 1) / S).
-template <int FB, bool TS>
+// XR: 8-groups of x per thread and token (1: slices of <= 4096 values, half the registers).
+template <int FB, bool TS, int XR>
 __global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MmArgs a) {
     constexpr int GSH = FB == 4 ? 5 : 6;
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -336,33 +346,46 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MmArgs a) {
     // every token's slice of x (8-groups t = tid + MK_THREADS i) and the norm weights into registers,
     // then the weights' first scale group: the memory counter completes in order, so the statistics
     // wait for x alone while the weights stream in behind
-    float4 xv[DMM_TOK][DMM_XR][2], wv[DMM_XR][2];
+    float4 xv[DMM_TOK][XR][2], wv[XR][2];
 #pragma unroll
-    for (int i = 0; i < DMM_XR; i++) {
+    for (int i = 0; i < XR; i++) {
         const int t = threadIdx.x + i * MK_THREADS;
         const bool in = 8 * t < Ks;
-        wv[i][0] = wv[i][1] = float4{1.0f, 1.0f, 1.0f, 1.0f};
-        if (a.nw && in) { wv[i][0] = gf4(a.nw + k0 + 8 * t); wv[i][1] = gf4(a.nw + k0 + 8 * t + 4); }
+        {   // unconditional too (without a norm: a load of x, replaced by ones)
+            const float* wp = (a.nw ? a.nw : a.x) + k0 + 8 * (in ? t : 0);
+            const float4 w0 = gf4(wp), w1 = gf4(wp + 4), one = float4{1.0f, 1.0f, 1.0f, 1.0f};
+            wv[i][0] = a.nw ? w0 : one; wv[i][1] = a.nw ? w1 : one;
+        }
+        // unconditional loads (tokens and 8-groups past the input clamped to the last ones): the
+        // waits before their uses then count exactly the loads behind them (the weights' ring),
+        // where a conditional load would make them wait for everything
 #pragma unroll
         for (int tk = 0; tk < DMM_TOK; tk++) {
-            xv[tk][i][0] = xv[tk][i][1] = float4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (tk < nt && in) {
-                const float* xt = a.x + (int64_t)(a.t0 + tk) * a.xs + k0 + 8 * t;
-                xv[tk][i][0] = gf4(xt); xv[tk][i][1] = gf4(xt + 4);
-            }
+            const float* xt = a.x + (int64_t)(a.t0 + min(tk, nt - 1)) * a.xs + k0 + 8 * (in ? t : 0);
+            xv[tk][i][0] = gf4(xt); xv[tk][i][1] = gf4(xt + 4);
         }
     }
     Ring<FB> ring;
-    mv_prefetch<FB, TS>(q, wg, nwg, wave, lane, ring);
+    __builtin_amdgcn_sched_barrier(0);   // the weights' loads stay behind every x load
+    {   // the first scale group, unconditionally (a wave without one reads its workgroup's last,
+        // unused): a load in a branch would make every later wait count from zero
+        MvGeom<FB> g = mv_geom<FB>(q, wg, nwg, wave);
+        const int nfw = g.nt * g.NF;
+        g.f0 = max(0, min(g.f0, nfw - 1));
+        const gptr8 b = mv_base<FB, TS>(q, g, lane);
+#pragma unroll
+        for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
+    }
 #pragma unroll
     for (int tk = 0; tk < DMM_TOK; tk++) {
         if (tk >= nt) break;
         float ss = 0.0f, mx = 0.0f;
 #pragma unroll
-        for (int i = 0; i < DMM_XR; i++)
+        for (int i = 0; i < XR; i++)
 #pragma unroll
             for (int c = 0; c < 2; c++) {
-                const float4 v = xv[tk][i][c], w = wv[i][c];
+                const bool in = 8 * ((int)threadIdx.x + i * MK_THREADS) < Ks;   // past the input: a copy, not counted
+                const float4 v = in ? xv[tk][i][c] : float4{0.0f, 0.0f, 0.0f, 0.0f}, w = wv[i][c];
                 ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
                 const float4 u = float4{v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w};
                 mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
@@ -381,15 +404,23 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MmArgs a) {
     lds_barrier();
     MvLds L;
     L.xf = nullptr; L.hown = nullptr; L.part = nullptr; L.zero16 = zero;
+    // every token's statistics read before any packing writes LDS (the reads could not pass those
+    // writes, which would chain the tokens one after another)
+    float tinv[DMM_TOK], tmax[DMM_TOK];
+#pragma unroll
+    for (int tk = 0; tk < DMM_TOK; tk++) {
+        float tot = 0.0f, gmax = 0.0f;
+        for (int w = 0; w < MK_WAVES; w++) { tot += red[(MK_WAVES + w) * DMM_TOK + tk]; gmax = fmaxf(gmax, red[w * DMM_TOK + tk]); }
+        tinv[tk] = a.nw ? 1.0f / sqrtf(tot / (float)p.K + a.eps) : 1.0f;
+        tmax[tk] = gmax;
+    }
 #pragma unroll
     for (int tk = 0; tk < DMM_TOK; tk++) {
         if (tk >= nt) break;
-        float tot = 0.0f, gmax = 0.0f;
-        for (int w = 0; w < MK_WAVES; w++) { tot += red[(MK_WAVES + w) * DMM_TOK + tk]; gmax = fmaxf(gmax, red[w * DMM_TOK + tk]); }
-        const float inv = a.nw ? 1.0f / sqrtf(tot / (float)p.K + a.eps) : 1.0f;
+        const float inv = tinv[tk], gmax = tmax[tk];
         if (a.nw) {
 #pragma unroll
-            for (int i = 0; i < DMM_XR; i++)
+            for (int i = 0; i < XR; i++)
 #pragma unroll
                 for (int c = 0; c < 2; c++) {
                     float4& v = xv[tk][i][c];
@@ -400,9 +431,9 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MmArgs a) {
         L.xh = xh + (size_t)tk * img; L.gsum = gsum + (size_t)tk * gstride;
         // the packing visits t = tid + MK_THREADS i in order of i
         auto ld = [&](int t, float4& lo, float4& hi) {
-            const bool second = DMM_XR > 1 && t >= MK_THREADS;
-            lo = second ? xv[tk][DMM_XR - 1][0] : xv[tk][0][0];
-            hi = second ? xv[tk][DMM_XR - 1][1] : xv[tk][0][1];
+            const bool second = XR > 1 && t >= MK_THREADS;
+            lo = second ? xv[tk][XR - 1][0] : xv[tk][0][0];
+            hi = second ? xv[tk][XR - 1][1] : xv[tk][0][1];
         };
         const float us = pack_x16_from<decltype(ld), false>(ld, Ks, gmax * inv, L, GSH);
         if (threadIdx.x == 0) red[2 * MK_WAVES * DMM_TOK + tk] = us;
@@ -622,8 +653,10 @@ hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, const f
     }
     static bool attr = false;
     if (!attr) {
-        for (const void* f : {(const void*)dpack_mm_kernel<4, false>, (const void*)dpack_mm_kernel<8, false>,
-                              (const void*)dpack_mm_kernel<4, true>, (const void*)dpack_mm_kernel<8, true>})
+        for (const void* f : {(const void*)dpack_mm_kernel<4, false, 1>, (const void*)dpack_mm_kernel<8, false, 1>,
+                              (const void*)dpack_mm_kernel<4, true, 1>, (const void*)dpack_mm_kernel<8, true, 1>,
+                              (const void*)dpack_mm_kernel<4, false, 2>, (const void*)dpack_mm_kernel<8, false, 2>,
+                              (const void*)dpack_mm_kernel<4, true, 2>, (const void*)dpack_mm_kernel<8, true, 2>})
             if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, DMV_MAX_LDS) != hipSuccess) return hipErrorInvalidValue;
         attr = true;
     }
@@ -638,13 +671,19 @@ hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, const f
     a.cnt = reinterpret_cast<unsigned*>(split); a.part = split ? split + tiles_al : nullptr;
     // one workgroup per CU over all slices (the images fill most of the LDS)
     const int nwg = std::min(p.tiles, std::max(1, cus / S));
-    const bool fb4 = p.gs == 32;
-    if (S == 1) {
-        if (fb4) hipLaunchKernelGGL((dpack_mm_kernel<4, false>), dim3(nwg), dim3(MK_THREADS), lds, s, a);
-        else hipLaunchKernelGGL((dpack_mm_kernel<8, false>), dim3(nwg), dim3(MK_THREADS), lds, s, a);
+    // the longest slice decides how many 8-groups of x each thread holds
+    const int FBv = p.gs >> 3, NF = ((p.K >> 7) + FBv - 1) / FBv;
+    int ks = 0;
+    for (int sl = 0; sl < S; sl++) ks = std::max(ks, std::min(NF * (sl + 1) / S * FBv * 128, p.K) - NF * sl / S * FBv * 128);
+    const bool xr1 = ks <= 8 * MK_THREADS;
+    const dim3 grid(nwg, S);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(MK_THREADS), lds, s, a); };
+    if (p.gs == 32) {
+        if (S == 1) xr1 ? go(dpack_mm_kernel<4, false, 1>) : go(dpack_mm_kernel<4, false, 2>);
+        else xr1 ? go(dpack_mm_kernel<4, true, 1>) : go(dpack_mm_kernel<4, true, 2>);
     } else {
-        if (fb4) hipLaunchKernelGGL((dpack_mm_kernel<4, true>), dim3(nwg, S), dim3(MK_THREADS), lds, s, a);
-        else hipLaunchKernelGGL((dpack_mm_kernel<8, true>), dim3(nwg, S), dim3(MK_THREADS), lds, s, a);
+        if (S == 1) xr1 ? go(dpack_mm_kernel<8, false, 1>) : go(dpack_mm_kernel<8, false, 2>);
+        else xr1 ? go(dpack_mm_kernel<8, true, 1>) : go(dpack_mm_kernel<8, true, 2>);
     }
     return hipGetLastError();
 }

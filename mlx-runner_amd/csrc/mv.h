@@ -163,9 +163,11 @@ __device__ __forceinline__ float pack_x16_from(const LD& ld, int K, float gmax, 
         *reinterpret_cast<uint4*>(xh + c * XH_STRIDE + XH_LO + (t & 3) * 4) = ol;
         // Xs of the quantization group: the 4 (gs 32) or 8 (gs 64) t of a group sit in consecutive
         // lanes of one wave (K is a multiple of 128, so whole groups are active)
+        // (lane moves within rows of 16: quad swaps, then the half-row mirror, whose partner 7 - i
+        // holds the same quad sum as i ^ 4)
         float xsum = ((lo.x + lo.y) + (lo.z + lo.w) + ((hi.x + hi.y) + (hi.z + hi.w))) * up;
-        xsum += __shfl_xor(xsum, 1, 64); xsum += __shfl_xor(xsum, 2, 64);
-        if (gsh == 6) xsum += __shfl_xor(xsum, 4, 64);
+        xsum = quad_sum(xsum);
+        if (gsh == 6) xsum += dpp<0x141>(xsum);
         if ((t & ((1 << (gsh - 3)) - 1)) == 0) gsum[t >> (gsh - 3)] = xsum;
     }
     if constexpr (BAR) lds_barrier();
