@@ -376,9 +376,10 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MmArgs a) {
 #pragma unroll
         for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
     }
+    // every token slot's statistics without a branch (slots past nt hold copies of the last
+    // token), so the 16 reductions interleave
 #pragma unroll
     for (int tk = 0; tk < DMM_TOK; tk++) {
-        if (tk >= nt) break;
         float ss = 0.0f, mx = 0.0f;
 #pragma unroll
         for (int i = 0; i < XR; i++)
@@ -404,20 +405,21 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MmArgs a) {
     lds_barrier();
     MvLds L;
     L.xf = nullptr; L.hown = nullptr; L.part = nullptr; L.zero16 = zero;
-    // every token's statistics read before any packing writes LDS (the reads could not pass those
-    // writes, which would chain the tokens one after another)
-    float tinv[DMM_TOK], tmax[DMM_TOK];
-#pragma unroll
-    for (int tk = 0; tk < DMM_TOK; tk++) {
+    // every token's norm scale and max, lane tk for token tk (one chain for all tokens), read
+    // before any packing writes LDS (reads could not pass those writes)
+    float linv, lmax;
+    {
+        const int tk = lane & (DMM_TOK - 1);
         float tot = 0.0f, gmax = 0.0f;
         for (int w = 0; w < MK_WAVES; w++) { tot += red[(MK_WAVES + w) * DMM_TOK + tk]; gmax = fmaxf(gmax, red[w * DMM_TOK + tk]); }
-        tinv[tk] = a.nw ? 1.0f / sqrtf(tot / (float)p.K + a.eps) : 1.0f;
-        tmax[tk] = gmax;
+        linv = a.nw ? 1.0f / sqrtf(tot / (float)p.K + a.eps) : 1.0f;
+        lmax = gmax;
     }
 #pragma unroll
     for (int tk = 0; tk < DMM_TOK; tk++) {
         if (tk >= nt) break;
-        const float inv = tinv[tk], gmax = tmax[tk];
+        const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(linv), tk));
+        const float gmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lmax), tk));
         if (a.nw) {
 #pragma unroll
             for (int i = 0; i < XR; i++)
