@@ -367,15 +367,7 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MmArgs a) {
     }
     Ring<FB> ring;
     __builtin_amdgcn_sched_barrier(0);   // the weights' loads stay behind every x load
-    {   // the first scale group, unconditionally (a wave without one reads its workgroup's last,
-        // unused): a load in a branch would make every later wait count from zero
-        MvGeom<FB> g = mv_geom<FB>(q, wg, nwg, wave);
-        const int nfw = g.nt * g.NF;
-        g.f0 = max(0, min(g.f0, nfw - 1));
-        const gptr8 b = mv_base<FB, TS>(q, g, lane);
-#pragma unroll
-        for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
-    }
+    mv_prefetch_all<FB, TS>(q, wg, nwg, wave, lane, ring);
     // every token slot's statistics without a branch (slots past nt hold copies of the last
     // token), so the 16 reductions interleave
 #pragma unroll

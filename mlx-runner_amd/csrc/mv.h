@@ -99,6 +99,19 @@ __device__ __forceinline__ void mv_prefetch(const MvPhase p, int wg, int nwg, in
     for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
 }
 
+// mv_prefetch without a branch: a wave without scale groups reads its workgroup's last one, unused
+// (the workgroup has at least one tile). Loads issued in a branch make every later wait on the
+// memory counter count from zero, so a kernel that issues x before the weights and waits for x
+// alone needs the weights' loads unconditional.
+template <int FB, bool TS = false>
+__device__ __forceinline__ void mv_prefetch_all(const MvPhase p, int wg, int nwg, int wave, int lane, Ring<FB>& ring) {
+    MvGeom<FB> g = mv_geom<FB>(p, wg, nwg, wave);
+    g.f0 = max(0, min(g.f0, g.nt * g.NF - 1));
+    const gptr8 b = mv_base<FB, TS>(p, g, lane);
+#pragma unroll
+    for (int d = 0; d <= FB; d++) ring.u[d] = ld_stream16(b + d * 1024);
+}
+
 // A operand of one code dword: halves (n0, n4, 16 n1, 16 n5, n2, n6, 16 n3, 16 n7) * 2^-24 (subnormal).
 // No inline assembly here: the compiler must see every VGPR write that feeds an MFMA operand to
 // insert the wait states the matrix core requires.
