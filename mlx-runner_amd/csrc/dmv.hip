@@ -259,7 +259,9 @@ __device__ __forceinline__ void mvt_run(const MvPhase p, const float* xh, int im
     // slots, slot kq of each chunk
     const float* xb = xh + (tok < nt ? tok : 0) * img + kq * 4 + (col >= 8 ? XH_LO : 0);
     const float* gs_t = gsum + (tok < nt ? tok : 0) * gstride;
-    f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f};
+    // run: the tile rows' code sums, scale * D per column (hi and lo columns added at the tile's
+    // end, the codes' 2^24 too); runb: bias * Xs, hi columns only (xs is zero on the lo lanes)
+    f32x4_t run = {0.0f, 0.0f, 0.0f, 0.0f}, runb = {0.0f, 0.0f, 0.0f, 0.0f};
     int tile = g.f0 / g.NF, f = g.f0 - tile * g.NF;
     const int first = tile;
     bool fresh = f == 0;                 // the wave holds the tile from its first scale group
@@ -287,26 +289,37 @@ __device__ __forceinline__ void mvt_run(const MvPhase p, const float* xh, int im
             }
             if (more) ring.u[k + 1] = ld_stream16(nxt + (k + 1) * 1024);
         }
-        // each group: hi + lo columns, then scale * D + bias * Xs with the group's word for this
-        // lane's rows (held by the scale block's lane of column gl in the same row quarter)
+        // each group: scale * D + bias * Xs with the group's word for this lane's rows (held by the
+        // scale block's lane of column gl in the same row quarter: a row broadcast)
         const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
-        // group gl (a compile-time constant: it selects the lane move)
-        auto group = [&](auto glc) {
-            constexpr int gl = decltype(glc)::value;
-            const int gi = 16 * f + gl;
-            const bool real = gi < gpr;
-            const float xs = gs_t[real ? gi : 0];
+        // (GUARD: the input's last scale group, some of whose groups lie past the input)
+        auto epilogue = [&](auto guard) {
+            constexpr bool GUARD = decltype(guard)::value;
+            auto group = [&](auto glc) {
+                constexpr int gl = decltype(glc)::value;
+                const int gi = 16 * f + gl;
+                const bool real = !GUARD || gi < gpr;
+                const float xs = col < 8 ? gs_t[real ? gi : 0] : 0.0f;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                // hi + lo columns (lane c ^ 8: row rotation by 8), the word of lane gl of this row
-                const float v = acc[gl][r] + dpp<0x128>(acc[gl][r]);
-                const uint32_t w = __float_as_uint(dpp<0x150 + gl>(__uint_as_float(sv[r])));
-                const float sc = __uint_as_float(w << 16) * 16777216.0f, bb = __uint_as_float(w & 0xffff0000u);
-                run[r] += real ? sc * v + bb * xs : 0.0f;
-            }
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t w = __float_as_uint(dpp<0x150 + gl>(__uint_as_float(sv[r])));
+                    const float a1 = fmaf(__uint_as_float(w << 16), acc[gl][r], run[r]);
+                    const float b1 = fmaf(__uint_as_float(w & 0xffff0000u), xs, runb[r]);
+                    // a group past the input: its products may be anything (0 * NaN is not 0)
+                    run[r] = GUARD && !real ? run[r] : a1;
+                    runb[r] = GUARD && !real ? runb[r] : b1;
+                }
+            };
+            StaticFor<0, 16>::run(group);
         };
-        StaticFor<0, 16>::run(group);
+        if (16 * f + 16 <= gpr) epilogue(std::false_type{});
+        else epilogue(std::true_type{});
         if (f == g.NF - 1 || i == nfb - 1) {     // tile done (or the wave's range)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {   // hi + lo columns (lane c ^ 8: row rotation by 8), codes' 2^24, bias
+                const float v = run[r] + dpp<0x128>(run[r]), b = runb[r] + dpp<0x128>(runb[r]);
+                run[r] = fmaf(v, 16777216.0f, b);
+            }
             if (fresh && f == g.NF - 1) {
                 emit(tile, run);
             } else if (col < DMM_TOK) {
@@ -314,7 +327,7 @@ __device__ __forceinline__ void mvt_run(const MvPhase p, const float* xh, int im
 #pragma unroll
                 for (int r = 0; r < 4; r++) slots[((wave * 2 + slot) * 16 + 4 * kq + r) * DMM_TOK + col] = run[r];
             }
-            run = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            run = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}; runb = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
         if (++f == g.NF) { f = 0; tile++; fresh = true; }
     }

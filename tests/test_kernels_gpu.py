@@ -228,10 +228,6 @@ def test_qmv_tiles_epilogues(gpu, gs):
         tiny = (h * 1e-20).astype(np.float32)   # scaled up by 2^e before rounding: no f16 underflow
         ref_tiny = np.concatenate([f.oracle(oracle).matmul_f64(tiny)[0] for f in fxs])
         assert max_rel_err(qmv_tiles(gpu, fxs, tiny) * 1e20, ref_tiny * 1e20) < TOL, K
-    # a single part of more tiles than four per workgroup (the lm_head: row chunks of its own)
-    f = QuantFixture(16 * 4 * 256 * 2 + 40, 256, 4, gs, seed=7, fast=True)
-    x = rng.normal(0, 1, (2, 256)).astype(np.float32)
-    assert max_rel_err(qmm_tiles(gpu, [f], x), f.oracle(oracle).matmul_f64(x)) < TOL
     K, I = 2048, 200
     g, u = (QuantFixture(I, K, 4, gs, seed=s, fast=True) for s in (5, 6))
     h = rng.normal(0, 1, K).astype(np.float32)
