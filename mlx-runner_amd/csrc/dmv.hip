@@ -627,24 +627,28 @@ hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* no
     }
 }
 
-// Input slices of a small-batch launch of nt tokens: the fewest whose longest slice fits the
-// registers' share and whose nt images fit in LDS (0: none); *lds = the launch's dynamic LDS.
+// Input slices of a small-batch launch of nt tokens: the fewest whose nt images fit in LDS and
+// whose longest slice fits one 8-group of x per thread (4096 values; the two-group variant needs
+// twice the registers and ran slower, measured: the 8B down projection at T = 5 as 2 x 6144 took
+// ~22 us), else the fewest that fit two; 0: none. *lds = the launch's dynamic LDS.
 static int mm_slices(const MvPhaseDesc& p, int nt, size_t* lds) {
     const int FB = p.gs >> 3, GSH = FB == 4 ? 5 : 6, NF = ((p.K >> 7) + FB - 1) / FB;
-    for (int S = 1; S <= DMM_MAX_S && S <= NF; S++) {
-        int ks = 0;
-        for (int sl = 0; sl < S; sl++)
-            ks = std::max(ks, std::min(NF * (sl + 1) / S * FB * 128, p.K) - NF * sl / S * FB * 128);
-        if (ks > DMM_XR * 8 * MK_THREADS) continue;
-        const size_t b = sizeof(float) * ((size_t)nt * (ks + (((ks >> GSH) + 3) & ~3)) + MV_ZERO + DMM_SLOTS + DMM_RED);
-        if (b <= (size_t)DMV_MAX_LDS) { *lds = b; return S; }
-    }
+    for (int xr = 1; xr <= DMM_XR; xr++)
+        for (int S = 1; S <= DMM_MAX_S && S <= NF; S++) {
+            int ks = 0;
+            for (int sl = 0; sl < S; sl++)
+                ks = std::max(ks, std::min(NF * (sl + 1) / S * FB * 128, p.K) - NF * sl / S * FB * 128);
+            if (ks > xr * 8 * MK_THREADS) continue;
+            const size_t b = sizeof(float) * ((size_t)nt * (ks + (((ks >> GSH) + 3) & ~3)) + MV_ZERO + DMM_SLOTS + DMM_RED);
+            if (b <= (size_t)DMV_MAX_LDS) { *lds = b; return S; }
+        }
     return 0;
 }
 
 size_t dpack_mm_split_floats(const MvPhaseDesc& p) {
-    size_t lds = 0;
-    const int S = dpack_mv_supported(p) ? mm_slices(p, DMM_TOK, &lds) : 0;   // the most slices: at the most tokens
+    if (!dpack_mv_supported(p)) return 0;
+    int S = 1;
+    for (int nt = 1; nt <= DMM_TOK; nt++) { size_t lds = 0; S = std::max(S, mm_slices(p, nt, &lds)); }
     if (S <= 1) return 0;
     return (size_t)(p.tiles + 63) / 64 * 64 + (size_t)S * DMM_TOK * 16 * p.tiles;
 }
