@@ -7,7 +7,8 @@ the reference's pipelined loop does (step n+1 committed before step n is read ba
 bracketed by device synchronisation. value = decode tokens/s of the whole job (one GPU).
 `--mode small` runs configs[0] instead (Qwen3-0.6B shape, 32 + 64 tokens), `--mode prefill`
 configs[2] (Llama-3-8B shape, one 2048-token prefill per step), `--mode sweep` configs[3] (the
-matvec / GEMM sweep), `--mode long` configs[4] (Qwen2.5-32B shape, 32K context, sparse decode
+matvec / GEMM sweep), `--mode verify` the speculative verify pass (f3) on configs[1]'s model,
+`--mode long` configs[4] (Qwen2.5-32B shape, 32K context, sparse decode
 attention, reused prefix).
 
 Extra objects on the JSON line:
@@ -24,7 +25,9 @@ Extra objects on the JSON line:
   `--mode prefill`, `--mode sweep` and `--mode long` results,
   each with its own roofline, measured in the same run after the decode workload;
 - cpu_baseline: the CPU oracle (C restatement of the reference's semantics, all host cores) timed on
-  a bounded sample: decode steps at the same context, starting from the GPU-built KV cache.
+  a bounded sample: decode steps at the same context, starting from the GPU-built KV cache;
+- verify_f3: the speculative verify pass (T = 2 / 5 / 8 tokens, logits of every row) on the same
+  model after the decoded positions, and the tokens a pass must yield to beat plain decode steps.
 """
 import argparse
 import ctypes
@@ -245,6 +248,33 @@ def sweep_main(a):
     return result
 
 
+def verify_main(a):
+    """f3 alone: the speculative verify pass on configs[1]'s model after a `context`-token prefill
+    (T = 2 / 5 / 8 tokens, logits of every row; 3 warm-up + `steps` timed passes each)."""
+    d = model_dir(a.config, a.seed)
+    model = mlxr.Transformer(d, context_length=a.context + 16)
+    greedy = mlxr.SamplingParameters.greedy()
+    prompt = np.random.default_rng(a.seed).integers(0, model.vocab_size, a.context).astype(np.int32)
+    model.prefill(prompt, 0, greedy)
+    mlxr.synchronize()
+    ms = {}
+    for T in (2, 5, 8):
+        for _ in range(3):
+            model.forward(prompt[:T], a.context, all_logits=True)
+        mlxr.synchronize()
+        t = time.perf_counter()
+        for _ in range(a.steps):
+            model.forward(prompt[:T], a.context, all_logits=True)
+        mlxr.synchronize()
+        ms[T] = (time.perf_counter() - t) / a.steps * 1e3
+        log(f"[bench] verify T={T}: {ms[T]:.2f} ms")
+    model.close()
+    return {"metric": "speculative verify pass ms (T tokens, all logits)", "value": round(ms[5], 3), "unit": "ms",
+            "higher_is_better": False, "steps": a.steps,
+            "config": {"workload": f"{a.config}: T-token verify pass at context {a.context} (f3)"},
+            "T": list(ms), "ms": [round(v, 3) for v in ms.values()]}
+
+
 def long_main(a):
     """Qwen2.5-32B shape, 32768-token context with sparse decode attention. Turn 1
     prefills the first 30000 ids; turn 2 reuses that prefix (reusable_prefix), prefills the remaining
@@ -357,7 +387,7 @@ def main():
                     help="launch the kernel-per-op decode step kernel by kernel (profiling) instead of as a hipGraph")
     ap.add_argument("--decode-mode", type=int, default=1, choices=[0, 1, 2],
                     help="1: persistent decode step, 0: kernel per op (repacked tiles), 2: kernel per op (MLX layout)")
-    ap.add_argument("--mode", default="decode", choices=["decode", "small", "prefill", "sweep", "long"],
+    ap.add_argument("--mode", default="decode", choices=["decode", "small", "prefill", "sweep", "long", "verify"],
                     help="decode: configs[1] (default); small: configs[0] (qwen3-0.6b, 32 + 64 tokens); prefill: "
                          "configs[2] (llama3-8b, 2048 tokens unless given); sweep: configs[3]; long: configs[4] "
                          "(qwen2.5-32b, 32768-token context, sparse)")
@@ -393,6 +423,9 @@ def main():
         return
     if a.mode == "sweep":
         print(json.dumps(sweep_main(a)), flush=True)
+        return
+    if a.mode == "verify":
+        print(json.dumps(verify_main(a)), flush=True)
         return
     if a.mode == "small":
         if "--config" not in sys.argv:
@@ -501,6 +534,26 @@ def main():
     }
     if not a.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(d, model, cfg, pos + a.steps, a.cpu_tokens, a.cpu_budget)
+    # speculative verify (f3): one T-token pass with the logits of every row, after the decoded
+    # positions (their K/V rows are scratch past the measured context)
+    ver = {}
+    for T in (2, 5, 8):
+        vt = prompt[:T]
+        for _ in range(3):
+            model.forward(vt, pos + a.steps, all_logits=True)
+        mlxr.synchronize()
+        t = time.perf_counter()
+        for _ in range(10):
+            model.forward(vt, pos + a.steps, all_logits=True)
+        mlxr.synchronize()
+        ver[T] = (time.perf_counter() - t) / 10 * 1e3
+        log(f"[bench] verify T={T}: {ver[T]:.2f} ms")
+    step_ms_mean = el * 1e3 / a.steps
+    result["verify_f3"] = {
+        "workload": f"{a.config}: T-token batched pass (all logits) at context {pos + a.steps}, eager launches",
+        "T": list(ver), "ms": [round(v, 3) for v in ver.values()], "decode_step_ms": round(step_ms_mean, 4),
+        # a verify pass yields its accepted drafts plus one token: it pays from this many tokens per pass
+        "tokens_per_pass_to_break_even": {str(T): round(v / step_ms_mean, 2) for T, v in ver.items()}}
     model.close()
     if not a.no_extra:
         # the other workloads, measured in the same run (short: seconds of GPU time each)
