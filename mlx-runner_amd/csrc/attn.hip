@@ -208,13 +208,16 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a) {
     __syncthreads();
     float Ls = 0.0f, o = 0.0f;
     const float* acc = pt_ + 2 * rows + (int64_t)h * NS * D + d;
+    // 32 ranges' loads in flight per batch (each batch is a memory round trip: the partials come
+    // from other XCDs), summed in range order
+    constexpr int CB = 32;
     int s = 0;
-    for (; s + 8 <= NS; s += 8) {
-        float v[8], l[8];
+    for (; s + CB <= NS; s += CB) {
+        float v[CB], l[CB];
 #pragma unroll
-        for (int i = 0; i < 8; i++) { v[i] = acc[(int64_t)(s + i) * D]; l[i] = lrow[s + i]; }
+        for (int i = 0; i < CB; i++) { v[i] = acc[(int64_t)(s + i) * D]; l[i] = lrow[s + i]; }
 #pragma unroll
-        for (int i = 0; i < 8; i++) { Ls += l[i] * w[s + i]; o += v[i] * w[s + i]; }
+        for (int i = 0; i < CB; i++) { Ls += l[i] * w[s + i]; o += v[i] * w[s + i]; }
     }
     for (; s < NS; s++) { Ls += lrow[s] * w[s]; o += acc[(int64_t)s * D] * w[s]; }
     a.out[(int64_t)t * a.out_stride + (int64_t)h * D + d] = o / Ls;
