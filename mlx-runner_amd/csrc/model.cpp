@@ -893,11 +893,29 @@ void record_gpu_time(Model* m, const Model::StepSlot& s) {
 }
 }  // namespace
 
+static bool sparse_plan_valid(const mlxr_sparse_cfg& c, int position);
+
 int model_forward(Model* m, const int32_t* tokens, int n, int offset, bool all_logits, bool dense, const float** out, Cancel cancel) {
     if (n <= 0 || !tokens) return set_error(MLXR_E_INVALID_ARG, "no tokens");
     if (all_logits && n > 8) return set_error(MLXR_E_INVALID_OUTPUT, "verify batch too large");
     if (offset < 0 || offset + n > m->max_seq) return set_error(MLXR_E_CONTEXT_FULL, "The context window is full.");
     if (int rc = check_tokens(m, tokens, n)) return rc;
+    // one token whose step the persistent kernel takes (the decode loop's own step: speculative
+    // decoding's steps without a draft): the token goes into the history, one greedy step runs
+    // (its pick is not used: the caller samples from the logits), and its logits are returned
+    bool idle = true;
+    for (auto& s : m->slots) idle = idle && !s.busy;
+    if (n == 1 && idle && offset + 1 < m->max_seq && m->mega_ok && m->decode_mode == 1 &&
+        !(m->sparse_on && sparse_plan_valid(m->sparse, offset))) {
+        if (int rc = write_tokens(m, tokens, 1, offset)) return rc;
+        mlxr_sample_params g{};
+        g.penalty = 1.0f; g.temperature = 0.0f; g.top_p = 1.0f; g.min_p = 0.0f;
+        mlxr_step st;
+        int32_t pick = 0;
+        if (int rc = model_begin_decode(m, offset, &g, &st)) return rc;
+        if (int rc = model_finish(m, &st, &pick)) return rc;
+        return model_step_logits(m, out);
+    }
     for (int start = 0; start < n;) {
         if (start > 0 && cancel.requested()) return set_error(MLXR_E_CANCELLED, "cancelled");   // Transformer.swift:1127
         const int k = std::min(m->max_batch, n - start);
