@@ -278,7 +278,7 @@ __device__ __forceinline__ void mv_run(const MvPhase p, const float* xh, const f
         f32x4_t acc;
 #pragma unroll
         for (int r = 0; r < 4; r++) {   // hi (column c) + lo (column c ^ 8) of each group
-            const float sa = accA[r] + __shfl_xor(accA[r], 8, 64), sb = accB[r] + __shfl_xor(accB[r], 8, 64);
+            const float sa = accA[r] + dpp<0x128>(accA[r]), sb = accB[r] + dpp<0x128>(accB[r]);   // lane c ^ 8: row rotation by 8
             acc[r] = col < 8 ? sa : sb;
         }
         const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
@@ -404,7 +404,7 @@ __device__ __forceinline__ void mvh_run(const MvPhase p, const float* xh, const 
         const uint32_t sv[4] = {sbr.x, sbr.y, sbr.z, sbr.w};
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float a = acc0[r] + __shfl_xor(acc0[r], 8, 64);
+            const float a = acc0[r] + dpp<0x128>(acc0[r]);   // lane c ^ 8: row rotation by 8
             const float sc = __uint_as_float(sv[r] << 16) * 16777216.0f, bb = __uint_as_float(sv[r] & 0xffff0000u);
             const float t = sc * a + bb * xs;
             run[r] += real ? t : 0.0f;
