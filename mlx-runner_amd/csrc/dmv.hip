@@ -83,9 +83,6 @@ __device__ __forceinline__ void dmv_body(const MvPhaseDesc& p, const float* __re
                 if (nw) { wv[i][0] = gf4(nw + 8 * t); wv[i][1] = gf4(nw + 8 * t + 4); }
             }
         }
-        // the weights' first scale group after x: the memory counter completes in order, so the
-        // statistics wait for x alone while the weights stream in behind
-        mv_prefetch<FB, TS>(p, wg, nwg, wave, lane, ring);
 #pragma unroll
         for (int i = 0; i < XR; i++)
 #pragma unroll
@@ -95,6 +92,12 @@ __device__ __forceinline__ void dmv_body(const MvPhaseDesc& p, const float* __re
                 const float4 a = float4{v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w};
                 mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
             }
+        // the weights' first scale group once x is in (the memory counter completes in order: a
+        // prefetch issued before would make the statistics wait for it); it streams in during the
+        // reductions and the packing. The empty asm takes the statistics as inputs and clobbers
+        // memory, so neither the statistics nor the prefetch's loads move across it.
+        asm volatile("" : : "v"(ss), "v"(mx) : "memory");
+        mv_prefetch<FB, TS>(p, wg, nwg, wave, lane, ring);
         ss = wave_sum(ss); mx = wave_max(mx);
         if (lane == 0) { red[wave] = ss; red[8 + wave] = mx; }
         lds_barrier();
