@@ -513,17 +513,33 @@ __global__ __launch_bounds__(256) void sparse_score_kernel(const float* q, const
     if (plan) { if (!plan->valid) return; b0 = plan->b0; nb = plan->nb; }
     const int lane = threadIdx.x & 63, hq = lane >> 4, dq = lane & 15;
     const int gw = blockIdx.x * 4 + (threadIdx.x >> 6), nw = gridDim.x * 4;
-    // qsum of every KV head into LDS (loads unrolled with guards: all in flight at once)
+    // this wave's first blocks of the index (unconditional: rows clamped into the range, heads
+    // past nKV read head 0), issued before the q loads so that their memory latencies overlap
+    uint4 kv[SCORE_BPW][4];
+    auto load_blocks = [&](int nbase) {
+#pragma unroll
+        for (int i = 0; i < SCORE_BPW; i++) {
+            const int n = max(0, min(nbase + i, nb - 1));
+            const uint4* row = reinterpret_cast<const uint4*>(idx + (int64_t)(b0 + n) * W);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int h = hq + 4 * j;
+                kv[i][j] = row[(h < nKV ? h : 0) * 16 + dq];
+            }
+        }
+    };
+    load_blocks(gw * SCORE_BPW);
+    // qsum of every KV head into LDS (unconditional loads, indices clamped: all in flight at once)
     __shared__ float qsum[16 * ATT_D];
 #pragma unroll
     for (int r = 0; r < 16 * ATT_D / 256; r++) {
         const int i = threadIdx.x + 256 * r, h = i / ATT_D, d = i % ATT_D;
         float x[ATT_MAXG];
 #pragma unroll
-        for (int g = 0; g < ATT_MAXG; g++) x[g] = i < W && g < G ? q[(int64_t)(h * G + g) * ATT_D + d] : 0.0f;
+        for (int g = 0; g < ATT_MAXG; g++) x[g] = q[(int64_t)min(h * G + min(g, G - 1), nH - 1) * ATT_D + d];
         float sum = 0.0f;
 #pragma unroll
-        for (int g = 0; g < ATT_MAXG; g++) sum += x[g];
+        for (int g = 0; g < ATT_MAXG; g++) sum += g < G ? x[g] : 0.0f;
         if (i < W) qsum[i] = sum;
     }
     __syncthreads();
@@ -535,17 +551,7 @@ __global__ __launch_bounds__(256) void sparse_score_kernel(const float* q, const
         for (int e = 0; e < 8; e++) qv[j][e] = h < nKV ? qsum[h * ATT_D + 8 * dq + e] : 0.0f;
     }
     for (int nbase = gw * SCORE_BPW; nbase < nb; nbase += nw * SCORE_BPW) {
-        uint4 kv[SCORE_BPW][4];
-#pragma unroll
-        for (int i = 0; i < SCORE_BPW; i++) {
-            const int n = min(nbase + i, nb - 1);
-            const uint4* row = reinterpret_cast<const uint4*>(idx + (int64_t)(b0 + n) * W);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int h = hq + 4 * j;
-                kv[i][j] = h < nKV ? row[h * 16 + dq] : uint4{0u, 0u, 0u, 0u};
-            }
-        }
+        if (nbase != gw * SCORE_BPW) load_blocks(nbase);
 #pragma unroll
         for (int i = 0; i < SCORE_BPW; i++) {
             const int n = nbase + i;
