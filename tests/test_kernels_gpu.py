@@ -286,9 +286,9 @@ def test_qmm_tiles_small_batch(gpu, gs):
     different magnitude, a single part of many tiles per workgroup (the lm_head), and the gated
     form."""
     rng = np.random.default_rng(gs)
-    for K, Os in ((128, (40,)), (1024, (264, 40, 88)), (4096, (72,)), (12288, (24,))):
+    for K, Os in ((128, (40,)), (1024, (264, 40, 88)), (4096, (72,)), (12288, (24,)), (27648, (40,))):
         fxs = [QuantFixture(O, K, 4, gs, seed=O + K, with_bias=len(Os) > 1, fast=True) for O in Os]
-        for T in (1, 3, 8):
+        for T in ((1, 3, 8) if K < 27648 else (8,)):   # the 32B down: seven input slices at T = 8
             mag = (10.0 ** np.linspace(-3, 3, T)).astype(np.float32)
             x = rng.normal(0, 1, (T, K)).astype(np.float32) * mag[:, None]
             ref = np.concatenate([f.oracle(oracle).matmul_f64(x) for f in fxs], axis=1)
@@ -530,13 +530,14 @@ def test_attention_decode_and_split(gpu, nH, nKV):
 
 
 @pytest.mark.parametrize("nH,nKV,offset,T,nsplit", [(32, 8, 700, 8, 3), (40, 8, 300, 8, 1), (4, 2, 100, 5, 64),
-                                                   (8, 1, 37, 2, 32), (64, 8, 511, 8, 5)])
+                                                   (8, 1, 37, 2, 32), (64, 8, 511, 8, 5), (40, 8, 1000, 8, 256)])
 def test_attention_verify_batch(gpu, nH, nKV, offset, T, nsplit):
     """The verify batch's attention (attention_split + attention_combine per query, Kernels.swift:
     1317-1374): the T queries of a KV head share one pass over each key range, query t masked past
     its own position offset + t. Every query against the reference attention at its position; keys
     past the batch's last position are NaN (never read); ranges past a query's position (nsplit 64
-    over 105 keys), ranges raised to 256 keys at most (nsplit 1 over 308 keys), and G T up to 64."""
+    over 105 keys), ranges raised to 128 keys at most (nsplit 1 over 308 keys), G T up to 64, and
+    the 32B shape's many ranges (G = 5, T = 8, 256 ranges of 4 keys)."""
     D, S = 128, 1024
     kc = bf16_to_f32(bf16_round(np.random.default_rng(nH + T).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
     vc = bf16_to_f32(bf16_round(np.random.default_rng(nH + T + 1).uniform(-1, 1, (nKV, S, D)).astype(np.float32)))
