@@ -110,6 +110,14 @@ def test_config2_qwen3_8b_decode_at_4k(gpu, workdir):
             amb += check_step(got, want, nxt, f"step {i}")
             tok = nxt
         assert amb <= 1
+        # the speculative verify pass (f3) at this shape: 5 tokens after the decoded ones, every
+        # row against the oracle teacher-forced (small-batch matvec on the tiles, verify attention)
+        batch = np.concatenate([[tok], ids[100:104]]).astype(np.int32)
+        rows = m.forward(batch, n + 4, all_logits=True)
+        for i in range(5):
+            want = ref.forward(batch[i:i + 1], n + 4 + i)
+            err = float(np.max(np.abs(rows[i] - want)))
+            assert err < LOGIT_TOL, ("verify row", i, err)
 
 
 def test_config3_llama3_8b_prefill_2048(gpu, workdir):
