@@ -328,7 +328,7 @@ __global__ __launch_bounds__(256) void attn_multi_kernel(AttnArgs a) {
     };
     int cur_rt = wave % nrt;
     load_q(cur_rt);
-    if (tid < nk) rowi[tid] = (int)kv_row(a.pt, a.nKV, kvh, n0 + tid);   // ATT_MC <= 256 keys
+    if (tid < nk) rowi[tid] = (int)kv_row(a.pt, a.nKV, kvh, n0 + tid);   // nk <= ATT_MC <= 256 threads
     if (tid < GT) {   // partials of row r = t G + g: [t][(head, split)], below 2^31 floats
         const int t = tid / G, g = tid - t * G;
         ro[tid] = int2{t * rows * (D + 2), (kvh * G + g) * a.nsplit + split};
