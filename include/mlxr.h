@@ -218,7 +218,8 @@ int mlxr_k_qmv_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode
  * Kernels.swift:60-113, 518-622): T = 1..8 tokens (x[t] at x + t * x_stride, y[t] at
  * y + t * y_stride), mode 0 y[t] = W x[t] (+ bias), 1 y[t] += W x[t] (+ bias), 2 (two parts of
  * equal O) y[t][o] = silu(A x_t)[o] * (B x_t)[o]; norm_w (or NULL) first replaces each x[t] by
- * RMSNorm(x[t]) * norm_w (eps). Same quantization limits as mlxr_k_qmv_tiles. */
+ * RMSNorm(x[t]) * norm_w (eps). x and norm_w 16-byte aligned, x_stride a multiple of 4. Same
+ * quantization limits as mlxr_k_qmv_tiles. */
 int mlxr_k_qmm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode, int T, const float* x, int x_stride,
                      const float* norm_w, float eps, float* y, int y_stride);
 /* Quantized embedding rows (`qembed`, Kernels.swift:1002-1023): ids device int32 [T]. */

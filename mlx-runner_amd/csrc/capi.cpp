@@ -315,6 +315,8 @@ int mlxr_k_qmm_tiles(const mlxr_qmat* parts, int nparts, int K, int gs, int mode
     if (int rc = ensure_stream()) return rc;
     if (T < 1 || T > 8 || mode < 0 || mode > 2 || !x || !y || x_stride < K || x_stride % 4)
         return set_error(MLXR_E_INVALID_ARG, "T 1..8 / mode / pointers / strides");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(norm_w)) & 15)   // read as 16-byte vectors
+        return set_error(MLXR_E_INVALID_ARG, "x and norm_w must be 16-byte aligned");
     MvPhaseDesc d; uint8_t* code;
     if (int rc = tiles_pack(parts, nparts, K, gs, mode == 2, d, code)) return rc;
     const int cols = mode == 2 ? d.o1 : d.rows;
