@@ -368,17 +368,21 @@ __global__ __launch_bounds__(256) void attn_multi_kernel(AttnArgs a) {
     }
     __syncthreads();
     // per-row max and exp over the row's own keys (n0 .. min(n1, *dpos + t + 1)), lane: keys 2 lane,
-    // 2 lane + 1 (nkq <= 128); p as three bf16 terms over the dead K image, zeros up to the 32-key
+    // 2 lane + 1 of each 128; p as three bf16 terms over the dead K image, zeros up to the 32-key
     // step edge. Padded rows stay as they are: an MFMA output row reads only its own A row.
     for (int r = wave; r < GT; r += 4) {
         const int nv = max(0, min(nk, pos0 + r / G + 1 - n0));
-        const int k2 = 2 * lane;
-        const float2 v = k2 < nkq ? *reinterpret_cast<const float2*>(sc + r * L.scs + k2) : float2{0.0f, 0.0f};
-        float m = fmaxf(k2 < nv ? v.x : -1e30f, k2 + 1 < nv ? v.y : -1e30f);
+        float m = -1e30f;
+        for (int k2 = 2 * lane; k2 < nkq; k2 += 128) {
+            const float2 v = *reinterpret_cast<const float2*>(sc + r * L.scs + k2);
+            m = fmaxf(m, fmaxf(k2 < nv ? v.x : -1e30f, k2 + 1 < nv ? v.y : -1e30f));
+        }
         m = wave_max(m);
-        const float p0 = k2 < nv ? expf(v.x - m) : 0.0f, p1 = k2 + 1 < nv ? expf(v.y - m) : 0.0f;
-        const float l = wave_sum(p0 + p1);
-        if (k2 < nkq) {
+        float l = 0.0f;
+        for (int k2 = 2 * lane; k2 < nkq; k2 += 128) {
+            const float2 v = *reinterpret_cast<const float2*>(sc + r * L.scs + k2);
+            const float p0 = k2 < nv ? expf(v.x - m) : 0.0f, p1 = k2 + 1 < nv ? expf(v.y - m) : 0.0f;
+            l += p0 + p1;
             const uint32_t h = att_pk(p0, p1);
             const float r0 = p0 - __uint_as_float(h << 16), r1 = p1 - __uint_as_float(h & 0xffff0000u);
             const uint32_t md = att_pk(r0, r1);
@@ -387,6 +391,7 @@ __global__ __launch_bounds__(256) void attn_multi_kernel(AttnArgs a) {
             *reinterpret_cast<uint32_t*>(pb + (GP + r) * L.PS + k2) = md;
             *reinterpret_cast<uint32_t*>(pb + (2 * GP + r) * L.PS + k2) = lo;
         }
+        l = wave_sum(l);
         if (lane == 0) { mx[r] = nv > 0 ? m : -1e30f; lsum[r] = l; }
     }
     __syncthreads();
