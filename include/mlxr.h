@@ -147,6 +147,8 @@ int mlxr_profile_decode_phases(mlxr_model* m, int offset, double* out, int max_i
 int mlxr_debug_stall_next_step(mlxr_model* m);
 /* 1 when begin_decode runs the persistent kernel for dense steps. */
 int mlxr_decode_mode(const mlxr_model* m);
+/* Why dense steps do not run the persistent kernel ("" when they do); valid until the model closes. */
+const char* mlxr_decode_mode_reason(const mlxr_model* m);
 /* Decode steps with the whole step captured as a hipGraph (1, default) or launched kernel by kernel (0). */
 int mlxr_set_graphs(mlxr_model* m, int enabled);
 

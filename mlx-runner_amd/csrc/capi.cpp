@@ -24,6 +24,9 @@ float* g_qsplit = nullptr; size_t g_qsplit_floats = 0;   // the GEMM's split-ove
 float* g_split = nullptr; size_t g_split_floats = 0;   // the long-input split matvec's scratch
 uint16_t* g_xbf = nullptr; size_t g_xbf_elems = 0;
 float* g_xsc = nullptr; size_t g_xsc_elems = 0;
+uint16_t* g_xlo = nullptr; size_t g_xlo_elems = 0;   // the MLX-layout GEMM's pre-pass: x lo part, group sums, lo flags
+float* g_xgs = nullptr; size_t g_xgs_elems = 0;
+int* g_xnz = nullptr; size_t g_xnz_elems = 0;
 float* g_bmax = nullptr; int* g_barg = nullptr; int g_blocks = 0;
 hipEvent_t g_t0 = nullptr, g_t1 = nullptr;
 
@@ -148,6 +151,11 @@ int mlxr_profile_kernel(mlxr_model* m, const char* kind, int iters, int context,
 }
 int mlxr_set_decode_mode(mlxr_model* m, int mode) { return m ? model_set_decode_mode(m->m, mode) : set_error(MLXR_E_INVALID_ARG, "null model"); }
 int mlxr_decode_mode(const mlxr_model* m) { return m && m->m->mega_ok && m->m->decode_mode == 1 ? 1 : 0; }
+const char* mlxr_decode_mode_reason(const mlxr_model* m) {
+    if (!m) return "null model";
+    if (m->m->mega_ok && m->m->decode_mode == 1) return "";
+    return m->m->mega_ok ? "decode mode set to the kernel-per-op step" : m->m->mega_reason.c_str();
+}
 int mlxr_profile_decode_phases(mlxr_model* m, int offset, double* out, int max_intervals) {
     if (!m || !out) return set_error(MLXR_E_INVALID_ARG, "null argument");
     return model_phase_times(m->m, offset, out, max_intervals);
@@ -231,12 +239,16 @@ int mlxr_k_qgemm(const mlxr_qmat* mat, int K, int bits, int gs, int st, int T, c
     if (T < 1 || !x || !y || x_stride < K || y_stride < mat->O || x_stride % 4) return set_error(MLXR_E_INVALID_ARG, "T / strides");
     if (int rc = ensure_buf(g_xbf, g_xbf_elems, (size_t)T * K)) return rc;
     if (int rc = ensure_buf(g_xsc, g_xsc_elems, (size_t)T)) return rc;
+    if (int rc = ensure_buf(g_xlo, g_xlo_elems, (size_t)T * K)) return rc;
+    if (int rc = ensure_buf(g_xgs, g_xgs_elems, (size_t)T * (K / gs))) return rc;
+    if (int rc = ensure_buf(g_xnz, g_xnz_elems, (size_t)T)) return rc;
     if (!g_qsplit) {
         if (int rc = ensure_buf(g_qsplit, g_qsplit_floats, QGEMM_SPLIT_FLOATS)) return rc;
         CK(hipMemset(g_qsplit, 0, QGEMM_SPLIT_FLOATS * 4));
     }
     QGemmArgs a; a.m = qmat(*mat); a.K = K; a.bits = bits; a.gs = gs; a.st = st; a.O = mat->O; a.T = T;
     a.x = x; a.x_stride = x_stride; a.y = y; a.y_stride = y_stride; a.xbf = g_xbf; a.xsc = g_xsc;
+    a.xlo = g_xlo; a.xgs = g_xgs; a.xnz = g_xnz;
     a.split = g_qsplit; a.split_floats = g_qsplit_floats;
     return done(launch_qgemm(a, g_stream));
 }

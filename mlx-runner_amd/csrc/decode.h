@@ -36,8 +36,12 @@ bool dpack_mv_supported(const MvPhaseDesc& p);
 // (its tile counters return to zero after every launch); with it, a projection without norm or
 // gate whose tiles are too few to spread evenly over the CUs runs as up to DMV_MAX_SLICES input
 // slices of every tile, the slices' partials combined in order by the last of them.
+// Every split launch (this one and the small-batch launch below) keeps its per-tile counters in the
+// first DMV_SPLIT_CNT words of the scratch and its partials after them, so launches of different
+// tile counts sharing one scratch never write partials over another launch's counters.
 constexpr int DMV_MAX_SLICES = 8;
-inline size_t dpack_mv_split_floats(int rows) { return (size_t)DMV_MAX_SLICES * rows + (size_t)(rows + 15) / 16 + 64; }
+constexpr int DMV_SPLIT_CNT = 16384;   // tiles of a split launch (max)
+inline size_t dpack_mv_split_floats(int rows) { return (size_t)DMV_SPLIT_CNT + (size_t)DMV_MAX_SLICES * rows; }
 hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* norm_w, float eps, float* y, int mode,
                            hipStream_t s, float* split = nullptr);
 // The same matrices for T = 1..8 tokens (x[t] at x + t * xs, y[t] at y + t * ys): y = W x (+ bias),

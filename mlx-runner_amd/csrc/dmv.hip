@@ -174,15 +174,15 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_kernel(MvPhaseDesc p, con
 // Split over the input (no norm, not gated): workgroup (w, s) computes the rows of its share of the
 // tiles (as dpack_mv_kernel shares them over gridDim.x workgroups) over the s-th of gridDim.y
 // contiguous runs of every tile's scale groups, from its own slice of x, into part[s][rows] with
-// coherent stores; for each tile, the last slice to finish (per-tile counters at the start of the
-// scratch, part after them, so that launches of other shapes and slice counts sharing the scratch
-// never overwrite a counter; reset by that slice for the next launch) adds the slices in order,
+// coherent stores; for each tile, the last slice to finish (per-tile counters in the scratch's fixed
+// counter region, part after it, so that launches of other shapes and slice counts sharing the
+// scratch never overwrite a counter; reset by that slice for the next launch) adds the slices in order,
 // the bias and the output: deterministic, and no combine launch.
 template <int FB>
 __global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc p, const float* __restrict__ x, float* __restrict__ split,
                                                                     float* __restrict__ y, int accumulate, int tpw) {
     unsigned* cnt = reinterpret_cast<unsigned*>(split);
-    float* part = split + ((p.tiles + 63) & ~63);
+    float* part = split + DMV_SPLIT_CNT;
     const int w = blockIdx.x, nw = gridDim.x, sl = blockIdx.y, S = gridDim.y;
     const int NF = ((p.K >> 7) + FB - 1) / FB;
     const int fa = NF * sl / S, fb = NF * (sl + 1) / S;
@@ -198,7 +198,7 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mv_split_kernel(MvPhaseDesc 
     __shared__ int last[MK_TPW];
     const MvGeom<FB> g = mv_geom<FB>(q, w, nw, 0);
     if ((int)threadIdx.x < g.nt)
-        last[threadIdx.x] = __hip_atomic_fetch_add(cnt + g.t0 + threadIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+        last[threadIdx.x] = __hip_atomic_fetch_add(cnt + g.t0 + threadIdx.x, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
     __syncthreads();
     for (int i = threadIdx.x; i < g.nt * 16; i += MK_THREADS) {
         if (!last[i >> 4]) continue;
@@ -517,7 +517,7 @@ __global__ void __launch_bounds__(MK_THREADS) dpack_mm_kernel(MmArgs a) {
     __syncthreads();
     int* last = reinterpret_cast<int*>(slots);
     if ((int)threadIdx.x < g0.nt)
-        last[threadIdx.x] = __hip_atomic_fetch_add(a.cnt + T0 + threadIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+        last[threadIdx.x] = __hip_atomic_fetch_add(a.cnt + T0 + threadIdx.x, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
     __syncthreads();
     auto partial = [&](int tl, int row, int tk) {
         float v = 0.0f;
@@ -583,7 +583,7 @@ hipError_t launch_dpack_mv(const MvPhaseDesc& p, const float* x, const float* no
     // the 32B projections: gate|up 43 -> 36 us at 2, down 48 -> 37 us at 1)
     const int nwg = std::min(p.tiles, (p.K > 16384 ? 1 : 2) * cus);
     const int tpw = (p.tiles + nwg - 1) / nwg;
-    if (split && !norm_w && mode != OUT_GATED) {
+    if (split && !norm_w && mode != OUT_GATED && p.tiles <= DMV_SPLIT_CNT) {
         // S input slices of every tile over nw = slots / S workgroups each (two per CU: a slice's
         // f16 image fits twice in LDS); the longest workgroup streams ceil(tiles / nw) tiles x
         // ceil(NF / S) scale groups over its 8 waves: take the S that makes the longest wave's chain
@@ -653,7 +653,7 @@ size_t dpack_mm_split_floats(const MvPhaseDesc& p) {
     int S = 1;
     for (int nt = 1; nt <= DMM_TOK; nt++) { size_t lds = 0; S = std::max(S, mm_slices(p, nt, &lds)); }
     if (S <= 1) return 0;
-    return (size_t)(p.tiles + 63) / 64 * 64 + (size_t)S * DMM_TOK * 16 * p.tiles;
+    return (size_t)DMV_SPLIT_CNT + (size_t)S * DMM_TOK * 16 * p.tiles;
 }
 
 hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, const float* norm_w, float eps, float* y, int ys,
@@ -677,12 +677,12 @@ hipError_t launch_dpack_mm(const MvPhaseDesc& p, const float* x, int xs, const f
     size_t lds = 0;
     const int S = mm_slices(p, T, &lds);
     if (S == 0) return hipErrorInvalidValue;
-    const size_t tiles_al = (size_t)(p.tiles + 63) / 64 * 64;
-    if (S > 1 && (!split || split_floats < tiles_al + (size_t)S * T * 16 * p.tiles)) return hipErrorInvalidValue;
+    if (S > 1 && (!split || p.tiles > DMV_SPLIT_CNT || split_floats < (size_t)DMV_SPLIT_CNT + (size_t)S * T * 16 * p.tiles))
+        return hipErrorInvalidValue;
     MmArgs a;
     a.p = p; a.x = x; a.xs = xs; a.nw = norm_w; a.eps = eps; a.y = y; a.ys = ys; a.accumulate = accumulate ? 1 : 0;
     a.t0 = 0; a.nt = T;
-    a.cnt = reinterpret_cast<unsigned*>(split); a.part = split ? split + tiles_al : nullptr;
+    a.cnt = reinterpret_cast<unsigned*>(split); a.part = split ? split + DMV_SPLIT_CNT : nullptr;
     // one workgroup per CU over all slices (the images fill most of the LDS)
     const int nwg = std::min(p.tiles, std::max(1, cus / S));
     // the longest slice decides how many 8-groups of x each thread holds

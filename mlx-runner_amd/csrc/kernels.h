@@ -41,16 +41,19 @@ struct QmmSmallArgs {
 };
 hipError_t launch_qmm_small(const QmmSmallArgs& a, hipStream_t s);
 
-// Prefill GEMM on bf16 MFMA: Y[T][O] = bf16(X[T][K]) * bf16(s*q+b)^T (+bias), fp32 accumulate.
+// Prefill GEMM over the MLX layout, any code width: Y[T][O] = X[T][K] W[O][K]^T (+bias) with exact
+// codes on the f16 matrix cores, x as f16 hi + lo (per-row power-of-two scale) and the group scale
+// and bias applied in fp32 per group: fp32-level results. Needs K % 64 == 0, gs % 32 == 0.
 struct QGemmArgs {
     QMat m;
     int K = 0, bits = 4, gs = 64, st = 0, O = 0, T = 0;
     const float* x = nullptr; int x_stride = 0;
     float* y = nullptr; int y_stride = 0;
-    uint16_t* xbf = nullptr;              // scratch: T*K 16-bit (x rounded once per call)
-    float* xsc = nullptr;                 // scratch: T floats (per-row power-of-two scales); null = bf16 path
-    bool x_ready = false;                 // xbf / xsc already hold this x (same K): skip the pre-pass
-    // optional scratch for the other widths' GEMM split over K when its grid is under one round:
+    // pre-pass scratch: hi and lo (T*K 16-bit each), group sums (T*K/gs floats), the rows' inverse
+    // scales (T floats) and lo-nonzero flags (T ints)
+    uint16_t* xbf = nullptr; uint16_t* xlo = nullptr; float* xgs = nullptr; float* xsc = nullptr; int* xnz = nullptr;
+    bool x_ready = false;                 // the scratch already holds this x (same K and gs): skip the pre-pass
+    // optional scratch for the split over K when the grid is under one round:
     // QGEMM_SPLIT_FLOATS floats, zero before first use (its tile counters return to zero)
     float* split = nullptr; size_t split_floats = 0;
 };

@@ -583,7 +583,8 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
         (rc = dalloc(m, &m->attn, (size_t)B * c.nH * c.D)) || (rc = dalloc(m, &m->gu, (size_t)B * 2 * I)) ||
         (rc = dalloc(m, &m->mlp, (size_t)B * I)) || (rc = dalloc(m, &m->logits, (size_t)8 * V)) || (rc = dalloc(m, &m->dmv_split, dpack_mv_split_floats(H))) ||
         (rc = dalloc(m, &m->part, partFloats)) || (rc = dalloc(m, &m->qsplit, QGEMM_SPLIT_FLOATS)) || (rc = dalloc(m, &m->bmax, (V + 255) / 256)) ||
-        (rc = dalloc(m, &m->barg, (V + 255) / 256)) || (rc = dalloc(m, &m->xbf, (size_t)B * Kmax)) || (rc = dalloc(m, &m->xsc, (size_t)B)) || (rc = dalloc(m, &m->diag, 8)))
+        (rc = dalloc(m, &m->barg, (V + 255) / 256)) || (rc = dalloc(m, &m->xbf, (size_t)B * Kmax)) || (rc = dalloc(m, &m->xsc, (size_t)B)) || (rc = dalloc(m, &m->diag, 8)) ||
+        (rc = dalloc(m, &m->xlo, (size_t)B * Kmax)) || (rc = dalloc(m, &m->xgs, (size_t)B * Kmax / 32)) || (rc = dalloc(m, &m->xnz, (size_t)B)))
         return fail(rc);
     HIPCHECK(hipMemset(m->hist, 0, (seq + 1) * 4));
     HIPCHECK(hipMemset(m->dmv_split, 0, dpack_mv_split_floats(H) * 4));   // the split matvec's tile counters
@@ -664,6 +665,7 @@ int project(Model* m, const Lin* parts, int n, const float* x, int xs, float* y,
     for (int i = 0; i < n; i++) {
         QGemmArgs g; g.m = parts[i].m; g.K = parts[i].K; g.bits = parts[i].bits; g.gs = parts[i].gs; g.st = parts[i].st;
         g.O = parts[i].O; g.T = T; g.x = x; g.x_stride = xs; g.y = y + col; g.y_stride = ys; g.xbf = m->xbf; g.xsc = m->xsc;
+        g.xlo = m->xlo; g.xgs = m->xgs; g.xnz = m->xnz;
         g.split = m->qsplit; g.split_floats = QGEMM_SPLIT_FLOATS;
         g.x_ready = i > 0 && parts[i].K == parts[0].K && parts[i].bits == parts[0].bits && parts[i].gs == parts[0].gs;
         HIPCHECK(launch_qgemm(g, s));

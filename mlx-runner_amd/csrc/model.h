@@ -67,6 +67,7 @@ struct Model {
     float* logits = nullptr; float* part = nullptr; float* bmax = nullptr; int* barg = nullptr;
     float* qsplit = nullptr;            // the other widths' prefill GEMM split over K (QGEMM_SPLIT_FLOATS, counters at zero)
     uint16_t* xbf = nullptr; float* xsc = nullptr;
+    uint16_t* xlo = nullptr; float* xgs = nullptr; int* xnz = nullptr;   // the MLX-layout GEMM's x lo part, group sums, lo flags
     int* diag = nullptr;
     // sparse
     bool sparse_alloc = false; bool sparse_on = false;

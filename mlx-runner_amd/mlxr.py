@@ -80,7 +80,7 @@ def _load():
         "mlxr_finish": (I, [P, C.POINTER(Step), C.POINTER(C.c_int32)]),
         "mlxr_reusable_prefix": (I, [P, I, I]), "mlxr_reset_write_tracking": (V, [P]),
         "mlxr_seed_sampler": (I, [P, C.c_uint64]), "mlxr_set_sparse": (I, [P, C.POINTER(SparseCfg)]),
-        "mlxr_last_gpu_time": (C.c_double, [P]), "mlxr_read_kv": (I, [P, I, I, P, P]), "mlxr_set_graphs": (I, [P, I]), "mlxr_set_decode_mode": (I, [P, I]), "mlxr_decode_mode": (I, [P]), "mlxr_profile_decode_phases": (I, [P, I, P, I]), "mlxr_debug_stall_next_step": (I, [P]),
+        "mlxr_last_gpu_time": (C.c_double, [P]), "mlxr_read_kv": (I, [P, I, I, P, P]), "mlxr_set_graphs": (I, [P, I]), "mlxr_set_decode_mode": (I, [P, I]), "mlxr_decode_mode": (I, [P]), "mlxr_decode_mode_reason": (C.c_char_p, [P]), "mlxr_profile_decode_phases": (I, [P, I, P, I]), "mlxr_debug_stall_next_step": (I, [P]),
         "mlxr_profile_kernel": (I, [P, C.c_char_p, I, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
         "mlxr_synth_write": (I, [C.c_char_p, C.c_uint64, F, C.c_char_p]),
         "mlxr_quantize_row": (I, [P, I, I, I, P, P, P]),
@@ -312,6 +312,11 @@ class Transformer:
     @property
     def persistent_decode(self) -> bool:
         return bool(lib.mlxr_decode_mode(self._h))
+
+    @property
+    def persistent_decode_reason(self) -> str:
+        """Why dense steps run kernel by kernel ("" when the persistent step runs them)."""
+        return lib.mlxr_decode_mode_reason(self._h).decode()
 
     def profile_decode_phases(self, offset: int):
         """[(mean start, mean end, latest end) us] of each interval of one persistent decode step."""

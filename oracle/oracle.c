@@ -116,7 +116,7 @@ double orc_round_f16_d(double v) {
     const double r = ldexp(nearbyint(ldexp(v, -q)), q);
     return fabs(r) > 65504.0 ? copysign(INFINITY, v) : r;
 }
-/* The 4-bit prefill GEMM's precision (mlx-runner_amd/csrc/gemm.hip, qgemm4_kernel): each token row
+/* The 4-bit model prefill's tile GEMM precision (mlx-runner_amd/csrc/ptile.hip): each token row
  * is scaled by the power of two 2^e that puts max|x| in [2^13, 2^14) and rounded to f16; each weight
  * is f16(fma(s16, q, b16)) with s, b converted to f16; products accumulate exactly here (f32 on the
  * GPU) and the row is scaled back by 2^-e. */
@@ -139,11 +139,7 @@ static double dot_f64(const float* w, const float* x, int K) {
 static void qlinear_impl(const orc_qlinear* l, const float* x, int T, float* y, int mode) {
     float* xr = NULL;
     double* inv = NULL;
-    if (mode == 1) {
-        xr = (float*)malloc((size_t)T * l->K * sizeof(float));
-        for (int64_t i = 0; i < (int64_t)T * l->K; i++) xr[i] = orc_round_bf16(x[i]);
-        x = xr;
-    } else if (mode == 2) {
+    if (mode == 2) {
         xr = (float*)malloc((size_t)T * l->K * sizeof(float));
         inv = (double*)malloc((size_t)T * sizeof(double));
         for (int t = 0; t < T; t++) {
@@ -173,7 +169,6 @@ static void qlinear_impl(const orc_qlinear* l, const float* x, int T, float* y, 
                 }
             } else {
                 orc_dequant_row(l, o, w);
-                if (mode == 1) for (int k = 0; k < l->K; k++) w[k] = orc_round_bf16(w[k]);
             }
             for (int t = 0; t < T; t++) {
                 const float* xt = x + (int64_t)t * l->K;
@@ -188,11 +183,11 @@ static void qlinear_impl(const orc_qlinear* l, const float* x, int T, float* y, 
     free(inv);
 }
 void orc_qlinear_f64(const orc_qlinear* l, const float* x, int T, float* y) { qlinear_impl(l, x, T, y, 0); }
-void orc_qlinear_bf16(const orc_qlinear* l, const float* x, int T, float* y) { qlinear_impl(l, x, T, y, 1); }
 void orc_qlinear_f16(const orc_qlinear* l, const float* x, int T, float* y) { qlinear_impl(l, x, T, y, 2); }
-/* The GPU GEMM path (T > 8 tokens): f16 operands for 4-bit with gs 32/64/128 and an even number of
- * groups per row, else bf16. */
-void orc_qlinear_prefill(const orc_qlinear* l, const float* x, int T, float* y) { qlinear_impl(l, x, T, y, f16_mode(l) ? 2 : 1); }
+/* The model prefill's precision (T > 8 tokens): the tile GEMM's f16 operands for 4-bit with gs
+ * 32/64/128 and an even number of groups per row; the MLX-layout GEMM's fp32-level products (exact
+ * codes, x as f16 hi + lo, scale and bias per group in fp32: modelled as exact) otherwise. */
+void orc_qlinear_prefill(const orc_qlinear* l, const float* x, int T, float* y) { qlinear_impl(l, x, T, y, f16_mode(l) ? 2 : 0); }
 
 /* ------------------------------------------------------------------ norms, RoPE */
 void orc_rms_norm(const float* x, float* y, const float* w, int dim, int rows, float eps) {

@@ -13,9 +13,8 @@
  * Precision contract (the build's declared precision, mirrored here):
  *   - activations fp32, accumulation in double (the reference tests' Float64 references);
  *   - K/V cache entries rounded to bf16 (round-to-nearest-even) when appended;
- *   - the batched prefill GEMM path (T > ORC_SMALL_T tokens per projection) multiplies
- *     bf16-rounded activations by bf16-rounded dequantized weights (`s*q+b` in fp32, then
- *     rounded), accumulating in double; the decode (T == 1) and small-batch paths keep fp32.
+ *   - optionally (orc_forward's small_t, a diagnostic) the 4-bit tile GEMM's f16 operand rounding
+ *     on chunks of more than small_t tokens; every other product is fp32-level (double here).
  */
 #ifndef MLXR_ORACLE_H
 #define MLXR_ORACLE_H
@@ -48,9 +47,11 @@ typedef struct {
 /* y[t][o] = sum_k (s*q+b) * x[t][k] (+ bias[o]); double accumulation, the reference test's
  * QuantFixture.reference (KernelTests.swift:102-113). x row stride K, y row stride O. */
 void orc_qlinear_f64(const orc_qlinear* l, const float* x, int T, float* y);
-/* The same product with bf16-rounded operands (the prefill GEMM's declared precision). */
-void orc_qlinear_bf16(const orc_qlinear* l, const float* x, int T, float* y);
+/* The 4-bit tile GEMM's operand rounding (f16 x with a per-row power-of-two scale, f16(fma(s, q, b))
+ * weights), double accumulation. */
 void orc_qlinear_f16(const orc_qlinear* l, const float* x, int T, float* y);
+/* The model prefill's precision: orc_qlinear_f16 where the tile GEMM runs (4-bit, gs 32/64/128, an
+ * even number of groups per row), orc_qlinear_f64 otherwise. */
 void orc_qlinear_prefill(const orc_qlinear* l, const float* x, int T, float* y);
 double orc_round_f16_d(double v);
 /* One row of dequantized weights (fp32 `s*q+b`, SieveImport.swift:108). */
@@ -110,8 +111,8 @@ const char* orc_last_error(void);
 int orc_model_vocab(const orc_model* m);
 int orc_model_hidden(const orc_model* m);
 /* Runs tokens at positions offset..offset+n-1 (KV appended), writes the last row's logits
- * (V floats) when logits != NULL. `small_t` mirrors the product's kernel choice: projections
- * over more than small_t tokens use the bf16 GEMM precision. Returns 0 on success. */
+ * (V floats) when logits != NULL. `small_t` (a diagnostic) mirrors the model prefill's kernel
+ * choice: projections over more than small_t tokens use orc_qlinear_prefill. Returns 0 on success. */
 int orc_forward(orc_model* m, const int32_t* tokens, int n, int offset, int small_t, float* logits);
 /* Sparse decode attention for single-token steps (0/NULL: dense). */
 void orc_model_set_sparse(orc_model* m, int enabled, int top_k, int window, int sink, int min_context, int per_head);

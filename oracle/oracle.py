@@ -28,7 +28,7 @@ def _load():
         "orc_bf16_to_f32": (F, [C.c_uint16]), "orc_f32_to_bf16": (C.c_uint16, [F]),
         "orc_f16_to_f32": (F, [C.c_uint16]), "orc_f32_to_f16": (C.c_uint16, [F]), "orc_round_bf16": (F, [F]),
         "orc_pack": (None, [P, C.c_int64, I, P]), "orc_unpack": (None, [P, C.c_int64, I, P]),
-        "orc_qlinear_f64": (None, [P, P, I, P]), "orc_qlinear_bf16": (None, [P, P, I, P]),
+        "orc_qlinear_f64": (None, [P, P, I, P]),
         "orc_qlinear_f16": (None, [P, P, I, P]), "orc_qlinear_prefill": (None, [P, P, I, P]),
         "orc_round_f16_d": (C.c_double, [C.c_double]),
         "orc_dequant_row": (None, [P, I, P]),
@@ -103,22 +103,16 @@ class QMatrix:
         lib.orc_qlinear_f64(C.byref(self.s), x.ctypes.data, x.shape[0], y.ctypes.data)
         return y
 
-    def matmul_bf16(self, x):
-        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.K)
-        y = np.zeros((x.shape[0], self.O), np.float32)
-        lib.orc_qlinear_bf16(C.byref(self.s), x.ctypes.data, x.shape[0], y.ctypes.data)
-        return y
-
     def matmul_f16(self, x):
-        """4-bit prefill GEMM precision: per-row power-of-two scaled f16 x, f16(fma(s, q, b)) weights."""
+        """The 4-bit tile GEMM's precision: per-row power-of-two scaled f16 x, f16(fma(s, q, b)) weights."""
         x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.K)
         y = np.zeros((x.shape[0], self.O), np.float32)
         lib.orc_qlinear_f16(C.byref(self.s), x.ctypes.data, x.shape[0], y.ctypes.data)
         return y
 
     def matmul_prefill(self, x):
-        """The GEMM path's declared precision for this matrix (f16 for 4-bit gs 32/64/128 with K / gs
-        even, else bf16)."""
+        """The model prefill's precision for this matrix (the tile GEMM's f16 operands for 4-bit gs
+        32/64/128 with K / gs even, else fp32-level: the double product)."""
         x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.K)
         y = np.zeros((x.shape[0], self.O), np.float32)
         lib.orc_qlinear_prefill(C.byref(self.s), x.ctypes.data, x.shape[0], y.ctypes.data)

@@ -5,8 +5,8 @@ synthetic weights (N(0, 0.02), MLX affine 4-bit g64 as mlxr_synth_write draws th
 
 1. Qwen3-0.6B, all 28 layers, tied 151936-row lm_head: a 32-token prompt and 64 greedy steps on
    the persistent decode step, every step's logits against the oracle teacher-forced.
-2. Qwen3-8B at full width (2 of its 36 layers; every layer has the same shapes): a 4096-token prefill,
-   then persistent decode steps over the GPU's own K/V cache loaded into the oracle.
+2. Qwen3-8B at full width (2 of its 36 layers; every layer has the same shapes): a 4096-token prefill
+   against the oracle's fp64 forward, then persistent decode steps, each side over its own K/V cache.
 3. Llama-3-8B at full width (2 layers), a 2048-token prefill: last-row logits against the oracle's
    fp64 forward.
 4. The matvec / GEMM sweep (K, N) x {3b g32, 4b g64, 6b g128, 8b g64} x T {1, 4, 512}, and the
@@ -98,10 +98,20 @@ def test_config2_qwen3_8b_decode_at_4k(gpu, workdir):
     with mlxr.Transformer(d, context_length=n + 256) as m:
         assert m.persistent_decode
         ref = oracle.Model(d, m.max_seq)
+        # the 4096-token prefill (two 2048-token chunks) against the oracle's own fp64 forward, which
+        # also fills the oracle's cache: the decode steps below run over each side's own K/V
+        got = m.forward(ids, 0)
+        say("config 2: oracle forward of 4096 tokens on", oracle.threads(), "threads")
+        want = ref.forward(ids, 0)
+        say("config 2: prefill max |d logit|", float(np.max(np.abs(got - want))))
         tok = m.prefill(ids, 0, GREEDY)
-        for layer in range(2):
-            ref.set_kv(layer, *m.read_kv(layer, n, 8, 128))
-        amb = 0
+        amb = check_step(got, want, tok, "prefill")
+        # prefill == incremental decode (ModelTests.swift:50-93): the last prompt token decoded as a
+        # step over the 4095-token prefix gives the prefill's logits
+        m.prefill(ids[:-1], 0, GREEDY)
+        inc = m.forward(ids[-1:], n - 1)
+        assert float(np.max(np.abs(inc - got))) < LOGIT_TOL
+        m.prefill(ids, 0, GREEDY)
         for i in range(4):
             st = m.begin_decode_step(n + i, GREEDY)
             nxt = m.finish(st)
@@ -109,6 +119,7 @@ def test_config2_qwen3_8b_decode_at_4k(gpu, workdir):
             want = ref.forward(np.array([tok], np.int32), n + i)
             amb += check_step(got, want, nxt, f"step {i}")
             tok = nxt
+        say("config 2: undecidable steps", amb)
         assert amb <= 1
         # the speculative verify pass (f3) at this shape: 5 tokens after the decoded ones, every
         # row against the oracle teacher-forced (small-batch matvec on the tiles, verify attention)
@@ -146,9 +157,8 @@ def _x_bf16(rng, T, K):
 
 @pytest.mark.parametrize("bits,gs", SWEEP_QUANT, ids=[f"{b}b-g{g}" for b, g in SWEEP_QUANT])
 def test_config4_sweep(gpu, bits, gs):
-    """Every (K, N) at T = 1 (qmv) and T = 4 (qmm) against the fp64 product at 1e-3 relative; T = 512
-    (the prefill GEMM) on 512 output rows against the oracle's model of the GEMM's operand rounding at
-    1e-3 and within the operand-rounding bound of the fp64 product."""
+    """Every (K, N) at T = 1 (qmv), T = 4 (qmm) and T = 512 (the prefill GEMM, on 512 output rows)
+    against the fp64 product at 1e-3 relative."""
     for K, N in SWEEP_SHAPES:
         say(f"config 4: K={K} N={N} {bits}-bit g{gs}")
         full = SynthMatrix(gpu, N, K, bits, gs, seed=104, tensor_id=K + N)
@@ -179,17 +189,9 @@ def test_config4_sweep(gpu, bits, gs):
         gpu.check(gpu.lib.mlxr_k_qgemm(qs, K, bits, gs, 0, 512, dxs.ptr, K, dys.ptr, 512))
         gpu.synchronize()
         got = dys.numpy()
-        so = sub.oracle(oracle)
-        assert max_rel_err(got, so.matmul_prefill(xs)) < 1e-3, ("T=512", K, N)
-        rel = 2.0 ** -10 if bits == 4 else 2.0 ** -8
-        bound = rel * (np.abs(xs).astype(np.float64) @ np.abs(sub_dense(sub)).T) + 1e-4
-        assert np.all(np.abs(got - so.matmul_f64(xs)) <= bound), ("T=512 bound", K, N)
-
-
-def sub_dense(m):
-    codes = np.stack([unpack_codes(m.packed[r], m.K, m.bits) for r in range(m.O)]).astype(np.float64)
-    g = np.repeat(np.arange(m.K // m.gs), m.gs)
-    return codes * m.scales[:, g].astype(np.float64) + m.biases[:, g].astype(np.float64)
+        err = max_rel_err(got, sub.oracle(oracle).matmul_f64(xs))
+        say(f"config 4: T=512 max rel err vs fp64 {err:.3g}")
+        assert err < 1e-3, ("T=512", K, N)
 
 
 @pytest.mark.parametrize("bits", [3, 6])
@@ -208,6 +210,42 @@ def test_config4_code_streams_bit_exact(gpu, bits):
     gpu.synchronize()
     want = np.stack([unpack_codes(m.packed[r], K, bits) for r in range(N)]).astype(np.float32)
     assert np.array_equal(out.numpy(), want)
+
+
+def test_config5_qwen2_5_32b_dense_decode_and_verify(gpu, workdir):
+    """Qwen2.5-32B width below the sparse threshold: five query heads per KV head and q/k/v biases
+    (the reference's INST_ASPLIT(4,5) case, Kernels.swift:2891-2892) on the dense decode step: a
+    512-token prefill against the oracle in the prefill's declared precision, then four greedy
+    steps and a 5-token verify pass (the small-batch launches in input slices at K = 5120), every
+    row against the oracle's fp64 forward over its own cache."""
+    d = synth(workdir, "qwen2.5-32b-2l", configs.with_layers(configs.QWEN2_5_32B, 2), 106)
+    n = 512
+    ids = np.random.default_rng(6).integers(0, 152064, n).astype(np.int32)
+    with mlxr.Transformer(d, context_length=2048) as m:
+        say("config 5 dense: persistent step", m.persistent_decode, m.persistent_decode_reason)
+        ref = oracle.Model(d, m.max_seq)
+        got = m.forward(ids, 0)
+        # the 4-bit model prefill's declared precision (the tile GEMM's f16 x, modelled by the
+        # oracle for chunks of more than 8 tokens): at this width its own distance to the fp64
+        # forward is ~2.3e-2 (27648-input down projection), so the fp64 comparison runs in the
+        # decode steps and the verify pass below, which are fp32-level
+        want = ref.forward(ids, 0, small_t=8)
+        say("config 5 dense: prefill max |d logit| vs the declared precision", float(np.max(np.abs(got - want))))
+        tok = m.prefill(ids, 0, GREEDY)
+        amb = check_step(got, want, tok, "prefill")
+        for i in range(4):
+            nxt = m.finish(m.begin_decode_step(n + i, GREEDY))
+            want = ref.forward(np.array([tok], np.int32), n + i)
+            amb += check_step(m.step_logits(), want, nxt, f"step {i}")
+            tok = nxt
+        say("config 5 dense: undecidable steps", amb)
+        assert amb <= 1
+        batch = np.concatenate([[tok], ids[10:14]]).astype(np.int32)
+        rows = m.forward(batch, n + 4, all_logits=True)
+        for i in range(5):
+            want = ref.forward(batch[i:i + 1], n + 4 + i)
+            err = float(np.max(np.abs(rows[i] - want)))
+            assert err < LOGIT_TOL, ("verify row", i, err)
 
 
 def test_config5_qwen2_5_32b_sparse_32k_prefix_reuse(gpu, workdir):

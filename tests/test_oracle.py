@@ -61,10 +61,6 @@ def test_qlinear_against_numpy(bits, gs):
     assert np.allclose(q.matmul_f64(x), ref, rtol=1e-6, atol=1e-6)
     for r in (0, 7, 23):
         assert np.array_equal(q.dequant_row(r), fx.dense()[r])
-    # bf16 precision: numpy rounding of both operands, float64 product
-    xb = bf16_to_f32(bf16_round(x)).astype(np.float64)
-    wb = bf16_to_f32(bf16_round(fx.dense())).astype(np.float64)
-    assert np.allclose(q.matmul_bf16(x), xb @ wb.T, rtol=1e-6, atol=1e-6)
 
 
 def test_round_f16_matches_numpy():
@@ -108,8 +104,8 @@ def test_qlinear_f16_precision(gs):
     assert np.all(np.abs(got - exact) <= bound)
     assert np.array_equal(got[2], np.zeros(O, np.float32))
     assert np.array_equal(q.matmul_prefill(x), got)
-    fx3 = QuantFixture(8, 128, 3, 32, seed=1, fast=True)
-    assert np.array_equal(fx3.oracle(oracle).matmul_prefill(x[:, :128]), fx3.oracle(oracle).matmul_bf16(x[:, :128]))
+    fx3 = QuantFixture(8, 128, 3, 32, seed=1, fast=True)   # other widths: the fp32-level product
+    assert np.array_equal(fx3.oracle(oracle).matmul_prefill(x[:, :128]), fx3.oracle(oracle).matmul_f64(x[:, :128]))
 
 
 def test_qlinear_special_cases():
