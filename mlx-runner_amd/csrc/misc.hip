@@ -400,112 +400,201 @@ hipError_t launch_silu_mul(const float* gu, float* out, int I, int T, hipStream_
     return hipGetLastError();
 }
 
-// ---- token selection (Kernels.swift:2362-2619) ----
-// Block maxima: one wave per block of 256 logits (4 contiguous per lane); lowest index of the max.
-constexpr int SMP_BLK = 256;
-__device__ __forceinline__ void smp_block(const float* logits, int V, int b, int lane, float& m, int& idx) {
-    const int i0 = b * SMP_BLK + lane * 4;
-    float best = -INFINITY; int bi = 0x7fffffff;
-    for (int j = 0; j < 4; j++) {
-        const int i = i0 + j;
-        if (i < V) { const float v = logits[i]; if (v > best) { best = v; bi = i; } }
-    }
-    m = wave_max(best);
-    int cand = best == m ? bi : 0x7fffffff;
+// ---- token selection (semantics: Kernels.swift:2362-2619, Engine.swift:112-173) ----
+//
+// Every comparison goes through one 64-bit selection key per logit: the value's order-preserving
+// bits in the high word (NaN mapped below every number, so it is never selected while any number
+// is present) and the complement of the index in the low word, so the larger key is the larger
+// value and, among equal values, the lower index. A maximum over keys is therefore the argmax with
+// the lowest index on ties, and keys are distinct, so a sort by key is a strict total order.
+constexpr int SEL_SPAN = 256;     // logits per span of the first pass (one wave, 4 per lane)
+constexpr int SEL_POOL = 1024;    // exact top-k limit (and the candidate pool of the sampled path)
+
+__device__ __forceinline__ uint32_t sel_order(float v) {
+    if (v != v) return 0u;
+    const uint32_t u = __float_as_uint(v);
+    return (u >> 31) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ uint64_t sel_key(float v, int i) { return ((uint64_t)sel_order(v) << 32) | (uint32_t)~(uint32_t)i; }
+__device__ __forceinline__ float sel_value(uint64_t k) {
+    const uint32_t o = (uint32_t)(k >> 32);
+    return __uint_as_float((o >> 31) ? (o & 0x7fffffffu) : ~o);
+}
+__device__ __forceinline__ int sel_index(uint64_t k) { return (int)~(uint32_t)k; }
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) cand = min(cand, __shfl_xor(cand, o, 64));
-    idx = cand;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t p = __shfl_xor(k, o, 64);
+        k = p > k ? p : k;
+    }
+    return k;
+}
+// span b's maximum key, the whole wave (lanes read 4 consecutive logits)
+__device__ __forceinline__ uint64_t span_max_key(const float* logits, int V, int b, int lane) {
+    const int i = b * SEL_SPAN + 4 * lane;
+    uint64_t k = 0;
+    if (i + 4 <= V) {
+        const float4 v = *reinterpret_cast<const float4*>(logits + i);
+        k = max(max(sel_key(v.x, i), sel_key(v.y, i + 1)), max(sel_key(v.z, i + 2), sel_key(v.w, i + 3)));
+    } else {
+        for (int j = i; j < V; j++) k = max(k, sel_key(logits[j], j));
+    }
+    return wave_max_key(k);
+}
+__device__ __forceinline__ void span_store(const SampleArgs& a, int b, uint64_t k) {
+    a.bmax[b] = sel_value(k); a.barg[b] = sel_index(k);
 }
 
-__global__ __launch_bounds__(256) void sample_blocks_kernel(const float* logits, int V, float* bmax, int* barg) {
-    const int nb = (V + SMP_BLK - 1) / SMP_BLK;
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+__global__ __launch_bounds__(256) void sample_blocks_kernel(SampleArgs a) {
+    const int nb = (a.V + SEL_SPAN - 1) / SEL_SPAN, b = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= nb) return;
-    float m; int idx;
-    smp_block(logits, V, b, threadIdx.x & 63, m, idx);
-    if ((threadIdx.x & 63) == 0) { bmax[b] = m; barg[b] = idx; }
+    const uint64_t k = span_max_key(a.logits, a.V, b, threadIdx.x & 63);
+    if ((threadIdx.x & 63) == 0) span_store(a, b, k);
 }
 
-// One workgroup: repetition penalty over the last `window` distinct tokens, then the greedy argmax
-// (temperature <= 0.001) or the sampled draw (top-k / min-p / top-p, xorshift64).
-constexpr int SMP_CAP = 1024;
-__device__ __forceinline__ uint32_t smp_key(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ void smp_emit(const SampleArgs& a, int pos, int tok, int st) {
+__device__ __forceinline__ void emit_token(const SampleArgs& a, int pos, int tok, int st) {
     a.hist[pos + 1] = tok; a.status[pos + 1] = st;
     if (a.host_tok) { a.host_tok[(pos + 1) & a.ring_mask] = tok; a.host_status[(pos + 1) & a.ring_mask] = st; }
     if (a.dpos_next) *a.dpos_next = pos + 1;
 }
 
+constexpr int SEL_STAGE = 2048;   // penalised tokens staged per round
+constexpr int SEL_MAXSPANS = 1024;
+
+// Repetition penalty over the distinct tokens among hist[pos - window + 1 .. pos]: v > 0 -> v / p,
+// else v * p, once per token. Every occurrence of a token computes the same new value from the
+// same old one, so the round reads all its tokens' logits before any is written, and duplicates
+// within a round then write identical values; a token already seen in an earlier round (windows
+// longer than one round) is skipped. The spans holding penalised tokens are marked in a bitmap and
+// their maxima recomputed once each.
+__device__ void apply_penalty(const SampleArgs& a, int pos, int* tok, float* nval, uint32_t* touched) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6, V = a.V;
+    const int n = min(a.window, pos + 1), nb = (V + SEL_SPAN - 1) / SEL_SPAN;
+    for (int i = tid; i < SEL_MAXSPANS / 32; i += blockDim.x) touched[i] = 0u;
+    for (int r0 = 0; r0 < n; r0 += SEL_STAGE) {
+        const int r1 = min(n, r0 + SEL_STAGE);
+        for (int j = r0 + tid; j < r1; j += blockDim.x) {
+            const int t = a.hist[pos - j];
+            bool fresh = t >= 0 && t < V;
+            for (int e = 0; fresh && e < r0; e++) fresh = a.hist[pos - e] != t;   // seen in an earlier round
+            tok[j - r0] = fresh ? t : -1;
+            if (fresh) {
+                const float v = a.logits[t];
+                nval[j - r0] = v > 0.0f ? v / a.penalty : v * a.penalty;
+                atomicOr(&touched[(t / SEL_SPAN) >> 5], 1u << ((t / SEL_SPAN) & 31));
+            }
+        }
+        __syncthreads();
+        for (int j = tid; j < r1 - r0; j += blockDim.x)
+            if (tok[j] >= 0) a.logits[tok[j]] = nval[j];
+        __threadfence_block();
+        __syncthreads();
+    }
+    // one wave per touched span
+    for (int w = 0; w < (nb + 31) / 32; w++) {
+        uint32_t bits = touched[w];
+        int q = 0;
+        while (bits) {
+            const int bit = __builtin_ctz(bits);
+            bits &= bits - 1;
+            if (q++ % nw != wave) continue;
+            const uint64_t k = span_max_key(a.logits, V, 32 * w + bit, lane);
+            if (lane == 0) span_store(a, 32 * w + bit, k);
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
+}
+
+// Descending bitonic sort of 64 keys across the lanes of a wave (lane i ends with rank i).
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane) {
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+        for (int d = size >> 1; d > 0; d >>= 1) {
+            const uint64_t p = __shfl_xor(k, d, 64);
+            // the lower lane of a pair keeps the larger key in a descending run, the smaller in an
+            // ascending one; runs alternate direction until the last stage
+            const bool lower = (lane & d) == 0, desc = size == 64 || (lane & size) == 0;
+            k = (lower == desc) ? (p > k ? p : k) : (p < k ? p : k);
+        }
+    return k;
+}
+
+// The sampled draw over the sorted top n (keys[0] the largest): probabilities exp((v - M) / T),
+// min-p then top-p cuts, one xorshift64 draw r = (s >> 40) / 2^24 walked down the kept mass. The
+// sums run sequentially in rank order (the reference's rounding, hence its draws for a seed).
+__device__ int draw_token(const SampleArgs& a, const uint64_t* keys, const float* prob, int n, int minp_cut) {
+    float mass = 0.0f;
+    for (int i = 0; i < n; i++) mass += prob[i];
+    int keep = minp_cut;
+    if (a.top_p < 1.0f) {
+        float run = 0.0f;
+        int i = 0;
+        while (i < keep) {
+            run += prob[i] / mass;
+            i++;
+            if (run >= a.top_p) { keep = i; break; }
+        }
+    }
+    keep = keep < 1 ? 1 : keep;
+    float kept = 0.0f;
+    for (int i = 0; i < keep; i++) kept += prob[i];
+    uint64_t st = a.rng[0];
+    st ^= st << 13; st ^= st >> 7; st ^= st << 17;
+    a.rng[0] = st;
+    float r = (float)(st >> 40) * (1.0f / 16777216.0f);
+    for (int i = 0; i < keep; i++) {
+        r -= prob[i] / kept;
+        if (r <= 0.0f) return sel_index(keys[i]);
+    }
+    return sel_index(keys[keep - 1]);
+}
+
+// One workgroup of 1024 threads: penalty, the maximum over the span maxima, then the greedy token
+// (temperature <= 0.001) or the sampled one.
 __global__ __launch_bounds__(1024) void sample_token_kernel(SampleArgs a) {
-    __shared__ float shf[16];
-    __shared__ int shi[16];
+    __shared__ uint64_t red[16];
     __shared__ uint32_t hist_cnt[256];
     __shared__ uint32_t pick[2];
-    __shared__ uint64_t cand[SMP_CAP];
-    __shared__ float prob[SMP_CAP];
-    __shared__ int ncand;
+    __shared__ uint64_t pool[SEL_POOL];
+    __shared__ uint64_t ranked[SEL_POOL];
+    __shared__ float prob[SEL_POOL];
+    __shared__ int tokbuf[SEL_STAGE];
+    __shared__ float valbuf[SEL_STAGE];
+    __shared__ uint32_t touched[SEL_MAXSPANS / 32];
     __shared__ uint32_t sgt[16], seq_[16];
+    __shared__ int minp_first, nfin;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
     const int V = a.V, pos = *a.dpos;
-    float* logits = a.logits;
-    const int nb = (V + SMP_BLK - 1) / SMP_BLK;
-    if (a.penalty != 1.0f) {
-        const int n = min(a.window, pos + 1);
-        for (int j = tid; j < n; j += blockDim.x) {
-            const int t = a.hist[pos - j];
-            bool dup = false;
-            for (int j2 = 0; j2 < j; j2++) dup = dup || (a.hist[pos - j2] == t);
-            if (!dup && t >= 0 && t < V) { const float v = logits[t]; logits[t] = v > 0.0f ? v / a.penalty : v * a.penalty; }
-        }
-        __threadfence_block();
-        __syncthreads();
-        for (int j = wave; j < n; j += nw) {
-            const int t = a.hist[pos - j];
-            bool dup = false;
-            for (int j2 = 0; j2 < j; j2++) dup = dup || (a.hist[pos - j2] == t);
-            if (dup || t < 0 || t >= V) continue;
-            float m; int idx;
-            smp_block(logits, V, t / SMP_BLK, lane, m, idx);
-            if (lane == 0) { a.bmax[t / SMP_BLK] = m; a.barg[t / SMP_BLK] = idx; }
-        }
-        __threadfence_block();
-        __syncthreads();
-    }
-    // maximum and its lowest index over the block maxima (ascending blocks, strictly greater wins)
-    float best = -INFINITY; int bi = 0x7fffffff;
-    for (int b = tid; b < nb; b += blockDim.x) { const float v = a.bmax[b]; if (v > best) { best = v; bi = a.barg[b]; } }
-    const float wm = wave_max(best);
-    int wi = best == wm ? bi : 0x7fffffff;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) wi = min(wi, __shfl_xor(wi, o, 64));
-    if (lane == 0) { shf[wave] = wm; shi[wave] = wi; }
+    const float* logits = a.logits;
+    const int nb = (V + SEL_SPAN - 1) / SEL_SPAN;
+    if (a.penalty != 1.0f && a.window > 0) apply_penalty(a, pos, tokbuf, valbuf, touched);
+    uint64_t best = 0;
+    for (int b = tid; b < nb; b += blockDim.x) best = max(best, sel_key(a.bmax[b], a.barg[b]));
+    best = wave_max_key(best);
+    if (lane == 0) red[wave] = best;
     __syncthreads();
-    float M = -INFINITY; int argmax = 0x7fffffff;
-    for (int w = 0; w < nw; w++) {
-        if (shf[w] > M) { M = shf[w]; argmax = shi[w]; }
-        else if (shf[w] == M && shi[w] < argmax) argmax = shi[w];
-    }
-    if (!isfinite(M)) {
-        if (tid == 0) smp_emit(a, pos, 0, 1);
+    uint64_t top = 0;
+    for (int w = 0; w < nw; w++) top = max(top, red[w]);
+    const float M = sel_value(top);
+    if ((uint32_t)(top >> 32) == 0u || !isfinite(M)) {
+        if (tid == 0) emit_token(a, pos, 0, 1);
         return;
     }
     if (a.temperature <= 0.001f) {
-        if (tid == 0) smp_emit(a, pos, argmax, 0);
+        if (tid == 0) emit_token(a, pos, sel_index(top), 0);
         return;
     }
-    // Sampled: exact top-k (k <= SMP_CAP, lowest index first among equal values) by an 8-bit radix
-    // select of the k-th largest key over all V logits, then a stable gather and a bitonic sort.
-    const int k = min(a.top_k > 0 ? min(a.top_k, V) : min(512, V), SMP_CAP);
+    // Sampled: exact top-k (k <= SEL_POOL, lowest index first among equal values) by an 8-bit radix
+    // select of the k-th largest order key over all V logits, then a stable gather.
+    const int k = min(a.top_k > 0 ? min(a.top_k, V) : min(512, V), SEL_POOL);
     uint32_t prefix = 0, mask = 0, want = (uint32_t)k;
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (int i = tid; i < 256; i += blockDim.x) hist_cnt[i] = 0;
         __syncthreads();
         for (int n = tid; n < V; n += blockDim.x) {
-            const uint32_t key = smp_key(logits[n]);
+            const uint32_t key = sel_order(logits[n]);
             if ((key & mask) == prefix) atomicAdd(&hist_cnt[(key >> shift) & 255u], 1u);
         }
         __syncthreads();
@@ -524,7 +613,7 @@ __global__ __launch_bounds__(1024) void sample_token_kernel(SampleArgs a) {
     const int chunk = (V + blockDim.x - 1) / blockDim.x;
     const int n0 = min(V, tid * chunk), n1 = min(V, n0 + chunk);
     uint32_t gt = 0, eq = 0;
-    for (int n = n0; n < n1; n++) { const uint32_t key = smp_key(logits[n]); gt += key > prefix; eq += key == prefix; }
+    for (int n = n0; n < n1; n++) { const uint32_t key = sel_order(logits[n]); gt += key > prefix; eq += key == prefix; }
     // exclusive scans over threads (wave scan then across waves)
     uint32_t gx = gt, ex = eq;
 #pragma unroll
@@ -538,60 +627,55 @@ __global__ __launch_bounds__(1024) void sample_token_kernel(SampleArgs a) {
     for (int w = 0; w < wave; w++) { gbase += sgt[w]; ebase += seq_[w]; }
     uint32_t gtot = 0; for (int w = 0; w < nw; w++) gtot += sgt[w];
     uint32_t gb = gbase + gx - gt, eb = ebase + ex - eq;
+    for (int i = tid; i < SEL_POOL; i += blockDim.x) pool[i] = 0;   // padding: below every real key
+    __syncthreads();
     for (int n = n0; n < n1; n++) {
         const float v = logits[n];
-        const uint32_t key = smp_key(v);
+        const uint32_t key = sel_order(v);
         int slot = -1;
         if (key > prefix) slot = (int)(gb++);
         else if (key == prefix) { if (eb < want) slot = (int)(gtot + eb); eb++; }
-        if (slot >= 0 && slot < SMP_CAP) cand[slot] = ((uint64_t)key << 32) | (uint64_t)(~(uint32_t)n);
+        if (slot >= 0 && slot < SEL_POOL) pool[slot] = sel_key(v, n);
     }
-    if (tid == 0) ncand = k;
-    for (int i = k + tid; i < SMP_CAP; i += blockDim.x) cand[i] = 0;
+    if (tid == 0) { minp_first = k; nfin = k; }
     __syncthreads();
-    // bitonic sort descending (value, then lowest index): keys are distinct
-    for (int size = 2; size <= SMP_CAP; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int q = tid; q < SMP_CAP / 2; q += blockDim.x) {
-                const int i = (q / stride) * (stride * 2) + (q % stride), j = i + stride;
-                const bool desc = (i & size) == 0;
-                const uint64_t x = cand[i], y = cand[j];
-                if ((x < y) == desc) { cand[i] = y; cand[j] = x; }
-            }
-            __syncthreads();
-        }
+    // sort: each wave sorts its 64 keys in registers, then every key's rank is its place in its
+    // own run plus, for every other run, how many of that run's keys are larger (binary search)
+    const uint64_t mine = wave_sort_desc(pool[tid], lane);
+    __syncthreads();
+    pool[tid] = mine;
+    __syncthreads();
+    int rank = lane;
+    for (int w = 0; w < nw; w++) {
+        if (w == wave) continue;
+        const uint64_t* run = pool + 64 * w;
+        int lo = 0, hi = 64;
+        while (lo < hi) { const int mid = (lo + hi) >> 1; if (run[mid] > mine) lo = mid + 1; else hi = mid; }
+        rank += lo;
     }
-    const int n = ncand;
+    if (rank < k) ranked[rank] = mine;
+    __syncthreads();
+    // candidates end at the first non-finite value (NaN or -inf: never drawn)
+    if (tid < k && !isfinite(sel_value(ranked[tid]))) atomicMin(&nfin, tid);
+    __syncthreads();
+    const int n = nfin;
     const float invT = 1.0f / a.temperature;
-    for (int i = tid; i < n; i += blockDim.x) {
-        const uint32_t key = (uint32_t)(cand[i] >> 32);
-        const uint32_t u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
-        prob[i] = expf((__uint_as_float(u) - M) * invT);
-    }
+    if (tid < n) prob[tid] = expf((sel_value(ranked[tid]) - M) * invT);
+    __syncthreads();
+    // min-p: the first rank whose probability falls below min_p * prob[0]
+    if (a.min_p > 0.0f && tid < n && prob[tid] < a.min_p * prob[0]) atomicMin(&minp_first, tid);
     __syncthreads();
     if (tid == 0) {
-        float total = 0.0f;
-        for (int i = 0; i < n; i++) total += prob[i];
-        int cut = n;
-        if (a.min_p > 0.0f) { const float th = a.min_p * prob[0]; for (int i = 0; i < n; i++) if (prob[i] < th) { cut = i; break; } }
-        if (a.top_p < 1.0f) { float acc = 0.0f; for (int i = 0; i < cut; i++) { acc += prob[i] / total; if (acc >= a.top_p) { cut = i + 1; break; } } }
-        cut = max(1, cut);
-        float tot = 0.0f;
-        for (int i = 0; i < cut; i++) tot += prob[i];
-        uint64_t st = a.rng[0];
-        st ^= st << 13; st ^= st >> 7; st ^= st << 17;
-        a.rng[0] = st;
-        float r = (float)(st >> 40) * (1.0f / 16777216.0f);
-        int chosen = (int)(~(uint32_t)cand[cut - 1]);
-        for (int i = 0; i < cut; i++) { r -= prob[i] / tot; if (r <= 0.0f) { chosen = (int)(~(uint32_t)cand[i]); break; } }
+        const int chosen = draw_token(a, ranked, prob, n, min(minp_first, n));
         if (a.diag) { a.diag[0] = n; a.diag[1] = 1; }
-        smp_emit(a, pos, chosen, 0);
+        emit_token(a, pos, chosen, 0);
     }
 }
 
 hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
-    const int nb = (a.V + SMP_BLK - 1) / SMP_BLK;
-    hipLaunchKernelGGL(sample_blocks_kernel, dim3((nb + 3) / 4), dim3(256), 0, s, (const float*)a.logits, a.V, a.bmax, a.barg);
+    const int nb = (a.V + SEL_SPAN - 1) / SEL_SPAN;
+    if (nb > SEL_MAXSPANS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(sample_blocks_kernel, dim3((nb + 3) / 4), dim3(256), 0, s, a);
     hipLaunchKernelGGL(sample_token_kernel, dim3(1), dim3(1024), 0, s, a);
     return hipGetLastError();
 }

@@ -775,6 +775,33 @@ def test_greedy_ties_and_penalty(gpu):
         assert sample_gpu(gpu, l, p, history=hist)[0] == [300]
 
 
+def test_penalty_long_window_and_nan(gpu):
+    """The repetition penalty over a window longer than one staging round (5000 of 6000 history
+    entries, tokens repeated within and across rounds) penalises each distinct token once: the
+    greedy token equals the oracle's penalised argmax, and so does the penalised logits' span
+    maximum (a penalised top token loses to the next). A NaN logit is never selected (the
+    reference's comparisons skip it)."""
+    V = 32768
+    l = test_logits(V, seed=5)
+    rng = np.random.default_rng(0)
+    hist = rng.integers(0, V, 6000).astype(np.int32)
+    top = np.argsort(-l)[:12]
+    hist[-3:] = top[0]            # the top token in the first round, three times
+    hist[-2500] = top[0]          # and again in the second round
+    hist[-4000] = top[1]          # the second one only in the second round
+    hist[-100] = top[2]; hist[-4100] = top[2]
+    for window in (64, 2048, 2049, 5000):
+        p = gpu.SamplingParameters(temperature=0, repetition_penalty=1.7, repetition_window=window)
+        ids, _ = oracle.sample_distribution(l, hist[-window:], 0, 40, 1, 0, 1.7)
+        assert sample_gpu(gpu, l, p, history=hist.tolist())[0] == [int(ids[0])], window
+    ln = l.copy()
+    best = int(np.argmax(l))
+    ln[best - 1] = np.nan
+    assert sample_gpu(gpu, ln, gpu.SamplingParameters(temperature=0))[0] == [best]
+    toks, _ = sample_gpu(gpu, ln, gpu.SamplingParameters(temperature=5.0, top_k=1000), draws=50)
+    assert best - 1 not in toks
+
+
 def test_non_finite_logits_reported(gpu):
     l = test_logits(4096)
     l[7] = np.inf
