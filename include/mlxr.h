@@ -76,8 +76,24 @@ int mlxr_num_layers(const mlxr_model* m);
 int64_t mlxr_weight_bytes(const mlxr_model* m);
 int64_t mlxr_device_bytes(const mlxr_model* m);
 const char* mlxr_quant_description(const mlxr_model* m);   /* e.g. "q4g64" (Linear.description) */
-int mlxr_sparse_available(const mlxr_model* m);            /* Transformer.sparseAvailable (:765) */
+int mlxr_sparse_available(const mlxr_model* m);            /* Transformer.sparseAvailable (:815) */
+/* Transformer.sparseLayerCount (:818): layers that decode sparse (every layer when available). */
+int mlxr_sparse_layer_count(const mlxr_model* m);
+/* Transformer.sparseOffReason (:821, set at :1029-1031): why a model opened with sparse attention
+ * decodes densely ("" otherwise); valid until the model closes. */
+const char* mlxr_sparse_off_reason(const mlxr_model* m);
 int mlxr_written_high(const mlxr_model* m);                /* Transformer.writtenHigh (:665) */
+/* config.modelType (ModelConfig.swift:39, lower-cased); valid until the model closes. */
+const char* mlxr_model_type(const mlxr_model* m);
+/* config.eosTokenIds (ModelConfig.swift:284-291: config.json and generation_config.json, each a
+ * number or a list, deduplicated; ascending here): copies up to cap ids to out, returns how many
+ * there are. */
+int mlxr_eos_token_ids(const mlxr_model* m, int32_t* out, int cap);
+/* config.isHybrid (ModelConfig.swift:125): always 0, no linear-attention architecture loads. */
+int mlxr_is_hybrid(const mlxr_model* m);
+/* supportsBatchedVerify (Transformer.swift:842-847): 1 when a forward of 2..8 tokens with all
+ * logits runs the batched verify pass (every projection of every loadable model does). */
+int mlxr_supports_batched_verify(const mlxr_model* m);
 
 /* ---------------------------------------------------------------- the step API */
 /* The isCancelled closure of forward / prefill (Transformer.swift:1118,1224): called with `user`
@@ -105,6 +121,12 @@ int mlxr_step_logits(mlxr_model* m, const float** logits_out);
  * position offset (written by the previous step's sampler or by prefill) without waiting. Steps
  * must be begun and finished in position order, at most two in flight. */
 int mlxr_begin_decode(mlxr_model* m, int offset, const mlxr_sample_params* sp, mlxr_step* out);
+/* beginSteps(_:offset:sample:) (Transformer.swift:1265-1296): writes tokens to positions
+ * offset..offset+n-1 and commits one step over them whose token (selected on the GPU from the
+ * last row) lands at offset + n, without waiting. Nothing may be in flight; the returned step
+ * (offset = offset + n - 1) counts as one for the in-flight limit and is finished with
+ * mlxr_finish. Draft models use it to catch up on the tokens the target accepted. */
+int mlxr_begin_steps(mlxr_model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, mlxr_step* out);
 /* finish(_:) (Transformer.swift:1298-1303): waits and returns the token at offset + 1. */
 int mlxr_finish(mlxr_model* m, const mlxr_step* step, int32_t* token_out);
 /* reusablePrefix(_:previousLength:) (Transformer.swift:1193-1209). */

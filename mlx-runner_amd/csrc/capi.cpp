@@ -112,7 +112,18 @@ int64_t mlxr_weight_bytes(const mlxr_model* m) { return m ? m->m->weight_bytes :
 int64_t mlxr_device_bytes(const mlxr_model* m) { return m ? m->m->device_bytes : 0; }
 const char* mlxr_quant_description(const mlxr_model* m) { return m ? m->m->quant_desc.c_str() : ""; }
 int mlxr_sparse_available(const mlxr_model* m) { return m && m->m->sparse_alloc ? 1 : 0; }
+int mlxr_sparse_layer_count(const mlxr_model* m) { return m && m->m->sparse_alloc ? m->m->cfg.L : 0; }
+const char* mlxr_sparse_off_reason(const mlxr_model* m) { return m ? m->m->sparse_off.c_str() : ""; }
 int mlxr_written_high(const mlxr_model* m) { return m ? m->m->written_high : 0; }
+const char* mlxr_model_type(const mlxr_model* m) { return m ? m->m->cfg.model_type.c_str() : ""; }
+int mlxr_eos_token_ids(const mlxr_model* m, int32_t* out, int cap) {
+    if (!m) return 0;
+    const auto& e = m->m->cfg.eos;
+    for (int i = 0; out && i < cap && i < (int)e.size(); i++) out[i] = e[i];
+    return (int)e.size();
+}
+int mlxr_is_hybrid(const mlxr_model* m) { (void)m; return 0; }
+int mlxr_supports_batched_verify(const mlxr_model* m) { return m ? 1 : 0; }
 
 int mlxr_forward(mlxr_model* m, const int32_t* tokens, int n, int offset, int all_logits, int dense, const float** logits_out,
                  mlxr_cancel_fn is_cancelled, void* user) {
@@ -131,6 +142,10 @@ int mlxr_step_logits(mlxr_model* m, const float** logits_out) {
 int mlxr_begin_decode(mlxr_model* m, int offset, const mlxr_sample_params* sp, mlxr_step* out) {
     if (!m || !out) return set_error(MLXR_E_INVALID_ARG, "null argument");
     return model_begin_decode(m->m, offset, sp, out);
+}
+int mlxr_begin_steps(mlxr_model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, mlxr_step* out) {
+    if (!m || !out) return set_error(MLXR_E_INVALID_ARG, "null argument");
+    return model_begin_steps(m->m, tokens, n, offset, sp, out);
 }
 int mlxr_finish(mlxr_model* m, const mlxr_step* step, int32_t* token_out) {
     if (!m || !token_out) return set_error(MLXR_E_INVALID_ARG, "null argument");

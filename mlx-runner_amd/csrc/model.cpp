@@ -42,6 +42,25 @@ int parse_config(const std::string& dir, Config& c) {
         if (const Json* tc = o.get("text_config")) for (auto& kv : tc->obj) o.obj.push_back(kv);
     }
     c.model_type = o.strOr("model_type", "");
+    // end-of-sequence ids: config.json's eos_token_id (a number or a list), plus
+    // generation_config.json's, deduplicated (ModelConfig.swift:284-291)
+    {
+        std::vector<int> eos;
+        auto take = [&](const Json& root) {
+            const Json* e = root.get("eos_token_id");
+            if (!e) return;
+            if (e->t == Json::Num) eos.push_back((int)e->num);
+            else if (e->t == Json::Arr)
+                for (const Json& v : e->arr) if (v.t == Json::Num) eos.push_back((int)v.num);
+        };
+        take(o);
+        std::string gtext, gerr;
+        Json g;
+        if (read_file(dir + "/generation_config.json", gtext) && Json::parse(gtext.data(), gtext.size(), g, gerr) && g.t == Json::Obj) take(g);
+        std::sort(eos.begin(), eos.end());
+        eos.erase(std::unique(eos.begin(), eos.end()), eos.end());
+        c.eos = eos;
+    }
     for (auto& ch : c.model_type) ch = (char)tolower(ch);
     static const char* ok_types[] = {"qwen3", "qwen2", "llama", "mistral"};
     bool supported = false;
@@ -594,6 +613,9 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
     // sparse index (Transformer.swift:1009-1063)
     if (sparse) {
         m->sparse = *sparse; sparse_clamp(m->sparse);
+        if (seq < m->sparse.min_context)
+            m->sparse_off = "the context length (" + std::to_string(seq) + ") is below " + std::to_string(m->sparse.min_context) +
+                            " tokens, where it starts";
         if (seq >= m->sparse.min_context) {
             m->sparse_alloc = true; m->sparse_on = true;
             m->sp_max_blocks = seq / 4;
@@ -1081,6 +1103,29 @@ int model_finish(Model* m, const mlxr_step* st, int32_t* tok) {
         return set_error(MLXR_E_GPU, "persistent decode step: a bounded wait expired (step result discarded)");
     }
     return read_ring(m, st->offset + 1, tok);
+}
+
+// beginSteps (Transformer.swift:1265-1296): tokens[0 .. n) go to positions offset .. offset + n - 1
+// and one step is committed over them whose token (at offset + n) is selected on the GPU, without
+// waiting: the first n - 1 tokens run as one pass without logits (the small-batch matvecs, or the
+// prefill GEMMs past 8 tokens), the last as a decode step. Nothing may be in flight; the returned
+// step counts as one for the in-flight limit and is finished like any decode step.
+int model_begin_steps(Model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, mlxr_step* out) {
+    if (n <= 0 || !tokens || n > m->max_batch || offset < 0 || offset + n >= m->max_seq)
+        return set_error(MLXR_E_CONTEXT_FULL, "The context window is full.");
+    if (int rc = check_sample(sp)) return rc;
+    if (int rc = check_tokens(m, tokens, n)) return rc;
+    for (auto& s : m->slots)
+        if (s.busy) return set_error(MLXR_E_INVALID_ARG, "begin_steps needs no step in flight");
+    if (int rc = write_tokens(m, tokens, n, offset)) return rc;
+    if (n > 1) {
+        if (int rc = set_dpos(m, offset)) return rc;
+        const int T = n - 1;
+        if (int rc = T == 1 ? encode_decode(m, nullptr, m->sparse_on, false) : encode_batch(m, T, false, false)) return rc;
+        m->dev_pos_known = -1;   // the pass leaves *dpos where it was; the step below writes it again
+        m->written_high = std::max(m->written_high, offset + T);
+    }
+    return model_begin_decode(m, offset + n - 1, sp, out);
 }
 
 int model_stall_next_step(Model* m) {

@@ -18,6 +18,7 @@ const char* last_error();
 // ModelConfig subset for the qwen3 / qwen2 / llama / mistral families (ModelConfig.swift:149-307).
 struct Config {
     std::string model_type;
+    std::vector<int> eos;          // end-of-sequence ids (config.json + generation_config.json)
     int H = 0, L = 0, nH = 0, nKV = 0, D = 0, I = 0, V = 0, max_pos = 4096;
     float eps = 1e-6f;
     double theta = 10000;
@@ -71,6 +72,7 @@ struct Model {
     int* diag = nullptr;
     // sparse
     bool sparse_alloc = false; bool sparse_on = false;
+    std::string sparse_off;          // why a model opened with sparse attention decodes densely
     mlxr_sparse_cfg sparse{};
     float* sp_scores = nullptr; int* sp_lists = nullptr; int* sp_plan = nullptr; int sp_max_blocks = 0;
     // host staging
@@ -131,6 +133,7 @@ int model_prefill(Model* m, const int32_t* tokens, int n, int offset, const mlxr
 int model_step_logits(Model* m, const float** out);
 int model_begin_decode(Model* m, int offset, const mlxr_sample_params* sp, mlxr_step* out);
 int model_finish(Model* m, const mlxr_step* st, int32_t* tok);
+int model_begin_steps(Model* m, const int32_t* tokens, int n, int offset, const mlxr_sample_params* sp, mlxr_step* out);
 int model_reusable_prefix(Model* m, int common, int prev_len);
 int model_stall_next_step(Model* m);
 int model_seed(Model* m, uint64_t seed);

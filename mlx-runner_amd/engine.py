@@ -351,13 +351,30 @@ class InferenceEngine:
                 return []
             start = time.perf_counter()
             try:
-                out = [d.prefill(history[keep:], keep, greedy_draft)]
+                catch_up = history[keep:]
+                out: List[int] = []
+                if len(catch_up) > 16:   # after long prompt-lookup runs only
+                    out.append(d.prefill(catch_up, keep, greedy_draft))
+                    inflight = d.begin_decode_step(P + 1, greedy_draft) if k > 1 else None
+                else:
+                    inflight = d.begin_steps(catch_up, keep, greedy_draft)
                 self.draft_cached = list(history)
                 draft_checked = P + 1
-                off = P + 1
-                while len(out) < k:
-                    out.append(d.finish(d.begin_decode_step(off, greedy_draft)))
-                    off += 1
+                # the next step is queued before the current one is read back (two in flight)
+                while inflight is not None:
+                    cur, inflight = inflight, None
+                    if cur.offset + 1 < P + k:
+                        try:
+                            inflight = d.begin_decode_step(cur.offset + 1, greedy_draft)
+                        except mlxr.EngineError:
+                            _try_finish(d, cur)
+                            raise
+                    try:
+                        out.append(d.finish(cur))
+                    except mlxr.EngineError:
+                        if inflight is not None:
+                            _try_finish(d, inflight)
+                        raise
                 self.draft_cached += out[:-1]   # the last draft was never processed
                 draft_time += time.perf_counter() - start
                 return out

@@ -77,6 +77,9 @@ def _load():
         "mlxr_prefill": (I, [P, P, I, I, C.POINTER(SampleParams), C.POINTER(C.c_int32), CancelFn, P]),
         "mlxr_step_logits": (I, [P, C.POINTER(C.POINTER(F))]),
         "mlxr_begin_decode": (I, [P, I, C.POINTER(SampleParams), C.POINTER(Step)]),
+        "mlxr_begin_steps": (I, [P, P, I, I, C.POINTER(SampleParams), C.POINTER(Step)]),
+        "mlxr_model_type": (C.c_char_p, [P]), "mlxr_eos_token_ids": (I, [P, P, I]), "mlxr_is_hybrid": (I, [P]),
+        "mlxr_supports_batched_verify": (I, [P]), "mlxr_sparse_layer_count": (I, [P]), "mlxr_sparse_off_reason": (C.c_char_p, [P]),
         "mlxr_finish": (I, [P, C.POINTER(Step), C.POINTER(C.c_int32)]),
         "mlxr_reusable_prefix": (I, [P, I, I]), "mlxr_reset_write_tracking": (V, [P]),
         "mlxr_seed_sampler": (I, [P, C.c_uint64]), "mlxr_set_sparse": (I, [P, C.POINTER(SparseCfg)]),
@@ -370,6 +373,42 @@ class Transformer:
         st = Step()
         check(lib.mlxr_begin_decode(self._h, int(offset), C.byref(sp), C.byref(st)))
         return DecodeStep(st)
+
+    def begin_steps(self, tokens, offset: int, sample: SamplingParameters) -> DecodeStep:
+        """beginSteps (Transformer.swift:1265-1296): tokens at offset.., one step selecting the
+        token after the last, not waited for (finish it like a decode step)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        sp = sample.params(self.vocab_size)
+        st = Step()
+        check(lib.mlxr_begin_steps(self._h, t.ctypes.data, int(t.size), int(offset), C.byref(sp), C.byref(st)))
+        return DecodeStep(st)
+
+    @property
+    def model_type(self) -> str:
+        return lib.mlxr_model_type(self._h).decode()
+
+    @property
+    def eos_token_ids(self) -> list:
+        n = lib.mlxr_eos_token_ids(self._h, None, 0)
+        out = np.zeros(max(n, 1), np.int32)
+        lib.mlxr_eos_token_ids(self._h, out.ctypes.data, n)
+        return out[:n].tolist()
+
+    @property
+    def sparse_layer_count(self) -> int:
+        return lib.mlxr_sparse_layer_count(self._h)
+
+    @property
+    def sparse_off_reason(self) -> str:
+        return lib.mlxr_sparse_off_reason(self._h).decode()
+
+    @property
+    def is_hybrid(self) -> bool:
+        return bool(lib.mlxr_is_hybrid(self._h))
+
+    @property
+    def supports_batched_verify(self) -> bool:
+        return bool(lib.mlxr_supports_batched_verify(self._h))
 
     def finish(self, step: DecodeStep) -> int:
         tok = C.c_int32()

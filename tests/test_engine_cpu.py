@@ -208,6 +208,11 @@ class FakeModel:
         self.inflight.append((offset, t))
         return st
 
+    def begin_steps(self, tokens, offset, sample):
+        assert not self.inflight, "begin_steps needs nothing in flight"
+        self._run(list(tokens), offset, None)
+        return self.begin_decode_step(offset + len(tokens) - 1, sample)
+
     def finish(self, step):
         off, t = self.inflight.pop(0)
         assert off == step.offset

@@ -422,3 +422,83 @@ def test_checkpoint_layouts_load_identically(gpu, models, tmp_path):
         la, lb = a.forward(toks, 0), b.forward(toks, 0)
         assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
         assert a.generate(toks, 8, GREEDY) == b.generate(toks, 8, GREEDY)
+
+
+def test_begin_steps_matches_prefill(gpu, models):
+    """beginSteps (Transformer.swift:1265-1296): n tokens written at offset and one step over them
+    whose token the GPU selects, not waited for. begin_steps(tokens) then begin_decode gives the
+    same tokens as prefill of the same tokens then begin_decode, for a single token, a few (the
+    small-batch pass) and more than eight (the prefill GEMMs); a step in flight is refused."""
+    d = models["qwen3"]
+    toks = prompt(60, 1000, seed=41)
+    P = 30
+    with mlxr.Transformer(d, context_length=512) as a, mlxr.Transformer(d, context_length=512) as b:
+        for n in (1, 3, 8, 12):
+            a.reset_write_tracking(); b.reset_write_tracking()
+            want = [b.prefill(toks[:P + n], 0, GREEDY)]
+            for i in range(4):
+                want.append(b.finish(b.begin_decode_step(P + n + i, GREEDY)))
+            a.prefill(toks[:P], 0, GREEDY)
+            st = a.begin_steps(toks[P:P + n], P, GREEDY)
+            assert st.offset == P + n - 1
+            nxt = a.begin_decode_step(P + n, GREEDY)        # queued behind it: two in flight
+            got = [a.finish(st), a.finish(nxt)]
+            for i in range(3):
+                got.append(a.finish(a.begin_decode_step(P + n + 1 + i, GREEDY)))
+            assert got == want, n
+        st = a.begin_decode_step(P, GREEDY)
+        with pytest.raises(mlxr.EngineError):
+            a.begin_steps(toks[:2], P + 1, GREEDY)
+        a.finish(st)
+
+
+def test_engine_draft_model_greedy_is_identical(gpu, models):
+    """Draft-model speculation (Engine.swift:619-669): a draft model catches up through
+    begin_steps and proposes greedy tokens in pipelined steps, the target verifies them in batched
+    passes. With the target's own weights as the draft, the tokens equal plain decoding's and the
+    drafts are accepted."""
+    import engine
+    d = models["qwen3"]
+    ids = list(prompt(40, 1000, seed=44))
+    with mlxr.Transformer(d, context_length=1024) as m, mlxr.Transformer(d, context_length=1024) as dm:
+        p = engine.GenerationParameters(temperature=0.0, repetition_penalty=1.0, max_tokens=40)
+        plain = [e[1] for e in engine.InferenceEngine(m).generate(ids, p) if e[0] == "token"]
+        m.reset_write_tracking()
+        eng = engine.InferenceEngine(m, draft_model=dm)
+        ev = eng.generate(ids, p)
+        spec = [e[1] for e in ev if e[0] == "token"]
+        st = ev[-1][1]
+        assert st.model_draft_tokens and st.accepted_model_draft_tokens > 0, st
+        if spec != plain:   # only where the oracle's top-2 margin cannot decide at the 2e-2 gate
+            i = next(k for k in range(len(plain)) if plain[k] != spec[k])
+            ref = oracle.Model(d, m.max_seq).forward(np.array(ids + plain[:i], np.int32), 0)
+            assert abs(ref[plain[i]] - ref[spec[i]]) < LOGIT_TOL
+
+
+def test_config_getters(gpu, models, tmp_path):
+    """The config members InferenceEngine reads (Engine.swift:322-355): model type, end-of-sequence
+    ids from config.json (a number or a list) and generation_config.json, deduplicated; no hybrid
+    model loads; every loadable model verifies in batches (supportsBatchedVerify)."""
+    import json
+    import shutil
+    d = str(tmp_path / "m")
+    shutil.copytree(models["qwen2"], d)
+    with open(os.path.join(d, "config.json")) as f:
+        cfg = json.load(f)
+    cfg["eos_token_id"] = [7, 5, 7]
+    with open(os.path.join(d, "config.json"), "w") as f:
+        json.dump(cfg, f)
+    with open(os.path.join(d, "generation_config.json"), "w") as f:
+        json.dump({"eos_token_id": 9, "do_sample": True}, f)
+    with mlxr.Transformer(d, context_length=256) as m:
+        assert m.model_type == "qwen2"
+        assert m.eos_token_ids == [5, 7, 9]
+        assert not m.is_hybrid and m.supports_batched_verify
+    with mlxr.Transformer(models["llama"], context_length=256) as m:
+        assert m.model_type == "llama" and m.eos_token_ids == []
+        assert m.sparse_layer_count == 0 and m.sparse_off_reason == ""
+    sp = mlxr.SparseAttention(min_context=1024)
+    with mlxr.Transformer(models["llama"], context_length=256, sparse=sp) as m:   # below where it starts
+        assert not m.sparse_available and m.sparse_layer_count == 0 and "below 1024" in m.sparse_off_reason
+    with mlxr.Transformer(models["llama"], context_length=2048, sparse=sp) as m:
+        assert m.sparse_available and m.sparse_layer_count == 2 and m.sparse_off_reason == ""
