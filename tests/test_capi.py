@@ -69,6 +69,18 @@ def test_malformed_safetensors(tmp_path, model_dir):
         "out of bounds": lambda p: write_st(p, {"x": {"dtype": "F32", "shape": [4], "data_offsets": [0, 16]}}, b"\0" * 8),
         "size mismatch": lambda p: write_st(p, {"x": {"dtype": "F32", "shape": [3], "data_offsets": [0, 16]}}, b"\0" * 16),
         "negative shape": lambda p: write_st(p, {"x": {"dtype": "F32", "shape": [-1], "data_offsets": [0, 0]}}),
+        # the reference's rejectsMalformedHeaders cases (EngineTests.swift:164-178), 16 payload bytes
+        "past end": lambda p: write_st(p, {"a": {"dtype": "F32", "shape": [4], "data_offsets": [0, 1000]}}, b"\0" * 16),
+        "start after end": lambda p: write_st(p, {"a": {"dtype": "F32", "shape": [4], "data_offsets": [8, 0]}}, b"\0" * 16),
+        "negative offset": lambda p: write_st(p, {"a": {"dtype": "F32", "shape": [4], "data_offsets": [-16, 0]}}, b"\0" * 16),
+        "shape bytes": lambda p: write_st(p, {"a": {"dtype": "F32", "shape": [5], "data_offsets": [0, 16]}}, b"\0" * 16),
+        "shape overflow": lambda p: write_st(p, {"a": {"dtype": "F32", "shape": [4611686018427387904, 4],
+                                                       "data_offsets": [0, 16]}}, b"\0" * 16),
+        "negative dim": lambda p: write_st(p, {"a": {"dtype": "F32", "shape": [-4], "data_offsets": [0, 16]}}, b"\0" * 16),
+        "not json": lambda p: open(p, "wb").write(struct.pack("<Q", 8) + b"not json" + b"\0" * 16),
+        # rejectsHugeHeaderLength (EngineTests.swift:186-197)
+        "huge header": lambda p: open(p, "wb").write(struct.pack("<Q", (1 << 64) - 5) + b"\0" * 64),
+        "entry not an object": lambda p: write_st(p, {"a": 3}, b"\0" * 16),
     }
     for name, make in cases.items():
         d = tmp_path / name.replace(" ", "_")
@@ -76,6 +88,31 @@ def test_malformed_safetensors(tmp_path, model_dir):
         (d / "config.json").write_text(cfg)
         make(str(d / "model.safetensors"))
         assert open_err(str(d)).case == "invalidFile", name
+
+
+def test_index_lists_the_shards(tmp_path, model_dir):
+    """WeightStore.shardFiles (GPU.swift:316-330): with model.safetensors.index.json, only the files
+    its weight_map names load, so an unrelated sidecar (here a corrupt one) is never opened; without
+    the index every .safetensors file loads and the corrupt one is rejected. An index that names no
+    existing file falls back to every file."""
+    import shutil
+    def layout(name, index):
+        d = tmp_path / name
+        shutil.copytree(model_dir, d)
+        (d / "optiq_vision.safetensors").write_bytes(struct.pack("<Q", 5) + b"{nope")
+        if index is not None:
+            (d / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": index}))
+        return str(d)
+    ok = layout("indexed", {"model.embed_tokens.weight": "model.safetensors"})
+    bad = layout("plain", None)
+    stale = layout("stale", {"model.embed_tokens.weight": "model-00001-of-00002.safetensors"})
+    assert open_err(bad).case == "invalidFile"
+    assert open_err(stale).case == "invalidFile"
+    if mlxr.device_count() == 0:
+        assert open_err(ok).case == "noMetalDevice"   # past the loader: only the device is missing
+    else:
+        with mlxr.Transformer(ok, 256) as m:
+            assert m.vocab_size > 0
 
 
 def test_config_validation(tmp_path, model_dir):

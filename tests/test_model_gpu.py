@@ -424,6 +424,38 @@ def test_checkpoint_layouts_load_identically(gpu, models, tmp_path):
         assert a.generate(toks, 8, GREEDY) == b.generate(toks, 8, GREEDY)
 
 
+def test_misaligned_tensors_load_identically(gpu, models, tmp_path):
+    """loadsTensorsZeroCopyAndRealignsMisalignedOnes (EngineTests.swift:125-150): a 6-byte F16
+    tensor first leaves the later tensors (codes, scales, norm weights) off their natural alignment
+    in the file; the model loads them realigned and its logits are bit-identical to the aligned
+    file's."""
+    import json
+    import shutil
+    from qfix import read_safetensors, write_safetensors
+    d = models["llama"]
+    src = read_safetensors(os.path.join(d, "model.safetensors"))
+    dt_of = {np.uint32: "U32", np.uint16: "BF16", np.float16: "F16", np.float32: "F32"}
+    out = str(tmp_path / "misaligned")
+    shutil.copytree(d, out)
+    tens = {"a_pad": np.array([1, 2, 3], np.float16)}
+    tens.update(src)
+    hdr, off, blobs = {}, 0, []
+    for k, a in tens.items():
+        b = np.ascontiguousarray(a).tobytes()
+        hdr[k] = {"dtype": dt_of[a.dtype.type], "shape": list(a.shape), "data_offsets": [off, off + len(b)]}
+        off += len(b)
+        blobs.append(b)
+    h = json.dumps(hdr)
+    h += " " * (-(8 + len(h)) % 16)           # data starts 16-byte aligned, as the reference test's does
+    with open(os.path.join(out, "model.safetensors"), "wb") as f:
+        f.write(len(h).to_bytes(8, "little") + h.encode() + b"".join(blobs))
+    starts = [8 + len(h) + v["data_offsets"][0] for k, v in hdr.items() if k != "a_pad"]
+    assert all(s % 4 == 2 for s in starts)   # every tensor after the F16 one starts 2 bytes off
+    toks = prompt(21, 1000, seed=45)
+    with mlxr.Transformer(d, context_length=256) as a, mlxr.Transformer(out, context_length=256) as b:
+        assert np.array_equal(a.forward(toks, 0).view(np.uint32), b.forward(toks, 0).view(np.uint32))
+
+
 def test_begin_steps_matches_prefill(gpu, models):
     """beginSteps (Transformer.swift:1265-1296): n tokens written at offset and one step over them
     whose token the GPU selects, not waited for. begin_steps(tokens) then begin_decode gives the
