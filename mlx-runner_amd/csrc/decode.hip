@@ -1073,12 +1073,16 @@ static const void* pick_kernel(const MegaArgs& a) {
               : (fb4 ? (const void*)decode_step_kernel<8, 4> : (const void*)decode_step_kernel<8, 8>);
 }
 
-// Cooperative launch: every workgroup of the grid is resident at once, or the launch fails (the
-// phases' hand-overs wait for other workgroups' results, so a partly resident grid would stall).
+// A plain launch on the model stream. Co-residency (the phases' hand-overs wait for other
+// workgroups' results) rests on the setup's check that the grid fits the device at the step's LDS
+// size (one workgroup per CU), and every wait is bounded: a grid that is only partly resident (the
+// device shared with other work) ends through the abort path instead of stalling. A cooperative
+// launch would give the same guarantee up front, but the runtime routes it through a queue of its
+// own, ordered against the model stream by markers, and tears that queue down at process exit.
 hipError_t launch_decode_step(const MegaArgs& a, int nwg, size_t lds, hipStream_t s) {
     MegaArgs args = a;
     void* kargs[] = {&args};
-    return hipLaunchCooperativeKernel(pick_kernel(a), dim3(nwg), dim3(MK_THREADS), kargs, (unsigned)lds, s);
+    return hipLaunchKernel(pick_kernel(a), dim3(nwg), dim3(MK_THREADS), kargs, lds, s);
 }
 
 int mega_blocks_per_cu(const MegaArgs& a, size_t lds) {

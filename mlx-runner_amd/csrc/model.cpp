@@ -440,15 +440,12 @@ static int mega_setup(Model* m) {
     if (lds > 158 * 1024) return no("LDS need " + std::to_string(lds >> 10) + " KiB");
     if (mega_set_lds_limit(lds) != hipSuccess) return no("LDS attribute");
     if (nwg > MEGA_MAX_WG) return no("too many workgroups");
-    // co-residency: the phases' hand-overs wait for other workgroups, so the whole grid must be
-    // resident at once (the launch is cooperative and fails rather than stalls otherwise)
+    // co-residency: the phases' hand-overs wait for other workgroups, so the whole grid must fit the
+    // device at once (every wait is bounded, so a grid that still ends up partly resident aborts)
     a.head = m->tile_head;   // the kernel variant follows the group size
     const int per_cu = mega_blocks_per_cu(a, lds);
     if (per_cu < 1 || nwg > per_cu * cus)
         return no("the grid cannot be resident at once (" + std::to_string(per_cu) + " workgroups per CU)");
-    int coop = 0;
-    HIPCHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, 0));
-    if (!coop) return no("no cooperative launch");
     // the layers' repacked phases (tiles_setup), plus the lm_head's
     int rc = MLXR_OK;
     if ((rc = dalloc(m, &m->mega_layers, c.L))) return rc;
