@@ -191,7 +191,7 @@ def prefill_main(a):
 def sweep_main(a):
     """the quantized matvec / GEMM sweep on 8B-shape projections. Weights are random code
     words with random bf16 scales / biases (every bit pattern is a valid code stream at any width;
-    parity is the kernel tests' job), activations N(0, 1). T = 1: the decode matvec (mlxr_k_qmv),
+    parity is the kernel tests' job), activations N(0, 1) rounded to bf16 values (stored fp32). T = 1: the decode matvec (mlxr_k_qmv),
     T = 4: the small-batch kernel (mlxr_k_qmm), T = 512: the prefill GEMM (mlxr_k_qgemm). HIP events
     around `iters` back-to-back calls; bytes = N*K*(b/8 + 4/gs) + T*K*4 + T*N*4, flops = 2*T*N*K."""
     rng = np.random.default_rng(a.seed)
@@ -205,7 +205,9 @@ def sweep_main(a):
             bi = mlxr.DeviceArray.from_numpy((rng.uniform(-0.2, 0.2, (N, K // gs)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
             qm = (mlxr.QMat * 1)(mlxr.QMat(w.ptr, sc.ptr, bi.ptr, None, N))
             for T in (1, 4, 512):
-                x = mlxr.DeviceArray.from_numpy(rng.normal(0, 1, (T, K)).astype(np.float32))
+                xv = rng.normal(0, 1, (T, K)).astype(np.float32)
+                xv = ((xv.view(np.uint32) + 0x7FFF + ((xv.view(np.uint32) >> 16) & 1)) & 0xFFFF0000).view(np.float32)   # bf16 values
+                x = mlxr.DeviceArray.from_numpy(xv)
                 y = mlxr.DeviceArray.zeros((T, N), np.float32)
                 if T == 1:
                     call = lambda: mlxr.lib.mlxr_k_qmv(qm, 1, K, bits, gs, 0, x.ptr, None, 0.0, y.ptr, 0)
@@ -236,8 +238,8 @@ def sweep_main(a):
         "metric": "quantized matvec / GEMM sweep (8B-shape projections, configs[3])",
         "value": round(sum(c["GBs"] for c in dec) / len(dec), 1), "unit": "GB/s (mean over the T = 1 cells)",
         "n_gpus": 1, "steps": len(cells), "warmup": 1, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u3/u4/u6/u8 weights (bf16 scale/bias); fp32 activations and arithmetic at T = 1 and 4; T = 512 on f16 (4-bit, row-scaled x) or bf16 (other widths) MFMA operands, fp32 accumulate",
-        "data": "synthetic: random code words and bf16 scales / biases, N(0,1) activations",
+        "vs_baseline": None, "dtype": "u3/u4/u6/u8 weights (bf16 scale/bias); fp32 activations and arithmetic at T = 1 and 4; T = 512: exact codes and x as f16 hi + lo on the f16 matrix cores (the lo products skipped where x is bf16-valued, as here), group scale / bias in fp32, fp32 accumulate",
+        "data": "synthetic: random code words and bf16 scales / biases, N(0,1) activations rounded to bf16",
         "config": {"workload": "configs[3]: K,N in (4096,14336),(14336,4096),(4096,151936) x 3b g32, 4b g64, 6b g128, 8b g64 x T in 1,4,512"},
         "roofline": {"bound": "hbm", "kernel": f"qmv_kernel, best cell K={best_dec['K']} N={best_dec['N']} {best_dec['bits']}b",
                      "achieved": best_dec["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
