@@ -27,6 +27,7 @@ float* g_xsc = nullptr; size_t g_xsc_elems = 0;
 uint16_t* g_xlo = nullptr; size_t g_xlo_elems = 0;   // the MLX-layout GEMM's pre-pass: x lo part, group sums, lo flags
 float* g_xgs = nullptr; size_t g_xgs_elems = 0;
 int* g_xnz = nullptr; size_t g_xnz_elems = 0;
+uint16_t* g_wsb = nullptr; size_t g_wsb_elems = 0;   // the MLX-layout GEMM's repacked scales
 float* g_bmax = nullptr; int* g_barg = nullptr; int g_blocks = 0;
 hipEvent_t g_t0 = nullptr, g_t1 = nullptr;
 
@@ -255,7 +256,8 @@ int mlxr_k_qgemm(const mlxr_qmat* mat, int K, int bits, int gs, int st, int T, c
     if (int rc = ensure_buf(g_xbf, g_xbf_elems, (size_t)T * K)) return rc;
     if (int rc = ensure_buf(g_xsc, g_xsc_elems, (size_t)T)) return rc;
     if (int rc = ensure_buf(g_xlo, g_xlo_elems, (size_t)T * K)) return rc;
-    if (int rc = ensure_buf(g_xgs, g_xgs_elems, (size_t)T * (K / gs))) return rc;
+    if (int rc = ensure_buf(g_xgs, g_xgs_elems, qgemm_gsum_floats(T, K, gs))) return rc;
+    if (int rc = ensure_buf(g_wsb, g_wsb_elems, qgemm_scale_halves(mat->O, K, gs))) return rc;
     if (int rc = ensure_buf(g_xnz, g_xnz_elems, (size_t)T)) return rc;
     if (!g_qsplit) {
         if (int rc = ensure_buf(g_qsplit, g_qsplit_floats, QGEMM_SPLIT_FLOATS)) return rc;
@@ -263,7 +265,7 @@ int mlxr_k_qgemm(const mlxr_qmat* mat, int K, int bits, int gs, int st, int T, c
     }
     QGemmArgs a; a.m = qmat(*mat); a.K = K; a.bits = bits; a.gs = gs; a.st = st; a.O = mat->O; a.T = T;
     a.x = x; a.x_stride = x_stride; a.y = y; a.y_stride = y_stride; a.xbf = g_xbf; a.xsc = g_xsc;
-    a.xlo = g_xlo; a.xgs = g_xgs; a.xnz = g_xnz;
+    a.xlo = g_xlo; a.xgs = g_xgs; a.xnz = g_xnz; a.wsb = g_wsb;
     a.split = g_qsplit; a.split_floats = g_qsplit_floats;
     return done(launch_qgemm(a, g_stream));
 }

@@ -7,18 +7,24 @@
 //   q * 2^-24 (q < 256 for every width), so no dequantization rounds anything.
 // - x: each token row is multiplied by the power of two 2^e that puts max|x| in [2^13, 2^14)
 //   (exact) and split into f16 hi + lo (x 2^e = hi + lo to ~2^-22 relative). Both enter the same
-//   accumulator (v_mfma_f32_32x32x16_f16), so sum q x is fp32 accumulation of near-exact products.
-//   A tile whose rows all have lo == 0 (inputs that are bf16 values, e.g.) skips the lo products:
-//   they would add exact zeros.
-// - Each quantization group accumulates in its own registers; at the group's end every output
-//   takes  tot = fma(s * 2^24, acc, fma(b, xsum, tot))  in fp32, with xsum = sum of the group's
-//   scaled x (the pre-pass writes it), and the row is multiplied back by 2^-e at the end.
+//   accumulator (v_mfma_f32_32x32x16_f16). A tile whose rows all have lo == 0 (inputs that are
+//   bf16 values, e.g.) skips the lo products: they would add exact zeros.
+// - Each quantization group accumulates into one of two register sets (groups alternate); once the
+//   next group's first products are issued, the finished one is folded in fp32,
+//   tot = fma(s 2^24, acc, tot), so the matrix cores keep working meanwhile.
+// - The bias terms sum_g b[n][g] xsum[m][g] (xsum: the group's sum of scaled x, from the pre-pass)
+//   go through the matrix cores too, 4 groups at a time, straight into tot: xsum as three bf16
+//   parts and b as one (bf16 biases) or two (f16) bf16 parts, every product exact in fp32.
+// - The row is multiplied back by 2^-e at the end.
 //
-// Tiling: a 256-thread workgroup owns 128 tokens x 128 rows; wave (wm, wn) the 64 x 64 quarter as
-// 2 x 2 tiles of 32 x 32. K advances 64 at a time: X hi / lo and the codes (as f16) are staged in
-// LDS (rows padded to 72 halves so that 32 lanes reading 16 bytes of consecutive rows spread over
-// the banks), the next block's global loads are in registers while this block's MFMAs run.
-// Tiles are ordered so the token tiles of one weight tile run on the same XCD (its L2).
+// Tiling: a 512-thread workgroup owns 128 tokens x 256 rows; wave (wm, wn) the 64 x 64 block
+// (2 x 2 tiles of 32 x 32) of tokens 64 wm and rows 64 wn. K advances 64 at a time through three
+// LDS stages filled by buffer -> LDS copies two blocks ahead (no registers hold the prefetch):
+// X hi and lo (16-byte chunks XOR-swizzled by row, so 32 lanes reading 16 bytes of consecutive
+// rows spread over the banks) and the raw code bytes of the 256 rows; the scales, biases and
+// token group sums of 4 groups at a time (repacked by the pre-passes so that such a chunk is a few
+// KB of consecutive bytes) into two more buffers. Tiles are ordered so the token tiles of one
+// weight tile run on the same XCD (its L2).
 #include "kernels.h"
 
 namespace mlxr {
@@ -26,12 +32,32 @@ namespace mlxr {
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 gx_bf8 __attribute__((ext_vector_type(8)));
+typedef uint32_t gx_u4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* gx_lptr;
+__device__ __forceinline__ uint4 gload_u4(const void* p) {
+    const gx_u4 v = gload(reinterpret_cast<const gx_u4*>(p));
+    return uint4{v.x, v.y, v.z, v.w};
+}
 
-constexpr int GX_M = 128, GX_N = 128, GX_K = 64, GX_LD = GX_K + 8;
+constexpr int GX_M = 128, GX_N = 256, GX_K = 64, GX_NST = 3;
+constexpr int GX_RSRC_W3 = 0x00020000;   // raw buffer, 32-bit data format
+// stage layout (bytes): X hi, X lo, codes (256 rows x 8 BITS); after the stages two chunk buffers:
+// scales [256 rows][4] f16, biases [256 rows][4] f16, token group sums [4][128 tokens] f32
+constexpr int GX_XB = GX_M * GX_K * 2;
+constexpr int GX_CB = GX_N * 8 * 2 + GX_M * 16;
+template <int BITS> constexpr int gx_wb() { return GX_N * 8 * BITS; }
+template <int BITS> constexpr int gx_stage() { return 2 * GX_XB + gx_wb<BITS>(); }
+template <int BITS> constexpr int gx_lds() { return GX_NST * gx_stage<BITS>() + 2 * GX_CB; }
+// s_waitcnt vmcnt(n) (n < 64), expcnt and lgkmcnt not waited for
+constexpr int gx_wait_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+// groups padded to a multiple of 4 (one chunk)
+__host__ __device__ constexpr int gx_gpad(int G) { return (G + 3) / 4 * 4; }
 
-// Pre-pass: row t of x -> hi / lo (f16, [T][K]), gsum[t][g] (sum of the scaled group, fp32, summed
-// in k order per 8-chunk and chunks in order), inv[t] = 2^-e, nz[t] = any lo != 0.
-__global__ __launch_bounds__(256) void x_split_kernel(const float* __restrict__ x, int xs, int K, int gs, uint16_t* __restrict__ hi,
+// Pre-pass: row t of x -> hi / lo (f16, [T][K]); gsum[g][t] (each group's sum of the scaled x,
+// summed in k order per 8-chunk and chunks in order; zero past G); inv[t] = 2^-e, nz[t] = any
+// lo != 0.
+__global__ __launch_bounds__(256) void x_split_kernel(const float* __restrict__ x, int xs, int K, int gs, int T, uint16_t* __restrict__ hi,
                                                       uint16_t* __restrict__ lo, float* __restrict__ gsum, float* __restrict__ inv,
                                                       int* __restrict__ nz) {
     extern __shared__ float xsp_part[];   // K / 8 chunk sums
@@ -76,217 +102,360 @@ __global__ __launch_bounds__(256) void x_split_kernel(const float* __restrict__ 
     }
     if (any) anyl = 1;
     __syncthreads();
-    const int cpg = gs >> 3, G = K / gs;
-    for (int g = tid; g < G; g += 256) {
+    const int cpg = gs >> 3, G = K / gs, Gp = gx_gpad(G);
+    for (int g = tid; g < Gp; g += 256) {
         float s = 0.0f;
-        for (int c = 0; c < cpg; c++) s += xsp_part[g * cpg + c];
-        gsum[(int64_t)t * G + g] = s;
+        if (g < G)
+            for (int c = 0; c < cpg; c++) s += xsp_part[g * cpg + c];
+        gsum[(int64_t)g * T + t] = s;
     }
     if (tid == 0) nz[t] = anyl;
 }
 
+// Pre-pass: the scales and biases repacked to [Gp / 4][O][4] (s, then b; their stored 16-bit words,
+// zero past G), so that 4 groups of 256 consecutive rows are 2 KB of consecutive bytes. A workgroup
+// moves 64 rows x 64 groups through LDS: row-contiguous reads, chunk-contiguous writes.
+__global__ __launch_bounds__(256) void scale_repack_kernel(const uint16_t* __restrict__ s, const uint16_t* __restrict__ b, int O, int G,
+                                                            uint16_t* __restrict__ out) {
+    __shared__ uint16_t tile[2][64][66];
+    const int Gp = gx_gpad(G), nc = Gp / 4, tid = threadIdx.x;
+    const int n0 = blockIdx.x * 64, g0 = blockIdx.y * 64;
+#pragma unroll 4
+    for (int i = 0; i < 16; i++) {
+        const int idx = i * 256 + tid, r = idx >> 6, gl = idx & 63, n = n0 + r, g = g0 + gl;
+        const bool in = n < O && g < G;
+        tile[0][r][gl] = in ? s[(int64_t)n * G + g] : 0;
+        tile[1][r][gl] = in ? b[(int64_t)n * G + g] : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int idx = i * 256 + tid, cl = idx >> 6, r = idx & 63, c = g0 / 4 + cl, n = n0 + r;
+        if (c >= nc || n >= O) continue;
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const uint16_t* t = &tile[p][r][4 * cl];
+            reinterpret_cast<uint2*>(out)[(int64_t)p * nc * O + (int64_t)c * O + n] =
+                uint2{(uint32_t)t[0] | ((uint32_t)t[1] << 16), (uint32_t)t[2] | ((uint32_t)t[3] << 16)};
+        }
+    }
+}
+
 struct QGemmXDev {
-    const uint8_t* w; const uint16_t* s; const uint16_t* b; const uint16_t* bias;
+    const uint8_t* w; const uint16_t* sb16; const uint16_t* bias; int st;
     int K, gs, O, T, ys, nT, ntiles;
     const uint16_t* xh; const uint16_t* xl; const float* gsum; const float* inv; const int* nz;
     float* y;
     float* split;             // split over K (gridDim.y slices): tile counters, then the slices' partial tiles
 };
 
-typedef uint32_t gx_u4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 gload_u4(const void* p) {
-    const gx_u4 v = gload(reinterpret_cast<const gx_u4*>(p));
-    return uint4{v.x, v.y, v.z, v.w};
-}
+// K slices: 4 fixed slices (whole blocks, at group boundaries) for inputs of at least 128 blocks;
+// 1 otherwise. The slice count depends on K alone, so a token's result never depends on T or on
+// how the slices are spread over workgroups.
+__host__ __device__ constexpr int qgemm_slices(int K) { return K / GX_K >= 128 ? 4 : 1; }
+
+// A fragment's 8 codes (codes 8 u .. 8 u + 7 of a row's block, its 8 BITS raw bytes at `row`) as
+// f16 subnormals, i.e. q * 2^-24 exactly.
 template <int BITS>
-__device__ __forceinline__ void load_codes32(const uint8_t* p, uint32_t* w) {
+__device__ __forceinline__ half8_t gx_codes(const uint8_t* row, int u) {
+    const int byte = u * BITS, dw = byte >> 2, sh = (byte & 3) * 8;
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(row) + dw;
     if constexpr (BITS == 4) {
-        const uint4 v = gload_u4(p);
-        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        // even codes' bytes and odd codes' bytes, then byte permutes into (even, odd) 16-bit pairs
+        const uint32_t ev = p[0] & 0x0F0F0F0Fu, od = (p[0] >> 4) & 0x0F0F0F0Fu;
+        return __builtin_bit_cast(half8_t, gx_u4{__builtin_amdgcn_perm(od, ev, 0x0C040C00u), __builtin_amdgcn_perm(od, ev, 0x0C050C01u),
+                                                 __builtin_amdgcn_perm(od, ev, 0x0C060C02u), __builtin_amdgcn_perm(od, ev, 0x0C070C03u)});
     } else if constexpr (BITS == 8) {
-        const uint4 a = gload_u4(p), b = gload_u4(p + 16);
-        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+        const uint32_t a = p[0], b = p[1];
+        return __builtin_bit_cast(half8_t, gx_u4{__builtin_amdgcn_perm(0u, a, 0x0C010C00u), __builtin_amdgcn_perm(0u, a, 0x0C030C02u),
+                                                 __builtin_amdgcn_perm(0u, b, 0x0C010C00u), __builtin_amdgcn_perm(0u, b, 0x0C030C02u)});
     } else {
+        uint64_t v = p[0];
+        if constexpr (BITS != 2) v |= (uint64_t)p[1] << 32;   // 8 BITS bits from bit sh may cross into the next dword
+        v >>= sh;
+        constexpr uint32_t M = (1u << BITS) - 1u;
+        uint32_t q[4];
 #pragma unroll
-        for (int i = 0; i < BITS; i++) w[i] = gload(reinterpret_cast<const uint32_t*>(p) + i);
+        for (int i = 0; i < 4; i++)
+            q[i] = (uint32_t)((v >> (2 * i * BITS)) & M) | ((uint32_t)((v >> ((2 * i + 1) * BITS)) & M) << 16);
+        return __builtin_bit_cast(half8_t, gx_u4{q[0], q[1], q[2], q[3]});
     }
 }
-// code j (0..31) of a 32-code run held in BITS words (little-endian bit stream)
-template <int BITS>
-__device__ __forceinline__ uint32_t code_of(const uint32_t* w, int j) {
-    constexpr uint32_t M = (1u << BITS) - 1u;
-    const int bit = j * BITS, wi = bit >> 5, off = bit & 31;
-    if (off + BITS <= 32) return (w[wi] >> off) & M;
-    return ((w[wi] >> off) | (w[wi + 1] << (32 - off))) & M;
-}
 
-// K slices: 4 fixed slices (whole blocks, at group boundaries) for inputs of at least 128 blocks
-// whose group size divides 64 or is a multiple of it; 1 otherwise. The slice count depends on K and
-// gs alone, so a token's result never depends on T or on how the slices are spread over workgroups.
-__host__ __device__ constexpr int qgemm_slices(int K, int gs) {
-    return (K / GX_K >= 128 && (64 % gs == 0 || gs % 64 == 0)) ? 4 : 1;
-}
-
-template <int BITS, int ST, int SF>
-__global__ __launch_bounds__(256, 2) void qgemmx_kernel(QGemmXDev a) {
-    __shared__ __attribute__((aligned(16))) uint16_t Xh[GX_M * GX_LD];
-    __shared__ __attribute__((aligned(16))) uint16_t Xl[GX_M * GX_LD];
-    __shared__ __attribute__((aligned(16))) uint16_t Wq[GX_N * GX_LD];
-    __shared__ __attribute__((aligned(16))) float Gs[2][GX_M];
-    __shared__ float Ss[2][GX_N], Bs[2][GX_N];   // [flush point][row]: s * 2^24, b
-    __shared__ int lo_any;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    // XCD x runs workgroups x, x + 8, ...: give it a contiguous run of tiles, token tiles fastest
-    const int g = blockIdx.x, xcd = g & 7, per = a.ntiles >> 3, rem = a.ntiles & 7;
-    const int tile = xcd * per + min(xcd, rem) + (g >> 3);
+template <int BITS, int GS, int SF, bool LO>
+__device__ __forceinline__ void qgemmx_body(const QGemmXDev& a, uint8_t* lds, int tile) {
+    constexpr int STG = gx_stage<BITS>();
+    constexpr int NCP = 2 + (LO ? 2 : 0) + BITS;   // copies a wave issues per block (a chunk adds 1 at its blocks)
+    constexpr int BPC = 4 * GS / GX_K;              // blocks per chunk of 4 groups (2, 4 or 8)
+    static_assert(NCP < 64 && BPC >= 2, "pipeline");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
     const int ot = tile / a.nT, tt = tile - ot * a.nT;
     const int n0 = ot * GX_N, m0 = tt * GX_M;
-    const int K = a.K, gs = a.gs, G = K / gs;
-    const int64_t rowBytes = (int64_t)K * BITS / 8;
-    if (tid == 0) lo_any = 0;
-    __syncthreads();
-    if (tid < GX_M && m0 + tid < a.T && gload(a.nz + m0 + tid)) lo_any = 1;
-    __syncthreads();
-    const bool has_lo = lo_any != 0;
-    // load roles: row lr of the tile, half lh (32 of the block's 64 k)
-    const int lr = tid >> 1, lh = tid & 1;
-    const int xm = min(m0 + lr, a.T - 1);
-    const bool xvalid = m0 + lr < a.T;
-    const uint16_t* xhrow = a.xh + (int64_t)xm * K + lh * 32;
-    const uint16_t* xlrow = a.xl + (int64_t)xm * K + lh * 32;
-    const int wrow = min(n0 + lr, a.O - 1);
-    const uint8_t* wptr = a.w + wrow * rowBytes + lh * (4 * BITS);
-    // group-sum loads: token gt of the tile for flush point gf (the block's k = 32 or 64); the same
-    // thread loads row gt's scale and bias of that group
-    const int gt = tid & 127, gf = tid >> 7;
-    const float* gsrow = a.gsum + (int64_t)min(m0 + gt, a.T - 1) * G;
-    const int64_t srow = (int64_t)min(n0 + gt, a.O - 1) * G;
+    const int K = a.K, G = K / GS, Gp = gx_gpad(G);
+    constexpr int NJ = 2;                                 // 32-row tiles per wave
+    const uint32_t rowb = (uint32_t)(K / 8 * BITS);     // code bytes per row
+    const __amdgpu_buffer_rsrc_t xhr = __builtin_amdgcn_make_buffer_rsrc((void*)a.xh, 0, a.T * K * 2, GX_RSRC_W3);
+    const __amdgpu_buffer_rsrc_t xlr = __builtin_amdgcn_make_buffer_rsrc((void*)a.xl, 0, a.T * K * 2, GX_RSRC_W3);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (int)((uint32_t)a.O * rowb), GX_RSRC_W3);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void*)a.sb16, 0, Gp * a.O * 4, GX_RSRC_W3);
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc((void*)a.gsum, 0, Gp * a.T * 4, GX_RSRC_W3);
+    uint8_t* cbuf = lds + GX_NST * STG;
 
-    f32x16_t acc[2][2], tot[2][2];
+    // this wave's copies of block blk into its stage (every wave issues NCP of them, in this order)
+    // per-lane parts of the copies' offsets (the rest is uniform): X row lane / 8 of a copy's 8 and
+    // its XOR-swizzled 16-byte chunk; codes (widths whose rows tile a copy's 64 dwords): row lane /
+    // (2 BITS) of the copy's rows, dword lane % (2 BITS). Rows past T or O read past the buffer's
+    // end: zeros.
+    constexpr bool WTILE = 64 % (2 * BITS) == 0;
+    const uint32_t xl_off = (uint32_t)(lane >> 3) * (uint32_t)K * 2u + 16u * (uint32_t)((lane & 7) ^ ((lane >> 3) & 7));
+    const uint32_t wl_off = WTILE ? (uint32_t)(lane / (2 * BITS)) * rowb + 4u * (uint32_t)(lane % (2 * BITS)) : 0u;
+    // this wave's copies of block blk into its stage (every wave issues NCP of them, in this order)
+    auto issue = [&](int blk) {
+        uint8_t* st = lds + (blk % GX_NST) * STG;
+        const uint32_t k0 = (uint32_t)blk * GX_K;
+        // opaque copies: each offset is one add per copy here, not a register kept across the loop
+        uint32_t xo = xl_off, wo = wl_off;
+        int ln = lane;
+        asm volatile("" : "+v"(xo), "+v"(wo), "+v"(ln));
+        // X hi (and lo): 1 KB = 8 rows of 128 bytes per copy
+#pragma unroll
+        for (int h = 0; h < (LO ? 2 : 1); h++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const int q = 2 * wave + c;
+                const uint32_t off = xo + (((uint32_t)(m0 + 8 * q) * (uint32_t)K + k0) * 2u);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(h ? xlr : xhr, (gx_lptr)(st + h * GX_XB + q * 1024), 16, off, 0, 0, 0);
+            }
+        // codes: 256 B per copy, the rows' 8 BITS bytes back to back (dword d of the block: row
+        // d / (2 BITS), dword d % (2 BITS))
+#pragma unroll
+        for (int c = 0; c < BITS; c++) {
+            const int q = wave * BITS + c;
+            uint32_t off;
+            if constexpr (WTILE) {
+                off = wo + ((uint32_t)(n0 + q * 32 / BITS) * rowb + (uint32_t)blk * (8u * BITS));
+            } else {
+                const int d = q * 64 + ln, r = d / (2 * BITS), dw = d - r * 2 * BITS;
+                off = (uint32_t)(n0 + r) * rowb + (uint32_t)blk * (8u * BITS) + 4u * dw;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (gx_lptr)(st + 2 * GX_XB + q * 256), 4, off, 0, 0, 0);
+        }
+    };
+    // chunk ch (groups 4 ch .. 4 ch + 3) into buffer ch & 1: 2 KB of scales, 2 KB of biases (256
+    // rows x 8 bytes), 2 KB of token group sums (4 groups x 128 tokens): six 1 KB copies, waves 6
+    // and 7 repeating waves 0 and 1's (the same bytes to the same place)
+    auto issue_chunk1 = [&](int ch, int q) {
+        uint8_t* cb = cbuf + (ch & 1) * GX_CB;
+        if (q < 4) {
+            const int part = q >> 1, half = q & 1;                      // scales / biases, rows 128 half ..
+            const uint32_t off = (uint32_t)part * (uint32_t)Gp * (uint32_t)a.O * 2u +
+                                 ((uint32_t)ch * (uint32_t)a.O + (uint32_t)n0 + 128u * half) * 8u + 16u * lane;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (gx_lptr)(cb + part * 2048 + half * 1024), 16, off, 0, 0, 0);
+        } else {
+            // groups 4 ch + 2 (q - 4) + (lane >> 5), tokens m0 + 4 (lane & 31) .. + 3 (rows past T
+            // read out of range or junk: never used)
+            const int gg = 4 * ch + 2 * (q - 4) + (lane >> 5);
+            const uint32_t off = ((uint32_t)gg * (uint32_t)a.T + (uint32_t)m0 + 4u * (lane & 31)) * 4u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(gr, (gx_lptr)(cb + 4096 + (q - 4) * 1024), 16, off, 0, 0, 0);
+        }
+    };
+    auto issue_chunk = [&](int ch) { issue_chunk1(ch, wave < 6 ? wave : wave - 6); };
+
+    f32x16_t acc[2][2][NJ], tot[2][NJ];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) { acc[i][j] = (f32x16_t)0.0f; tot[i][j] = (f32x16_t)0.0f; }
+        for (int j = 0; j < NJ; j++) { acc[0][i][j] = (f32x16_t)0.0f; acc[1][i][j] = (f32x16_t)0.0f; tot[i][j] = (f32x16_t)0.0f; }
+    const int h = lane >> 5, l31 = lane & 31;
 
-    const int nblk = K / GX_K;
-    const int unit = gs > GX_K ? gs / GX_K : 1;      // slice boundaries fall on group boundaries
-    const int nunits = nblk / unit, z = blockIdx.y, S = gridDim.y;
-    const int sl0 = z * SF / S, sl1 = (z + 1) * SF / S;
-
-    // block kb's global data in registers
-    uint4 xhr[4], xlr[4];
-    uint32_t wr[BITS];
-    float gsr, ssr, bsr;
-    auto fetch = [&](int kb) {
-        const int k0 = kb * GX_K;
-        const uint4* ph = reinterpret_cast<const uint4*>(xhrow + k0);
-        const uint4* pl = reinterpret_cast<const uint4*>(xlrow + k0);
+    // folds group g, held in register set SET (= g & 1), into tot: tot = fma(s 2^24, acc, tot)
+    auto fold = [&](auto SETC, int g) {
+        constexpr int SET = decltype(SETC)::value;
+        const uint8_t* cb = cbuf + ((g >> 2) & 1) * GX_CB;
+        const int gi = g & 3;
+        float sv[NJ];
 #pragma unroll
-        for (int v = 0; v < 4; v++) xhr[v] = xvalid ? gload_u4(ph + v) : uint4{0, 0, 0, 0};
-        if (has_lo) {
-#pragma unroll
-            for (int v = 0; v < 4; v++) xlr[v] = xvalid ? gload_u4(pl + v) : uint4{0, 0, 0, 0};
+        for (int j = 0; j < NJ; j++) {
+            const int rr = wn * 64 + j * 32 + l31;
+            const uint16_t s16 = *reinterpret_cast<const uint16_t*>(cb + rr * 8 + gi * 2);
+            sv[j] = (a.st == 0 ? bf16_to_f32(s16) : f16_to_f32(s16)) * 16777216.0f;
         }
-        load_codes32<BITS>(wptr + (int64_t)kb * (8 * BITS), wr);
-        const int kend = k0 + 32 * (gf + 1);
-        if (kend % gs == 0) {
-            const int gg = kend / gs - 1;
-            gsr = gload(gsrow + gg);
-            ssr = ld_scale<ST>(a.s + srow + gg) * 16777216.0f;
-            bsr = ld_scale<ST>(a.b + srow + gg);
-        }
-    };
-    for (int sl = sl0; sl < sl1; sl++) {
-        const int kb0 = nunits * sl / SF * unit, kb1 = nunits * (sl + 1) / SF * unit;
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) { acc[i][j] = (f32x16_t)0.0f; tot[i][j] = (f32x16_t)0.0f; }
-        fetch(kb0);
-        for (int kb = kb0; kb < kb1; kb++) {
-            const int k0 = kb * GX_K;
-            {
-                uint4* dh = reinterpret_cast<uint4*>(Xh + lr * GX_LD + lh * 32);
+            for (int j = 0; j < NJ; j++)
 #pragma unroll
-                for (int v = 0; v < 4; v++) dh[v] = xhr[v];
-                if (has_lo) {
-                    uint4* dl = reinterpret_cast<uint4*>(Xl + lr * GX_LD + lh * 32);
+                for (int r = 0; r < 16; r++) tot[i][j][r] = fmaf(sv[j], acc[SET][i][j][r], tot[i][j][r]);
+    };
+
+    // the bias terms of chunk ch's groups in [g0, g1) on the matrix cores: sum_g b[n][g] xsum[m][g]
+    // with xsum split into bf16 hi + mid + lo (truncations; exact) and b into bf16 bhi + blo (blo = 0
+    // for bf16 biases; 3 bits for f16 ones), every product exact and summed in fp32.
+    // 32x32x16 bf16: k 0-3 hi * bhi, 4-7 mid * bhi, 8-11 lo * bhi, 12-15 hi * blo (4 groups each);
+    // f16 biases add mid * blo and lo * blo in a second product.
+    auto bias_terms = [&](int ch, int g0, int g1) {
+        const uint8_t* cb = cbuf + (ch & 1) * GX_CB;
+        const float* xs = reinterpret_cast<const float*>(cb + 4096);
+        auto tr = [](float v) { return __uint_as_float(__float_as_uint(v) & 0xFFFF0000u); };
+        auto bw = [](float v) { return (uint32_t)(__float_as_uint(v) >> 16); };
+        const bool f16b = a.st != 0;
+        gx_u4 A1[2], A2[2];
 #pragma unroll
-                    for (int v = 0; v < 4; v++) dl[v] = xlr[v];
-                }
-                // the 32 codes as f16 bit patterns (subnormals q * 2^-24)
-                uint32_t p[16];
+        for (int i = 0; i < 2; i++) {
+            const int mm = wm * 64 + i * 32 + l31;
+            uint32_t hi[4], md[4], lo[4];
 #pragma unroll
-                for (int j = 0; j < 16; j++) p[j] = code_of<BITS>(wr, 2 * j) | (code_of<BITS>(wr, 2 * j + 1) << 16);
-                uint4* dw = reinterpret_cast<uint4*>(Wq + lr * GX_LD + lh * 32);
-#pragma unroll
-                for (int v = 0; v < 4; v++) dw[v] = uint4{p[4 * v], p[4 * v + 1], p[4 * v + 2], p[4 * v + 3]};
-                Gs[gf][gt] = gsr;
-                Ss[gf][gt] = ssr;
-                Bs[gf][gt] = bsr;
+            for (int q = 0; q < 4; q++) {
+                const int g = 4 * ch + q;
+                const float v = (g >= g0 && g < g1) ? xs[q * GX_M + mm] : 0.0f;
+                const float vh = tr(v), r1 = v - vh, vm = tr(r1), vl = r1 - vm;
+                hi[q] = bw(vh); md[q] = bw(vm); lo[q] = bw(vl);
             }
-            __syncthreads();
-            if (kb + 1 < kb1) fetch(kb + 1);
+            A1[i] = h == 0 ? gx_u4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), md[0] | (md[1] << 16), md[2] | (md[3] << 16)}
+                           : gx_u4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+            A2[i] = h == 0 ? gx_u4{md[0] | (md[1] << 16), md[2] | (md[3] << 16), lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)}
+                           : gx_u4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                __builtin_amdgcn_sched_barrier(0);   // one k-step's fragments live at a time
-                const int ko = ks * 16 + 8 * (lane >> 5);
-                half8_t ah[2], al[2], bw[2];
+        for (int j = 0; j < NJ; j++) {
+            const int rr = wn * 64 + j * 32 + l31;
+            const uint2 b4 = *reinterpret_cast<const uint2*>(cb + 2048 + rr * 8);
+            const uint16_t bb[4] = {(uint16_t)b4.x, (uint16_t)(b4.x >> 16), (uint16_t)b4.y, (uint16_t)(b4.y >> 16)};
+            uint32_t bh[4], bl[4];
 #pragma unroll
-                for (int i = 0; i < 2; i++) ah[i] = *reinterpret_cast<const half8_t*>(Xh + (wm * 64 + i * 32 + (lane & 31)) * GX_LD + ko);
+            for (int q = 0; q < 4; q++) {
+                if (!f16b) { bh[q] = bb[q]; bl[q] = 0; }
+                else { const float f = f16_to_f32(bb[q]), fh = tr(f); bh[q] = bw(fh); bl[q] = bw(f - fh); }
+            }
+            const uint32_t ph0 = bh[0] | (bh[1] << 16), ph1 = bh[2] | (bh[3] << 16);
+            const uint32_t pl0 = bl[0] | (bl[1] << 16), pl1 = bl[2] | (bl[3] << 16);
+            const gx_u4 B1 = h == 0 ? gx_u4{ph0, ph1, ph0, ph1} : gx_u4{ph0, ph1, pl0, pl1};
 #pragma unroll
-                for (int j = 0; j < 2; j++) bw[j] = *reinterpret_cast<const half8_t*>(Wq + (wn * 64 + j * 32 + (lane & 31)) * GX_LD + ko);
+            for (int i = 0; i < 2; i++)
+                tot[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(gx_bf8, A1[i]), __builtin_bit_cast(gx_bf8, B1), tot[i][j], 0, 0, 0);
+            if (f16b) {
+                const gx_u4 B2 = h == 0 ? gx_u4{pl0, pl1, pl0, pl1} : gx_u4{0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    tot[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(gx_bf8, A2[i]), __builtin_bit_cast(gx_bf8, B2), tot[i][j], 0, 0, 0);
+            }
+        }
+    };
+
+    // block blk: group g accumulates into register set g & 1 (for gs 32, the block's two parts are
+    // two groups; else the block lies in one group, SB = its set, FIRST = it starts the group), the
+    // group's first k-step starting from zero. Once a group's first products are issued, the
+    // previous group (the other set) is folded (not before the slice's first group).
+    auto compute = [&](auto SBC, auto FIRSTC, int blk, int kbfirst) {
+        constexpr int SB = decltype(SBC)::value;
+        constexpr bool FIRST = decltype(FIRSTC)::value;
+        int ln_ = threadIdx.x & 63;
+        asm volatile("" : "+v"(ln_));
+        const int h = ln_ >> 5, l31 = ln_ & 31;
+        const uint8_t* st = lds + (blk % GX_NST) * STG;
+        const int k0 = blk * GX_K;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            __builtin_amdgcn_sched_barrier(0);
+            half8_t ah[2], bw[NJ];
+            auto xfrag = [&](int part) {   // part 0: hi, 1: lo
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const int r = wm * 64 + i * 32 + l31, c = 2 * ks + h;
+                    ah[i] = *reinterpret_cast<const half8_t*>(st + part * GX_XB + r * 128 + 16 * (c ^ (r & 7)));
+                }
+            };
+            xfrag(0);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) bw[j] = gx_codes<BITS>(st + 2 * GX_XB + (wn * 64 + j * 32 + l31) * (8 * BITS), 2 * ks + h);
+            // a group starts at this k-step: every part for gs 32, the block's first k-step else
+            const bool gstart = GS == 32 ? (ks & 1) == 0 : (ks == 0 && FIRST);
+            auto mm = [&](auto SC) {
+                constexpr int S = decltype(SC)::value;
 #pragma unroll
                 for (int i = 0; i < 2; i++)
 #pragma unroll
-                    for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], acc[i][j], 0, 0, 0);
-                if (has_lo) {
-#pragma unroll
-                    for (int i = 0; i < 2; i++) al[i] = *reinterpret_cast<const half8_t*>(Xl + (wm * 64 + i * 32 + (lane & 31)) * GX_LD + ko);
+                    for (int j = 0; j < NJ; j++)
+                        acc[S][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], gstart ? (f32x16_t)0.0f : acc[S][i][j], 0, 0, 0);
+                if constexpr (LO) {
+                    xfrag(1);
 #pragma unroll
                     for (int i = 0; i < 2; i++)
 #pragma unroll
-                        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j], acc[i][j], 0, 0, 0);
+                        for (int j = 0; j < NJ; j++) acc[S][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], acc[S][i][j], 0, 0, 0);
                 }
-                if (ks & 1) {
-                    const int f = ks >> 1;
-                    if ((k0 + 32 * (f + 1)) % gs == 0) {
-                        // group end: tot = fma(s 2^24, acc, fma(b, xsum, tot)); lane's token of
-                        // register r in tile i: 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4
-#pragma unroll
-                        for (int i = 0; i < 2; i++) {
-                            float4 xg[4];
-#pragma unroll
-                            for (int q = 0; q < 4; q++)
-                                xg[q] = *reinterpret_cast<const float4*>(&Gs[f][wm * 64 + i * 32 + 8 * q + 4 * (lane >> 5)]);
-#pragma unroll
-                            for (int j = 0; j < 2; j++) {
-                                const int nr = wn * 64 + j * 32 + (lane & 31);
-                                const float sv = Ss[f][nr], bv = Bs[f][nr];
-#pragma unroll
-                                for (int r = 0; r < 16; r++) {
-                                    const float xv = r % 4 == 0 ? xg[r / 4].x : r % 4 == 1 ? xg[r / 4].y : r % 4 == 2 ? xg[r / 4].z : xg[r / 4].w;
-                                    tot[i][j][r] = fmaf(sv, acc[i][j][r], fmaf(bv, xv, tot[i][j][r]));
-                                    acc[i][j][r] = 0.0f;
-                                }
-                            }
-                        }
-                    }
-                }
-            }
-            __syncthreads();
+                if (gstart && (ks > 0 || blk > kbfirst)) fold(std::integral_constant<int, 1 - S>{}, (k0 + 16 * ks) / GS - 1);
+            };
+            if (GS == 32 && ks >= 2) mm(std::integral_constant<int, 1>{});
+            else mm(std::integral_constant<int, GS == 32 ? 0 : SB>{});
         }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const int nblk = K / GX_K;
+    const int unit = GS > GX_K ? GS / GX_K : 1;      // slice boundaries fall on group boundaries
+    const int nunits = nblk / unit, z = blockIdx.y, S = gridDim.y;
+    const int sl0 = z * SF / S, sl1 = (z + 1) * SF / S;
+    for (int sl = sl0; sl < sl1; sl++) {
+        const int kb0 = nunits * sl / SF * unit, kb1 = nunits * (sl + 1) / SF * unit;
+        const int g0 = kb0 * GX_K / GS, g1 = kb1 * GX_K / GS;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) tot[i][j] = (f32x16_t)0.0f;
+        // every stage and chunk buffer of the previous slice has been read (its last fold plus this barrier)
+        __syncthreads();
+        issue_chunk(kb0 / BPC);
+        issue(kb0);
+        if (kb0 + 1 < kb1) issue(kb0 + 1);
+        // block kb's step; SB, FIRST: as for compute (compile-time, so the loop is unrolled by the
+        // period of the register sets: 1 block for gs 32, 2 for gs 64, 4 for gs 128)
+        auto step = [&](int kb, auto SBC, auto FIRSTC) {
+            // this wave's copies of block kb have landed (block kb + 1's may still be in flight) ...
+            if (kb + 1 < kb1) __builtin_amdgcn_s_waitcnt(gx_wait_vm(NCP));
+            else __builtin_amdgcn_s_waitcnt(gx_wait_vm(0));
+            // ... and every wave's. Block kb - 1's stage, which block kb + 2 overwrites, is no longer
+            // read; nor the chunk buffer that block kb + 1's chunk (if it starts one) overwrites:
+            // the chunk two before it ended at block kb - 2 or earlier (chunks are >= 2 blocks); its
+            // bias terms ran at its first block, and a group is folded in the block after its last,
+            // so in block kb - 1 or earlier. The chunk's copies precede block kb + 2's, so the wait
+            // before block kb + 1 covers them.
+            __builtin_amdgcn_s_barrier();
+            if (kb + 1 < kb1 && (kb + 1) % BPC == 0) issue_chunk((kb + 1) / BPC);
+            if (kb + 2 < kb1) issue(kb + 2);
+            compute(SBC, FIRSTC, kb, kb0);
+            if (kb == kb0 || kb % BPC == 0) bias_terms(kb / BPC, g0, g1);
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using TT = std::true_type;
+        using FF = std::false_type;
+        // register set of group g: (g - g0) & 1
+        if constexpr (GS == 32) {
+            for (int kb = kb0; kb < kb1; kb++) step(kb, I0{}, TT{});
+        } else if constexpr (GS == 64) {
+            int kb = kb0;
+            for (; kb + 1 < kb1; kb += 2) { step(kb, I0{}, TT{}); step(kb + 1, I1{}, TT{}); }
+            if (kb < kb1) step(kb, I0{}, TT{});
+        } else {
+            int kb = kb0;   // slices hold whole groups: an even number of blocks
+            for (; kb + 3 < kb1; kb += 4) { step(kb, I0{}, TT{}); step(kb + 1, I0{}, FF{}); step(kb + 2, I1{}, TT{}); step(kb + 3, I1{}, FF{}); }
+            if (kb < kb1) { step(kb, I0{}, TT{}); step(kb + 1, I0{}, FF{}); }
+        }
+        // the slice's last group
+        if (GS == 32 || ((g1 - 1 - g0) & 1)) fold(std::integral_constant<int, 1>{}, g1 - 1);
+        else fold(std::integral_constant<int, 0>{}, g1 - 1);
         if (sl1 - sl0 > 1) {
             // one workgroup walks several slices: the running sum of the finished slices waits in
-            // the thread's own output elements (the same order of additions as the split launch).
-            // The lane index is made opaque here so that the output addresses are computed in
-            // place rather than kept live across the K loop.
+            // the thread's own output elements (the same order of additions as the split launch:
+            // (slice 0 + slice 1) + slice 2 ...). The lane index is made opaque so the output
+            // addresses are computed in place rather than kept live across the K loop.
             int ol = lane;
             asm volatile("" : "+v"(ol));
-            const bool first = sl == sl0, lastsl = sl + 1 == sl1;
+            const bool firstsl = sl == sl0, lastsl = sl + 1 == sl1;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
+            for (int j = 0; j < NJ; j++) {
                 const int n = n0 + wn * 64 + j * 32 + (ol & 31);
                 if (n >= a.O) continue;
 #pragma unroll
@@ -296,7 +465,7 @@ __global__ __launch_bounds__(256, 2) void qgemmx_kernel(QGemmXDev a) {
                         const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (ol >> 5) + (r & 3);
                         if (m >= a.T) continue;
                         float* yp = a.y + (int64_t)m * a.ys + n;
-                        if (!first) tot[i][j][r] = *yp + tot[i][j][r];
+                        if (!firstsl) tot[i][j][r] = *yp + tot[i][j][r];
                         if (!lastsl) *yp = tot[i][j][r];
                     }
             }
@@ -307,13 +476,13 @@ __global__ __launch_bounds__(256, 2) void qgemmx_kernel(QGemmXDev a) {
         // the slices in order (deterministic) and writes the output
         unsigned* cnt = reinterpret_cast<unsigned*>(a.split);
         float* part = a.split + QGEMM_SPLIT_TILES;
-        auto pidx = [&](int zz, int i, int j, int r) {   // [slice][tile][thread][64 values]
-            return (((size_t)zz * a.ntiles + tile) * 256 + tid) * 64 + (i * 2 + j) * 16 + r;
+        auto pidx = [&](int zz, int i, int j, int r) {   // [slice][tile][64 values][thread]: a wave's accesses are contiguous
+            return (((size_t)zz * a.ntiles + tile) * 64 + (i * NJ + j) * 16 + r) * 512 + tid;
         };
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < NJ; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) __hip_atomic_store(part + pidx(z, i, j, r), tot[i][j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
@@ -322,22 +491,33 @@ __global__ __launch_bounds__(256, 2) void qgemmx_kernel(QGemmXDev a) {
         __syncthreads();
         if (!last) return;
         if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // slices in order ((s0 + s1) + s2 ...); this slice's own partial from registers, every other
+        // slice's 64 values loaded at once
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < NJ; j++) acc[1][i][j] = tot[i][j];
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    float v = __hip_atomic_load(part + pidx(0, i, j, r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    for (int zz = 1; zz < S; zz++) v += __hip_atomic_load(part + pidx(zz, i, j, r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    tot[i][j][r] = v;
-                }
+        for (int zz = 0; zz < SF; zz++) {
+            if (zz >= S) break;
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        acc[0][i][j][r] = zz == z ? acc[1][i][j][r] : __hip_atomic_load(part + pidx(zz, i, j, r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) tot[i][j] = zz == 0 ? acc[0][i][j] : tot[i][j] + acc[0][i][j];
+        }
     }
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NJ; j++) {
         const int n = n0 + wn * 64 + j * 32 + (lane & 31);
         if (n >= a.O) continue;
-        const float bias = a.bias ? ld_scale<ST>(a.bias + n) : 0.0f;
+        const float bias = a.bias ? (a.st == 0 ? ld_scale<0>(a.bias + n) : ld_scale<1>(a.bias + n)) : 0.0f;
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -346,6 +526,23 @@ __global__ __launch_bounds__(256, 2) void qgemmx_kernel(QGemmXDev a) {
                 if (m < a.T) a.y[(int64_t)m * a.ys + n] = tot[i][j][r] * a.inv[m] + bias;
             }
     }
+}
+
+template <int BITS, int GS, int SF>
+__global__ __launch_bounds__(512, 1) void qgemmx_kernel(QGemmXDev a) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t gx_lds_base[];
+    __shared__ int lo_any;
+    const int tid = threadIdx.x;
+    // XCD x runs workgroups x, x + 8, ...: give it a contiguous run of tiles, token tiles fastest
+    const int g = blockIdx.x, xcd = g & 7, per = a.ntiles >> 3, rem = a.ntiles & 7;
+    const int tile = xcd * per + min(xcd, rem) + (g >> 3);
+    const int m0 = (tile % a.nT) * GX_M;
+    if (tid == 0) lo_any = 0;
+    __syncthreads();
+    if (tid < GX_M && m0 + tid < a.T && a.nz[m0 + tid]) lo_any = 1;
+    __syncthreads();
+    if (lo_any) qgemmx_body<BITS, GS, SF, true>(a, gx_lds_base, tile);
+    else qgemmx_body<BITS, GS, SF, false>(a, gx_lds_base, tile);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -387,15 +584,23 @@ hipError_t launch_x_to_f16(const float* x, int xs, int K, int T, uint16_t* out, 
 }
 
 
+bool qgemm_supported(int K, int gs) { return K % GX_K == 0 && (gs == 32 || gs == 64 || gs == 128) && K % gs == 0; }
+
 hipError_t launch_qgemm(const QGemmArgs& a, hipStream_t s) {
-    if (a.K % GX_K || a.gs % 32 || a.K % a.gs || a.T < 1 || !a.xbf || !a.xlo || !a.xgs || !a.xsc || !a.xnz) return hipErrorInvalidValue;
+    if (!qgemm_supported(a.K, a.gs) || a.T < 1 || !a.xbf || !a.xlo || !a.xgs || !a.xsc || !a.xnz || !a.wsb) return hipErrorInvalidValue;
+    const int G = a.K / a.gs, Gp = gx_gpad(G);
     if (!a.x_ready) {
-        hipLaunchKernelGGL(x_split_kernel, dim3(a.T), dim3(256), (size_t)(a.K / 8) * 4, s, a.x, a.x_stride, a.K, a.gs, a.xbf,
+        hipLaunchKernelGGL(x_split_kernel, dim3(a.T), dim3(256), (size_t)(a.K / 8) * 4, s, a.x, a.x_stride, a.K, a.gs, a.T, a.xbf,
                            a.xlo, a.xgs, a.xsc, a.xnz);
         if (hipError_t e = hipGetLastError()) return e;
     }
+    {
+        hipLaunchKernelGGL(scale_repack_kernel, dim3((unsigned)((a.m.O + 63) / 64), (unsigned)((Gp + 63) / 64)), dim3(256), 0, s, a.m.s, a.m.b,
+                           a.m.O, G, a.wsb);
+        if (hipError_t e = hipGetLastError()) return e;
+    }
     const int nT = (a.T + GX_M - 1) / GX_M, nO = (a.O + GX_N - 1) / GX_N, tiles = nT * nO;
-    QGemmXDev d{a.m.w, a.m.s, a.m.b, a.m.bias, a.K, a.gs, a.O, a.T, a.y_stride, nT, tiles,
+    QGemmXDev d{a.m.w, a.wsb, a.m.bias, a.st, a.K, a.gs, a.O, a.T, a.y_stride, nT, tiles,
                 a.xbf, a.xlo, a.xgs, a.xsc, a.xnz, a.y, a.split};
     dim3 grid(tiles, 1);
     static int cus = 0;
@@ -404,20 +609,37 @@ hipError_t launch_qgemm(const QGemmArgs& a, hipStream_t s) {
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return hipErrorInvalidDevice;
     }
-    const int SF = qgemm_slices(a.K, a.gs);
-    // under one round of workgroups (two per CU): the K slices on workgroups of their own, when a
+    const int SF = qgemm_slices(a.K);
+    // under one round of workgroups (one per CU): the K slices on workgroups of their own, when a
     // scratch is given
-    if (SF > 1 && tiles * SF <= 2 * cus && (size_t)tiles * SF <= QGEMM_SPLIT_TILES && a.split && a.split_floats >= QGEMM_SPLIT_FLOATS)
+    if (SF > 1 && tiles * SF <= cus && (size_t)tiles * SF <= QGEMM_SPLIT_TILES && a.split && a.split_floats >= QGEMM_SPLIT_FLOATS)
         grid.y = SF;
-#define GEMM_CASE(B) case B: \
-    if (SF == 4) { if (a.st == 0) hipLaunchKernelGGL((qgemmx_kernel<B, 0, 4>), grid, dim3(256), 0, s, d); \
-                   else hipLaunchKernelGGL((qgemmx_kernel<B, 1, 4>), grid, dim3(256), 0, s, d); } \
-    else { if (a.st == 0) hipLaunchKernelGGL((qgemmx_kernel<B, 0, 1>), grid, dim3(256), 0, s, d); \
-           else hipLaunchKernelGGL((qgemmx_kernel<B, 1, 1>), grid, dim3(256), 0, s, d); } \
-    return hipGetLastError();
+    static bool attr = false;
+    if (!attr) {
+#define GEMM_ATTR1(B, GS) \
+        for (const void* f : {(const void*)qgemmx_kernel<B, GS, 1>, (const void*)qgemmx_kernel<B, GS, 4>}) \
+            if (hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, gx_lds<B>())) return e;
+#define GEMM_ATTR(B) GEMM_ATTR1(B, 32) GEMM_ATTR1(B, 64) GEMM_ATTR1(B, 128)
+        GEMM_ATTR(2) GEMM_ATTR(3) GEMM_ATTR(4) GEMM_ATTR(5) GEMM_ATTR(6) GEMM_ATTR(8)
+#undef GEMM_ATTR
+#undef GEMM_ATTR1
+        attr = true;
+    }
+    auto go = [&](auto kern, int lds) -> hipError_t {
+        hipLaunchKernelGGL(kern, grid, dim3(512), (size_t)lds, s, d);
+        return hipGetLastError();
+    };
+#define GEMM_GS(B, GS) if (a.gs == GS) return SF == 4 ? go(qgemmx_kernel<B, GS, 4>, gx_lds<B>()) : go(qgemmx_kernel<B, GS, 1>, gx_lds<B>());
+#define GEMM_CASE(B) case B: GEMM_GS(B, 32) GEMM_GS(B, 64) GEMM_GS(B, 128) break;
     switch (a.bits) { GEMM_CASE(2) GEMM_CASE(3) GEMM_CASE(4) GEMM_CASE(5) GEMM_CASE(6) GEMM_CASE(8) }
 #undef GEMM_CASE
+#undef GEMM_GS
     return hipErrorInvalidValue;
 }
+
+// Scratch of the MLX-layout GEMM (per call): the x pre-pass' group sums (floats) and the repacked
+// scales and biases (16-bit words).
+size_t qgemm_gsum_floats(int T, int K, int gs) { return (size_t)T * gx_gpad(K / gs); }
+size_t qgemm_scale_halves(int O, int K, int gs) { return (size_t)2 * gx_gpad(K / gs) * O; }
 
 }  // namespace mlxr

@@ -43,25 +43,30 @@ hipError_t launch_qmm_small(const QmmSmallArgs& a, hipStream_t s);
 
 // Prefill GEMM over the MLX layout, any code width: Y[T][O] = X[T][K] W[O][K]^T (+bias) with exact
 // codes on the f16 matrix cores, x as f16 hi + lo (per-row power-of-two scale) and the group scale
-// and bias applied in fp32 per group: fp32-level results. Needs K % 64 == 0, gs % 32 == 0.
+// and bias applied in fp32 per group: fp32-level results. Needs qgemm_supported(K, gs).
 struct QGemmArgs {
     QMat m;
     int K = 0, bits = 4, gs = 64, st = 0, O = 0, T = 0;
     const float* x = nullptr; int x_stride = 0;
     float* y = nullptr; int y_stride = 0;
-    // pre-pass scratch: hi and lo (T*K 16-bit each), group sums (T*K/gs floats), the rows' inverse
-    // scales (T floats) and lo-nonzero flags (T ints)
+    // pre-pass scratch: hi and lo (T*K 16-bit each), group sums (qgemm_gsum_floats), the rows' inverse
+    // scales (T floats), lo-nonzero flags (T ints) and the repacked scales and biases
+    // (qgemm_scale_halves 16-bit words)
     uint16_t* xbf = nullptr; uint16_t* xlo = nullptr; float* xgs = nullptr; float* xsc = nullptr; int* xnz = nullptr;
+    uint16_t* wsb = nullptr;
     bool x_ready = false;                 // the scratch already holds this x (same K and gs): skip the pre-pass
     // optional scratch for the split over K when the grid is under one round:
     // QGEMM_SPLIT_FLOATS floats, zero before first use (its tile counters return to zero)
     float* split = nullptr; size_t split_floats = 0;
 };
-// tile counters for up to 512 tiles, then at most 512 partial 128 x 128 tiles (slices x tiles stay
-// within two workgroups per CU of a 256-CU device)
-constexpr size_t QGEMM_SPLIT_TILES = 512;
-constexpr size_t QGEMM_SPLIT_FLOATS = QGEMM_SPLIT_TILES + QGEMM_SPLIT_TILES * 128 * 128;
+// tile counters for up to 256 tiles, then at most 256 partial 128 x 256 tiles (slices x tiles stay
+// within one workgroup per CU of a 256-CU device)
+constexpr size_t QGEMM_SPLIT_TILES = 256;
+constexpr size_t QGEMM_SPLIT_FLOATS = QGEMM_SPLIT_TILES + QGEMM_SPLIT_TILES * 128 * 256;
 hipError_t launch_qgemm(const QGemmArgs& a, hipStream_t s);
+size_t qgemm_gsum_floats(int T, int K, int gs);
+bool qgemm_supported(int K, int gs);   // K % 64 == 0, gs 32 / 64 / 128
+size_t qgemm_scale_halves(int O, int K, int gs);
 // The 4-bit GEMM pre-pass: row t of x scaled by the power of two that puts max|x| in [2^13, 2^14),
 // rounded to f16 (each 8-group stored as 0,4,1,5,2,6,3,7), inv[t] = the inverse scale.
 // launch_x_to_f16's single-pass kernel (misc.hip) for K <= 32768; false (nothing launched) above.

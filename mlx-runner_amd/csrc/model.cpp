@@ -592,6 +592,10 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
     m->nsplit_ver = std::max(m->nsplit_dec, (seq + 127) / 128);
     const size_t partFloats = (size_t)8 * c.nH * m->nsplit_ver * (c.D + 2);   // split-attention partials (T <= 8)
     int Kmax = std::max(c.I, std::max(c.H, c.nH * c.D));
+    size_t wsb_halves = 0;   // the MLX-layout GEMM's repacked scales: the largest projection's
+    for (auto& ly : m->layers)
+        for (const Lin* l : {&ly.q, &ly.k, &ly.v, &ly.o, &ly.gate, &ly.up, &ly.down}) wsb_halves = std::max(wsb_halves, qgemm_scale_halves(l->O, l->K, l->gs));
+    wsb_halves = std::max(wsb_halves, qgemm_scale_halves(m->head.O, m->head.K, m->head.gs));
     int rc;
     if ((rc = dalloc(m, &m->hist, seq + 1)) || (rc = dalloc(m, &m->status, seq + 1)) || (rc = dalloc(m, &m->rng, 2)) ||
         (rc = dalloc(m, &m->dpos, 64)) || (rc = dalloc(m, &m->h, (size_t)B * H)) || (rc = dalloc(m, &m->xn, (size_t)B * H)) ||
@@ -600,7 +604,7 @@ int model_open(const char* dir_c, int context_len, const mlxr_sparse_cfg* sparse
         (rc = dalloc(m, &m->mlp, (size_t)B * I)) || (rc = dalloc(m, &m->logits, (size_t)8 * V)) || (rc = dalloc(m, &m->dmv_split, dpack_mv_split_floats(H))) ||
         (rc = dalloc(m, &m->part, partFloats)) || (rc = dalloc(m, &m->qsplit, QGEMM_SPLIT_FLOATS)) || (rc = dalloc(m, &m->bmax, (V + 255) / 256)) ||
         (rc = dalloc(m, &m->barg, (V + 255) / 256)) || (rc = dalloc(m, &m->xbf, (size_t)B * Kmax)) || (rc = dalloc(m, &m->xsc, (size_t)B)) || (rc = dalloc(m, &m->diag, 8)) ||
-        (rc = dalloc(m, &m->xlo, (size_t)B * Kmax)) || (rc = dalloc(m, &m->xgs, (size_t)B * Kmax / 32)) || (rc = dalloc(m, &m->xnz, (size_t)B)))
+        (rc = dalloc(m, &m->xlo, (size_t)B * Kmax)) || (rc = dalloc(m, &m->xgs, qgemm_gsum_floats(B, Kmax, 32))) || (rc = dalloc(m, &m->xnz, (size_t)B)) || (rc = dalloc(m, &m->wsb, wsb_halves)))
         return fail(rc);
     HIPCHECK(hipMemset(m->hist, 0, (seq + 1) * 4));
     HIPCHECK(hipMemset(m->dmv_split, 0, dpack_mv_split_floats(H) * 4));   // the split matvec's tile counters
@@ -684,7 +688,7 @@ int project(Model* m, const Lin* parts, int n, const float* x, int xs, float* y,
     for (int i = 0; i < n; i++) {
         QGemmArgs g; g.m = parts[i].m; g.K = parts[i].K; g.bits = parts[i].bits; g.gs = parts[i].gs; g.st = parts[i].st;
         g.O = parts[i].O; g.T = T; g.x = x; g.x_stride = xs; g.y = y + col; g.y_stride = ys; g.xbf = m->xbf; g.xsc = m->xsc;
-        g.xlo = m->xlo; g.xgs = m->xgs; g.xnz = m->xnz;
+        g.xlo = m->xlo; g.xgs = m->xgs; g.xnz = m->xnz; g.wsb = m->wsb;
         g.split = m->qsplit; g.split_floats = QGEMM_SPLIT_FLOATS;
         g.x_ready = i > 0 && parts[i].K == parts[0].K && parts[i].bits == parts[0].bits && parts[i].gs == parts[0].gs;
         HIPCHECK(launch_qgemm(g, s));

@@ -69,6 +69,7 @@ struct Model {
     float* qsplit = nullptr;            // the other widths' prefill GEMM split over K (QGEMM_SPLIT_FLOATS, counters at zero)
     uint16_t* xbf = nullptr; float* xsc = nullptr;
     uint16_t* xlo = nullptr; float* xgs = nullptr; int* xnz = nullptr;   // the MLX-layout GEMM's x lo part, group sums, lo flags
+    uint16_t* wsb = nullptr;          // the MLX-layout GEMM's repacked scales
     int* diag = nullptr;
     // sparse
     bool sparse_alloc = false; bool sparse_on = false;

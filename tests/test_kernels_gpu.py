@@ -128,11 +128,13 @@ def test_qgemm_prefill_tiles(gpu, bits, gs):
         assert max_rel_err(qgemm(gpu, fx, x), fx.oracle(oracle).matmul_f64(x)) < TOL, (T, O, K)
         xb = bf16_to_f32(bf16_round(x)).reshape(T, K)
         assert max_rel_err(qgemm(gpu, fx, xb), fx.oracle(oracle).matmul_f64(xb)) < TOL, ("bf16 x", T, O, K)
-    # a bf16-valued row next to fp32 rows in one token tile: each row keeps its own precision
-    fx = QuantFixture(300, 1024, bits, gs, seed=1, fast=True)
+    # a bf16-valued row next to fp32 rows in one token tile: each row keeps its own precision; with
+    # bf16 and f16 scales and biases (f16 biases enter the bias products as two bf16 parts)
     x = np.random.default_rng(bits).normal(0, 1, (40, 1024)).astype(np.float32)
     x[::3] = bf16_to_f32(bf16_round(x[::3])).reshape(-1, 1024)
-    assert max_rel_err(qgemm(gpu, fx, x), fx.oracle(oracle).matmul_f64(x)) < TOL
+    for st in ("bf16", "f16"):
+        fx = QuantFixture(300, 1024, bits, gs, st=st, seed=1, fast=True)
+        assert max_rel_err(qgemm(gpu, fx, x), fx.oracle(oracle).matmul_f64(x)) < TOL, st
 
 
 def test_qgemm_row_scaling(gpu):
