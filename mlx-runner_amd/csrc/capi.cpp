@@ -244,6 +244,14 @@ int mlxr_k_qmm(const mlxr_qmat* parts, int nparts, int K, int bits, int gs, int 
     QmmSmallArgs a; a.nparts = nparts;
     for (int i = 0; i < nparts; i++) a.part[i] = qmat(parts[i]);
     a.K = K; a.bits = bits; a.gs = gs; a.st = st; a.O = O; a.T = T; a.x = x; a.x_stride = x_stride; a.y = y; a.y_stride = y_stride;
+    if (qmmx_supported(K, bits, gs)) {
+        if (int rc = ensure_buf(g_xbf, g_xbf_elems, (size_t)T * K)) return rc;
+        if (int rc = ensure_buf(g_xlo, g_xlo_elems, (size_t)T * K)) return rc;
+        if (int rc = ensure_buf(g_xgs, g_xgs_elems, qgemm_gsum_floats(T, K, gs))) return rc;
+        if (int rc = ensure_buf(g_xsc, g_xsc_elems, (size_t)T)) return rc;
+        if (int rc = ensure_buf(g_xnz, g_xnz_elems, (size_t)T)) return rc;
+        a.xbf = g_xbf; a.xlo = g_xlo; a.xgs = g_xgs; a.xsc = g_xsc; a.xnz = g_xnz;
+    }
     return done(launch_qmm_small(a, g_stream));
 }
 

@@ -642,4 +642,148 @@ hipError_t launch_qgemm(const QGemmArgs& a, hipStream_t s) {
 size_t qgemm_gsum_floats(int T, int K, int gs) { return (size_t)T * gx_gpad(K / gs); }
 size_t qgemm_scale_halves(int O, int K, int gs) { return (size_t)2 * gx_gpad(K / gs) * O; }
 
+
+// ---------------------------------------------------------------------------------------------
+// Small batch (T <= 8) on the matrix cores, code widths 4 and 8: the same arithmetic as the GEMM
+// above (exact codes, x as f16 hi + lo with a per-token power of two, scale and bias per group in
+// fp32), shaped for a few tokens. v_mfma_f32_16x16x32_f16 with the tokens as the 16 A rows (rows
+// past T zero) and 16 weight rows as the B columns, so each lane's accumulator holds its own
+// weight row (its scale and bias load with its codes) for tokens 4 (lane / 16) .. + 3.
+// A 1024-thread workgroup owns 16 rows; its 16 waves take a sixteenth of the groups each and add
+// their partial sums in wave order. Lane quarter q takes codes GS/4 q .. + GS/4 - 1 of every
+// group (the k order inside a group is free: the same for codes and x), so its codes are one
+// contiguous load per group.
+struct QmmXDev {
+    const uint8_t* w[3]; const uint16_t* s[3]; const uint16_t* b[3]; const uint16_t* bias[3];
+    int o1, o2, K, O, T, ys;
+    const uint16_t* xh; const uint16_t* xl; const float* gsum; const float* inv; const int* nz; float* y;
+};
+constexpr int QX_WAVES = 4;
+
+template <int BITS, int GS, int ST>
+__global__ __launch_bounds__(256) void qmmx_kernel(QmmXDev a) {
+    __shared__ f32x4_t red[QX_WAVES][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, q = lane >> 4, T = a.T;
+    const int K = a.K, G = K / GS, g0 = G * wave / QX_WAVES, g1 = G * (wave + 1) / QX_WAVES;
+    const int n = blockIdx.x * 16 + l16;   // the lane's weight row
+    int row = min(n, a.O - 1), part = 0;
+    if (row >= a.o1) {
+        if (row < a.o1 + a.o2) { part = 1; row -= a.o1; }
+        else { part = 2; row -= a.o1 + a.o2; }
+    }
+    const uint8_t* wp = a.w[part] + (int64_t)row * (K / 8 * BITS);
+    const uint16_t* sp = a.s[part] + (int64_t)row * G;
+    const uint16_t* bp = a.b[part] + (int64_t)row * G;
+    const bool tok = l16 < T;                                   // A row l16: a token
+    const int64_t xo = (int64_t)(tok ? l16 : 0) * K;
+    // any token with lo parts (the loads issued together, not one round trip per token)
+    int nzv[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) nzv[t] = a.nz[min(t, T - 1)];
+    int lo = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) lo |= nzv[t];
+    constexpr int CPL = GS / 4, NS = GS / 32, DW = CPL * BITS / 32;
+    constexpr int QX_NB = GS == 128 ? 2 : 4;   // groups per batch of loads
+    f32x4_t tot = {0.0f, 0.0f, 0.0f, 0.0f};
+    // groups in batches of QX_NB: every load of a batch is issued before any is used, so a wave
+    // pays one memory round trip per batch
+    for (int gb = g0; gb < g1; gb += QX_NB) {
+        uint32_t cw[QX_NB][DW];
+        float sv[QX_NB], bv[QX_NB], xs[QX_NB][4];
+        half8_t ah[QX_NB][NS];
+#pragma unroll
+        for (int u = 0; u < QX_NB; u++) {
+            const int g = min(gb + u, g1 - 1), k0 = g * GS + CPL * q;
+            const uint32_t* cp = reinterpret_cast<const uint32_t*>(wp + k0 / 8 * BITS);
+            if constexpr (DW % 4 == 0) {
+#pragma unroll
+                for (int i = 0; i < DW / 4; i++) {
+                    const uint4 v = gload_u4(cp + 4 * i);
+                    cw[u][4 * i] = v.x; cw[u][4 * i + 1] = v.y; cw[u][4 * i + 2] = v.z; cw[u][4 * i + 3] = v.w;
+                }
+            } else if constexpr (DW == 2) {
+                const uint2 v = *reinterpret_cast<const uint2*>(cp);
+                cw[u][0] = v.x; cw[u][1] = v.y;
+            } else {
+                cw[u][0] = cp[0];
+            }
+            sv[u] = ld_scale<ST>(sp + g) * 16777216.0f;
+            bv[u] = ld_scale<ST>(bp + g);
+#pragma unroll
+            for (int i = 0; i < 4; i++) xs[u][i] = 4 * q + i < T ? a.gsum[(int64_t)g * T + 4 * q + i] : 0.0f;
+#pragma unroll
+            for (int st = 0; st < NS; st++)
+                ah[u][st] = tok ? __builtin_bit_cast(half8_t, gload_u4(a.xh + xo + k0 + 8 * st)) : (half8_t)0;
+        }
+#pragma unroll
+        for (int u = 0; u < QX_NB; u++) {
+            if (gb + u >= g1) break;
+            const int k0 = (gb + u) * GS + CPL * q;
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < NS; st++) {
+                half8_t bw;
+                if constexpr (BITS == 4) {
+                    const uint32_t ev = cw[u][st] & 0x0F0F0F0Fu, od = (cw[u][st] >> 4) & 0x0F0F0F0Fu;
+                    bw = __builtin_bit_cast(half8_t, gx_u4{__builtin_amdgcn_perm(od, ev, 0x0C040C00u), __builtin_amdgcn_perm(od, ev, 0x0C050C01u),
+                                                           __builtin_amdgcn_perm(od, ev, 0x0C060C02u), __builtin_amdgcn_perm(od, ev, 0x0C070C03u)});
+                } else {
+                    const uint32_t c0 = cw[u][2 * st], c1 = cw[u][2 * st + 1];
+                    bw = __builtin_bit_cast(half8_t, gx_u4{__builtin_amdgcn_perm(0u, c0, 0x0C010C00u), __builtin_amdgcn_perm(0u, c0, 0x0C030C02u),
+                                                           __builtin_amdgcn_perm(0u, c1, 0x0C010C00u), __builtin_amdgcn_perm(0u, c1, 0x0C030C02u)});
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[u][st], bw, acc, 0, 0, 0);
+                if (lo) {
+                    const half8_t al = tok ? __builtin_bit_cast(half8_t, gload_u4(a.xl + xo + k0 + 8 * st)) : (half8_t)0;
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, acc, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) tot[i] = fmaf(sv[u], acc[i], fmaf(bv[u], xs[u][i], tot[i]));
+        }
+    }
+    red[wave][lane] = tot;
+    __syncthreads();
+    if (wave != 0 || n >= a.O) return;
+    f32x4_t sum = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < QX_WAVES; w++) sum += red[w][lane];
+    const float bias = a.bias[part] ? ld_scale<ST>(a.bias[part] + row) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int t = 4 * q + i;
+        if (t < T) a.y[(int64_t)t * a.ys + n] = sum[i] * a.inv[t] + bias;
+    }
+}
+
+bool qmmx_supported(int K, int bits, int gs) {
+    return (bits == 4 || bits == 8) && (gs == 32 || gs == 64 || gs == 128) && K % gs == 0 && K % 32 == 0;
+}
+
+hipError_t launch_qmmx(const QmmSmallArgs& a, hipStream_t s) {
+    if (!qmmx_supported(a.K, a.bits, a.gs) || a.T < 1 || a.T > 8 || !a.xbf || !a.xlo || !a.xgs || !a.xsc || !a.xnz)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(x_split_kernel, dim3(a.T), dim3(256), (size_t)(a.K / 8) * 4, s, a.x, a.x_stride, a.K, a.gs, a.T, a.xbf, a.xlo,
+                       a.xgs, a.xsc, a.xnz);
+    if (hipError_t e = hipGetLastError()) return e;
+    QmmXDev d{};
+    for (int i = 0; i < 3; i++) {
+        const QMat& m = a.part[i < a.nparts ? i : a.nparts - 1];
+        d.w[i] = m.w; d.s[i] = m.s; d.b[i] = m.b; d.bias[i] = m.bias;
+    }
+    d.o1 = a.part[0].O; d.o2 = a.nparts > 1 ? a.part[1].O : 0;
+    d.K = a.K; d.O = a.O; d.T = a.T; d.ys = a.y_stride;
+    d.xh = a.xbf; d.xl = a.xlo; d.gsum = a.xgs; d.inv = a.xsc; d.nz = a.xnz; d.y = a.y;
+    const dim3 grid((unsigned)((a.O + 15) / 16));
+#define QMMX_GO(B, GS) if (a.bits == B && a.gs == GS) { \
+        if (a.st == 0) hipLaunchKernelGGL((qmmx_kernel<B, GS, 0>), grid, dim3(64 * QX_WAVES), 0, s, d); \
+        else hipLaunchKernelGGL((qmmx_kernel<B, GS, 1>), grid, dim3(64 * QX_WAVES), 0, s, d); \
+        return hipGetLastError(); }
+    QMMX_GO(4, 32) QMMX_GO(4, 64) QMMX_GO(4, 128) QMMX_GO(8, 32) QMMX_GO(8, 64) QMMX_GO(8, 128)
+#undef QMMX_GO
+    return hipErrorInvalidValue;
+}
+
 }  // namespace mlxr

@@ -31,15 +31,20 @@ struct QmvArgs {
 };
 hipError_t launch_qmv(const QmvArgs& a, hipStream_t s);
 
-// Small batch (2..8 tokens): y[t][o] = W x[t] (+bias), fp32 math, per-token results identical to qmv's.
+// Small batch (2..8 tokens): y[t][o] = W x[t] (+bias) at fp32-level precision.
 struct QmmSmallArgs {
     QMat part[3];
     int nparts = 1;
     int K = 0, bits = 4, gs = 64, st = 0, O = 0, T = 1;
     const float* x = nullptr; int x_stride = 0;
     float* y = nullptr; int y_stride = 0;
+    // optional pre-pass scratch (as QGemmArgs'): with it, widths 4 and 8 (qmmx_supported) run on
+    // the matrix cores (launch_qmmx); without it, or for other widths, on the fp32 vector path
+    uint16_t* xbf = nullptr; uint16_t* xlo = nullptr; float* xgs = nullptr; float* xsc = nullptr; int* xnz = nullptr;
 };
 hipError_t launch_qmm_small(const QmmSmallArgs& a, hipStream_t s);
+bool qmmx_supported(int K, int bits, int gs);
+hipError_t launch_qmmx(const QmmSmallArgs& a, hipStream_t s);
 
 // Prefill GEMM over the MLX layout, any code width: Y[T][O] = X[T][K] W[O][K]^T (+bias) with exact
 // codes on the f16 matrix cores, x as f16 hi + lo (per-row power-of-two scale) and the group scale

@@ -681,6 +681,7 @@ int project(Model* m, const Lin* parts, int n, const float* x, int xs, float* y,
         for (int i = 0; i < n; i++) { a.part[i] = parts[i].m; O += parts[i].O; }
         a.K = parts[0].K; a.bits = parts[0].bits; a.gs = parts[0].gs; a.st = parts[0].st; a.O = O; a.T = T;
         a.x = x; a.x_stride = xs; a.y = y; a.y_stride = ys;
+        a.xbf = m->xbf; a.xlo = m->xlo; a.xgs = m->xgs; a.xsc = m->xsc; a.xnz = m->xnz;
         HIPCHECK(launch_qmm_small(a, s));
         return MLXR_OK;
     }

@@ -254,7 +254,8 @@ hipError_t launch_qmv(const QmvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Small batch (T = 2..8). A lane holds x of its 32-code chunk for up to QMM_TP tokens in registers
+// Small batch (T = 2..8) on the fp32 vector units (code widths other than 4 and 8, or callers
+// without the pre-pass scratch; widths 4 and 8 run on the matrix cores: qmmx_kernel). A lane holds x of its 32-code chunk for up to QMM_TP tokens in registers
 // and reuses it for QMM_R rows (each row's codes converted once and dotted with every token), so x
 // is loaded once per chunk per pass instead of once per row and token. More than QMM_TP tokens take
 // a second pass over the same rows (their weights then come from the caches). For inputs of at
@@ -396,6 +397,7 @@ __global__ __launch_bounds__(256) void qmm_small_kernel(QmmDev a) {
 
 hipError_t launch_qmm_small(const QmmSmallArgs& a, hipStream_t s) {
     if (a.T < 1 || a.T > QMM_TT) return hipErrorInvalidValue;
+    if (a.xbf && qmmx_supported(a.K, a.bits, a.gs)) return launch_qmmx(a, s);
     QmmDev d{};
     for (int i = 0; i < 3; i++) {
         const QMat& m = a.part[i < a.nparts ? i : a.nparts - 1];
