@@ -102,7 +102,8 @@ int mlxr_supports_batched_verify(const mlxr_model* m);
 typedef int (*mlxr_cancel_fn)(void* user);
 /* forward(_:offset:allLogits:dense:isCancelled:) (Transformer.swift:1117-1136): runs tokens at
  * offset..offset+n-1 in chunks of MLXR_PREFILL_CHUNK; *logits_out = last row's logits (V floats)
- * or, with all_logits (n <= 8), [n][V]. Owned by the model, valid until the next call. */
+ * or, with all_logits (n <= 8), [n][V]. Owned by the model, valid until the next call. Like the
+ * reference's forward it selects no token: the history past offset + n - 1 is left as it was. */
 int mlxr_forward(mlxr_model* m, const int32_t* tokens, int n, int offset, int all_logits, int dense,
                  const float** logits_out, mlxr_cancel_fn is_cancelled, void* user);
 /* prefill(_:offset:sample:isCancelled:) (Transformer.swift:1224-1249): token selected on the GPU

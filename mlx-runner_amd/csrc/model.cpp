@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <dirent.h>
 #include <fcntl.h>
@@ -927,20 +928,39 @@ int model_forward(Model* m, const int32_t* tokens, int n, int offset, bool all_l
     if (offset < 0 || offset + n > m->max_seq) return set_error(MLXR_E_CONTEXT_FULL, "The context window is full.");
     if (int rc = check_tokens(m, tokens, n)) return rc;
     // one token whose step the persistent kernel takes (the decode loop's own step: speculative
-    // decoding's steps without a draft): the token goes into the history, one greedy step runs
-    // (its pick is not used: the caller samples from the logits), and its logits are returned
+    // decoding's steps without a draft): the token goes into the history and one persistent step runs
+    // without token selection (select = 0: it writes neither hist[offset + 1] nor the ring and leaves
+    // *dpos at offset, as the reference's forward leaves them); its logits are returned
     bool idle = true;
     for (auto& s : m->slots) idle = idle && !s.busy;
     if (n == 1 && idle && offset + 1 < m->max_seq && m->mega_ok && m->decode_mode == 1 &&
         !(m->sparse_on && sparse_plan_valid(m->sparse, offset))) {
         if (int rc = write_tokens(m, tokens, 1, offset)) return rc;
-        mlxr_sample_params g{};
-        g.penalty = 1.0f; g.temperature = 0.0f; g.top_p = 1.0f; g.min_p = 0.0f;
-        mlxr_step st;
-        int32_t pick = 0;
-        if (int rc = model_begin_decode(m, offset, &g, &st)) return rc;
-        if (int rc = model_finish(m, &st, &pick)) return rc;
-        return model_step_logits(m, out);
+        if (int rc = set_dpos(m, offset)) return rc;
+        HIPCHECK(hipEventRecord(m->slots[0].start, m->stream));
+        MegaArgs a = m->mega;
+        a.select = 0;
+        HIPCHECK(launch_decode_step(a, m->mega_nwg, m->mega_lds, m->stream));
+        if (m->sparse_alloc && (offset + 1) % 4 == 0)   // the sparse index row of the block this token completes
+            for (auto& ly : m->layers)
+                HIPCHECK(launch_sparse_index(ly.kc, m->page_table, ly.idx, m->cfg.nKV, m->cfg.D, m->dpos, 0, 1, m->stream));
+        HIPCHECK(hipEventRecord(m->slots[0].stop, m->stream));
+        m->written_high = std::max(m->written_high, offset + 1);
+        if (int rc = sync_stream(m)) return rc;
+        record_gpu_time(m, m->slots[0]);
+        if (*(volatile int*)m->abort_host) {
+            // a bounded wait expired: clear the flags and use the kernel-per-op step from now on
+            HIPCHECK(hipMemsetAsync(&m->mega.sync->abort, 0, sizeof(unsigned), m->stream));
+            HIPCHECK(hipMemsetAsync(m->mega.head_done, 0, sizeof(unsigned), m->stream));
+            HIPCHECK(hipStreamSynchronize(m->stream));
+            *(volatile int*)m->abort_host = 0;
+            m->mega_ok = false;
+            m->mega_reason = "a persistent step's bounded wait expired";
+            return set_error(MLXR_E_GPU, "persistent decode step: a bounded wait expired (step result discarded)");
+        }
+        HIPCHECK(hipMemcpy(m->h_logits, m->logits, (size_t)m->cfg.V * 4, hipMemcpyDeviceToHost));
+        *out = m->h_logits;
+        return MLXR_OK;
     }
     for (int start = 0; start < n;) {
         if (start > 0 && cancel.requested()) return set_error(MLXR_E_CANCELLED, "cancelled");   // Transformer.swift:1127

@@ -1,8 +1,8 @@
 """CPU checks of the model-level oracle and of the synthetic model files (no GPU).
 
 The oracle's whole-model forward is pinned against an independent numpy forward of the same
-MLX-format files, read with the `safetensors` package (not the oracle's own reader) and dequantized
-with numpy bit arrays: embedding row, RMSNorm, q/k-norm, half-split RoPE, GQA attention with a
+MLX-format files, read by the test-side reader `qfix.read_safetensors` (numpy over the raw header and
+buffer; independent of the oracle's C reader) and dequantized with numpy bit arrays: embedding row, RMSNorm, q/k-norm, half-split RoPE, GQA attention with a
 bf16 KV cache, SwiGLU, tied / untied lm_head (Transformer.swift:1323-1584).
 """
 import json
