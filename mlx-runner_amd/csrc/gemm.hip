@@ -758,6 +758,160 @@ __global__ __launch_bounds__(256) void qmmx_kernel(QmmXDev a) {
     }
 }
 
+// Small batch over the MLX layout with wide code loads (widths 4 and 8, groups of 8 * gs | K):
+// the same operands and arithmetic as qmmx_kernel, laid out so that each lane's code load is 16
+// bytes. A "span" is 64 bytes of one weight row (4 lanes x 16 bytes, 128 / BITS codes per lane);
+// lane quarter q holds span bytes 16 q .. 16 q + 15, and MFMA step j takes its codes 8 j .. 8 j + 7,
+// matched in the A operand by the same tokens' x at the same k. A span may hold several
+// quantization groups (4-bit gs 32 / 64: lanes of one group are q, or q / 2); each group then runs
+// its own MFMAs with the x of the other groups' lanes zeroed, so every accumulator holds one
+// group and is folded with that group's scale and bias in fp32 (y += s 2^24 acc + b sum x).
+// A batch is QY_NG groups of a row: its spans' codes, the 16-byte runs of scales and biases and
+// every span's x are loaded before any is used (one memory round trip per batch); the token
+// group sums sit in LDS. 16 rows per workgroup, the four waves on a quarter of the batches each,
+// partial sums added in wave order.
+template <int BITS, int GS> struct QyShape {
+    static constexpr int C = 128 / BITS;                 // codes per lane per span
+    static constexpr int SPAN = 4 * C;                   // codes of a row per span
+    static constexpr int NG = GS == 128 ? 4 : 8;         // groups per batch
+    static constexpr int SPB = NG * GS / SPAN;           // spans per batch
+    static constexpr int NGS = SPAN / GS;                // groups per span
+    static constexpr int LPG = GS / C;                   // lane quarters per group
+    static constexpr int STEPS = C / 8;                  // MFMA steps per span
+};
+
+template <int BITS, int GS, int ST, int NW, bool PF>
+__global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
+    using S = QyShape<BITS, GS>;
+    static_assert(S::SPAN >= GS && S::SPB >= 1, "span shape");
+    extern __shared__ __attribute__((aligned(16))) float qy_gsum[];   // [G][8]: token group sums, zero past T
+    __shared__ f32x4_t red[NW][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, q = lane >> 4, T = a.T;
+    const int K = a.K, G = K / GS, NB = G / S::NG;
+    for (int i = tid; i < G * 8; i += 64 * NW) {
+        const int g = i >> 3, t = i & 7;
+        qy_gsum[i] = t < T ? a.gsum[(int64_t)g * T + t] : 0.0f;
+    }
+    const int n = blockIdx.x * 16 + l16;   // the lane's weight row
+    int row = min(n, a.O - 1), part = 0;
+    if (row >= a.o1) {
+        if (row < a.o1 + a.o2) { part = 1; row -= a.o1; }
+        else { part = 2; row -= a.o1 + a.o2; }
+    }
+    const uint8_t* wp = a.w[part] + (int64_t)row * (K / 8 * BITS) + 16 * q;
+    const uint16_t* sp = a.s[part] + (int64_t)row * G;
+    const uint16_t* bp = a.b[part] + (int64_t)row * G;
+    const bool tok = l16 < T;                                   // A row l16: a token
+    const int64_t xo = (int64_t)(tok ? l16 : 0) * K + S::C * q;
+    int nzv[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) nzv[t] = a.nz[min(t, T - 1)];
+    int lo = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) lo |= nzv[t];
+    const int gq = q / S::LPG;                                  // the lane's group within a span
+    __syncthreads();
+    const int b0 = NB * wave / NW, b1 = NB * (wave + 1) / NW;
+    f32x4_t tot = {0.0f, 0.0f, 0.0f, 0.0f};
+    // codes and scales of batch bt (every load unconditional, indices clamped: a load issued in a
+    // branch would make the compiler's later waits count from zero)
+    uint4 cw[S::SPB];
+    uint32_t sw[S::NG / 2], bw[S::NG / 2];
+    auto load_w = [&](int bt) {
+        bt = max(0, min(bt, NB - 1));
+        const int k0 = bt * S::NG * GS;
+#pragma unroll
+        for (int u = 0; u < S::SPB; u++) cw[u] = gload_u4(wp + (int64_t)(k0 + u * S::SPAN) / 8 * BITS);
+        if constexpr (S::NG == 8) {
+            const uint4 s4 = gload_u4(sp + S::NG * bt), b4 = gload_u4(bp + S::NG * bt);
+            sw[0] = s4.x; sw[1] = s4.y; sw[2] = s4.z; sw[3] = s4.w;
+            bw[0] = b4.x; bw[1] = b4.y; bw[2] = b4.z; bw[3] = b4.w;
+        } else {
+            const uint2 s2 = *reinterpret_cast<const uint2*>(sp + S::NG * bt), b2 = *reinterpret_cast<const uint2*>(bp + S::NG * bt);
+            sw[0] = s2.x; sw[1] = s2.y; bw[0] = b2.x; bw[1] = b2.y;
+        }
+    };
+    if constexpr (PF) load_w(b0);
+    for (int bt = b0; bt < b1; bt++) {
+        const int k0 = bt * S::NG * GS;
+        if constexpr (!PF) load_w(bt);
+        half8_t xv[S::SPB][S::STEPS];
+#pragma unroll
+        for (int u = 0; u < S::SPB; u++)
+#pragma unroll
+            for (int j = 0; j < S::STEPS; j++) {
+                const half8_t v = __builtin_bit_cast(half8_t, gload_u4(a.xh + xo + k0 + u * S::SPAN + 8 * j));
+                xv[u][j] = tok ? v : (half8_t)0;
+            }
+        // this batch's codes and scales into their own registers; with PF (waves of three or more
+        // batches) the next batch's stream in behind
+        uint4 cur[S::SPB];
+        uint32_t scur[S::NG / 2], bcur[S::NG / 2];
+#pragma unroll
+        for (int u = 0; u < S::SPB; u++) cur[u] = cw[u];
+#pragma unroll
+        for (int i = 0; i < S::NG / 2; i++) { scur[i] = sw[i]; bcur[i] = bw[i]; }
+        if constexpr (PF) load_w(bt + 1);
+#pragma unroll
+        for (int u = 0; u < S::SPB; u++) {
+            const uint32_t cd[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
+            half8_t wv[S::STEPS], xl[S::STEPS];
+#pragma unroll
+            for (int j = 0; j < S::STEPS; j++) {
+                if constexpr (BITS == 4) {
+                    const uint32_t ev = cd[j] & 0x0F0F0F0Fu, od = (cd[j] >> 4) & 0x0F0F0F0Fu;
+                    wv[j] = __builtin_bit_cast(half8_t, gx_u4{__builtin_amdgcn_perm(od, ev, 0x0C040C00u), __builtin_amdgcn_perm(od, ev, 0x0C050C01u),
+                                                              __builtin_amdgcn_perm(od, ev, 0x0C060C02u), __builtin_amdgcn_perm(od, ev, 0x0C070C03u)});
+                } else {
+                    const uint32_t c0 = cd[2 * j], c1 = cd[2 * j + 1];
+                    wv[j] = __builtin_bit_cast(half8_t, gx_u4{__builtin_amdgcn_perm(0u, c0, 0x0C010C00u), __builtin_amdgcn_perm(0u, c0, 0x0C030C02u),
+                                                              __builtin_amdgcn_perm(0u, c1, 0x0C010C00u), __builtin_amdgcn_perm(0u, c1, 0x0C030C02u)});
+                }
+                xl[j] = (half8_t)0;
+                if (lo && tok) xl[j] = __builtin_bit_cast(half8_t, gload_u4(a.xl + xo + k0 + u * S::SPAN + 8 * j));
+            }
+#pragma unroll
+            for (int gi = 0; gi < S::NGS; gi++) {
+                const bool mine = S::NGS == 1 || gq == gi;
+                f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < S::STEPS; j++) {
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(mine ? xv[u][j] : (half8_t)0, wv[j], acc, 0, 0, 0);
+                    if (lo) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(mine ? xl[j] : (half8_t)0, wv[j], acc, 0, 0, 0);
+                }
+                const int gb = u * S::NGS + gi;                    // group within the batch
+                const uint32_t sr = (scur[gb >> 1] >> (16 * (gb & 1))) & 0xFFFFu, br = (bcur[gb >> 1] >> (16 * (gb & 1))) & 0xFFFFu;
+                const float sv = (ST == 0 ? __uint_as_float(sr << 16) : f16_to_f32((uint16_t)sr)) * 16777216.0f;
+                const float bv = ST == 0 ? __uint_as_float(br << 16) : f16_to_f32((uint16_t)br);
+                const f32x4_t xs = *reinterpret_cast<const f32x4_t*>(qy_gsum + (bt * S::NG + gb) * 8 + 4 * q);
+#pragma unroll
+                for (int i = 0; i < 4; i++) tot[i] = fmaf(sv, acc[i], fmaf(bv, xs[i], tot[i]));
+            }
+        }
+    }
+    red[wave][lane] = tot;
+    __syncthreads();
+    if (wave != 0 || n >= a.O) return;
+    f32x4_t sum = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < NW; w++) sum += red[w][lane];
+    const float bias = a.bias[part] ? ld_scale<ST>(a.bias[part] + row) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int t = 4 * q + i;
+        if (t < T) a.y[(int64_t)t * a.ys + n] = sum[i] * a.inv[t] + bias;
+    }
+}
+
+// qmmy_kernel's shapes: 4-bit at gs 32 / 64 / 128, 8-bit at gs 32 / 64; K a multiple of a batch; the
+// group sums' LDS within 64 KiB
+static bool qmmy_supported(int K, int bits, int gs) {
+    if (!((bits == 4 && (gs == 32 || gs == 64 || gs == 128)) || (bits == 8 && (gs == 32 || gs == 64)))) return false;
+    const int ng = gs == 128 ? 4 : 8;
+    return K % (ng * gs) == 0 && (size_t)(K / gs) * 32 <= 65536;
+}
+
 bool qmmx_supported(int K, int bits, int gs) {
     return (bits == 4 || bits == 8) && (gs == 32 || gs == 64 || gs == 128) && K % gs == 0 && K % 32 == 0;
 }
@@ -777,6 +931,29 @@ hipError_t launch_qmmx(const QmmSmallArgs& a, hipStream_t s) {
     d.K = a.K; d.O = a.O; d.T = a.T; d.ys = a.y_stride;
     d.xh = a.xbf; d.xl = a.xlo; d.gsum = a.xgs; d.inv = a.xsc; d.nz = a.xnz; d.y = a.y;
     const dim3 grid((unsigned)((a.O + 15) / 16));
+    if (qmmy_supported(a.K, a.bits, a.gs)) {
+        const size_t lds = (size_t)(a.K / a.gs) * 32;
+        // eight waves (an eighth of the batches each) where a quarter of the batches would be a
+        // long chain per wave
+        // long chain per wave; the next batch's loads in flight behind each batch where a wave has
+        // three or more
+        const int nb = a.K / a.gs / (a.gs == 128 ? 4 : 8);
+        const bool w8 = nb >= 16, pf = nb / (w8 ? 8 : 4) >= 3;
+#define QMMY_GO(B, GS) if (a.bits == B && a.gs == GS) { \
+        if (w8 && pf) { \
+            if (a.st == 0) hipLaunchKernelGGL((qmmy_kernel<B, GS, 0, 8, true>), grid, dim3(512), lds, s, d); \
+            else hipLaunchKernelGGL((qmmy_kernel<B, GS, 1, 8, true>), grid, dim3(512), lds, s, d); \
+        } else if (w8) { \
+            if (a.st == 0) hipLaunchKernelGGL((qmmy_kernel<B, GS, 0, 8, false>), grid, dim3(512), lds, s, d); \
+            else hipLaunchKernelGGL((qmmy_kernel<B, GS, 1, 8, false>), grid, dim3(512), lds, s, d); \
+        } else { \
+            if (a.st == 0) hipLaunchKernelGGL((qmmy_kernel<B, GS, 0, 4, false>), grid, dim3(256), lds, s, d); \
+            else hipLaunchKernelGGL((qmmy_kernel<B, GS, 1, 4, false>), grid, dim3(256), lds, s, d); \
+        } \
+        return hipGetLastError(); }
+        QMMY_GO(4, 32) QMMY_GO(4, 64) QMMY_GO(4, 128) QMMY_GO(8, 32) QMMY_GO(8, 64)
+#undef QMMY_GO
+    }
 #define QMMX_GO(B, GS) if (a.bits == B && a.gs == GS) { \
         if (a.st == 0) hipLaunchKernelGGL((qmmx_kernel<B, GS, 0>), grid, dim3(64 * QX_WAVES), 0, s, d); \
         else hipLaunchKernelGGL((qmmx_kernel<B, GS, 1>), grid, dim3(64 * QX_WAVES), 0, s, d); \

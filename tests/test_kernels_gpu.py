@@ -103,6 +103,33 @@ def test_qmm_small_batch(gpu, bits):
         assert max_rel_err(got, fx.oracle(oracle).matmul_f64(x[:, :K])) < TOL, T
 
 
+@pytest.mark.parametrize("bits,gs,st", [(4, 32, "bf16"), (4, 64, "f16"), (4, 128, "bf16"), (8, 32, "f16"), (8, 64, "bf16"),
+                                         (8, 128, "bf16")])
+def test_qmm_small_batch_wide_loads(gpu, bits, gs, st):
+    """The small-batch kernel with 16-byte code loads (several groups per load at 4-bit gs 32 / 64:
+    one MFMA set per group, the other groups' lanes zeroed): K of several batches per wave (the
+    eight-wave launch at 4096 / gs 32), two fused parts with ragged row counts, f16 and bf16
+    scales, T = 1..8 with fp32 inputs (x lo parts in use) and bf16-valued inputs (no lo parts);
+    1e-3 against the fp64 product. 8-bit gs 128 runs the per-group kernel."""
+    K = 4096 if gs == 32 else 2048
+    fa = QuantFixture(40, K, bits, gs, st=st, seed=K + bits, fast=True)
+    fb = QuantFixture(27, K, bits, gs, st=st, seed=K + bits + 1, fast=True)
+    qm = (gpu.QMat * 2)(fa.device(gpu), fb.device(gpu))
+    O = fa.O + fb.O
+    for T in (1, 3, 4, 8):
+        rng = np.random.default_rng(T * 31 + bits)
+        for bf16_x in (False, True):
+            x = rng.normal(0, 1, (T, K)).astype(np.float32)
+            if bf16_x:
+                x = bf16_to_f32(bf16_round(x)).reshape(T, K)
+            dx = gpu.DeviceArray.from_numpy(x)
+            dy = gpu.DeviceArray.from_numpy(np.zeros((T, O), np.float32))
+            gpu.check(gpu.lib.mlxr_k_qmm(qm, 2, K, bits, gs, 0 if st == "bf16" else 1, T, dx.ptr, K, dy.ptr, O))
+            gpu.synchronize()
+            ref = np.concatenate([fa.oracle(oracle).matmul_f64(x), fb.oracle(oracle).matmul_f64(x)], axis=1)
+            assert max_rel_err(dy.numpy(), ref) < TOL, (T, bf16_x)
+
+
 def qgemm(mlxr, fx, x):
     T = x.shape[0]
     qm = (mlxr.QMat * 1)(fx.device(mlxr))
