@@ -771,7 +771,8 @@ __global__ __launch_bounds__(256) void qmmx_kernel(QmmXDev a) {
 // group sums sit in LDS. 16 rows per workgroup, the four waves on a quarter of the batches each,
 // partial sums added in wave order.
 template <int BITS, int GS> struct QyShape {
-    static constexpr int C = 128 / BITS;                 // codes per lane per span
+    static constexpr int C = BITS == 8 ? 16 : 32;        // codes per lane per span
+    static constexpr int NDW = C * BITS / 32;            // their dwords (2, 3, 4 or 6)
     static constexpr int SPAN = 4 * C;                   // codes of a row per span
     static constexpr int NG = GS == 128 ? 4 : 8;         // groups per batch
     static constexpr int SPB = NG * GS / SPAN;           // spans per batch
@@ -799,7 +800,7 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
         if (row < a.o1 + a.o2) { part = 1; row -= a.o1; }
         else { part = 2; row -= a.o1 + a.o2; }
     }
-    const uint8_t* wp = a.w[part] + (int64_t)row * (K / 8 * BITS) + 16 * q;
+    const uint8_t* wp = a.w[part] + (int64_t)row * (K / 8 * BITS) + 4 * S::NDW * q;
     const uint16_t* sp = a.s[part] + (int64_t)row * G;
     const uint16_t* bp = a.b[part] + (int64_t)row * G;
     const bool tok = l16 < T;                                   // A row l16: a token
@@ -816,13 +817,23 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
     f32x4_t tot = {0.0f, 0.0f, 0.0f, 0.0f};
     // codes and scales of batch bt (every load unconditional, indices clamped: a load issued in a
     // branch would make the compiler's later waits count from zero)
-    uint4 cw[S::SPB];
+    uint32_t cw[S::SPB][S::NDW];
     uint32_t sw[S::NG / 2], bw[S::NG / 2];
     auto load_w = [&](int bt) {
         bt = max(0, min(bt, NB - 1));
         const int k0 = bt * S::NG * GS;
 #pragma unroll
-        for (int u = 0; u < S::SPB; u++) cw[u] = gload_u4(wp + (int64_t)(k0 + u * S::SPAN) / 8 * BITS);
+        for (int u = 0; u < S::SPB; u++) {
+            const uint8_t* p = wp + (int64_t)(k0 + u * S::SPAN) / 8 * BITS;
+            if constexpr (S::NDW == 4) {
+                const uint4 v = gload_u4(p);
+                cw[u][0] = v.x; cw[u][1] = v.y; cw[u][2] = v.z; cw[u][3] = v.w;
+            } else {
+                typedef const __attribute__((address_space(1))) uint32_t* gp32;
+#pragma unroll
+                for (int i = 0; i < S::NDW; i++) cw[u][i] = *((gp32)p + i);
+            }
+        }
         if constexpr (S::NG == 8) {
             const uint4 s4 = gload_u4(sp + S::NG * bt), b4 = gload_u4(bp + S::NG * bt);
             sw[0] = s4.x; sw[1] = s4.y; sw[2] = s4.z; sw[3] = s4.w;
@@ -846,16 +857,18 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
             }
         // this batch's codes and scales into their own registers; with PF (waves of three or more
         // batches) the next batch's stream in behind
-        uint4 cur[S::SPB];
+        uint32_t cur[S::SPB][S::NDW];
         uint32_t scur[S::NG / 2], bcur[S::NG / 2];
 #pragma unroll
-        for (int u = 0; u < S::SPB; u++) cur[u] = cw[u];
+        for (int u = 0; u < S::SPB; u++)
+#pragma unroll
+            for (int i = 0; i < S::NDW; i++) cur[u][i] = cw[u][i];
 #pragma unroll
         for (int i = 0; i < S::NG / 2; i++) { scur[i] = sw[i]; bcur[i] = bw[i]; }
         if constexpr (PF) load_w(bt + 1);
 #pragma unroll
         for (int u = 0; u < S::SPB; u++) {
-            const uint32_t cd[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
+            const uint32_t* cd = cur[u];
             half8_t wv[S::STEPS], xl[S::STEPS];
 #pragma unroll
             for (int j = 0; j < S::STEPS; j++) {
@@ -863,10 +876,20 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
                     const uint32_t ev = cd[j] & 0x0F0F0F0Fu, od = (cd[j] >> 4) & 0x0F0F0F0Fu;
                     wv[j] = __builtin_bit_cast(half8_t, gx_u4{__builtin_amdgcn_perm(od, ev, 0x0C040C00u), __builtin_amdgcn_perm(od, ev, 0x0C050C01u),
                                                               __builtin_amdgcn_perm(od, ev, 0x0C060C02u), __builtin_amdgcn_perm(od, ev, 0x0C070C03u)});
-                } else {
+                } else if constexpr (BITS == 8) {
                     const uint32_t c0 = cd[2 * j], c1 = cd[2 * j + 1];
                     wv[j] = __builtin_bit_cast(half8_t, gx_u4{__builtin_amdgcn_perm(0u, c0, 0x0C010C00u), __builtin_amdgcn_perm(0u, c0, 0x0C030C02u),
                                                               __builtin_amdgcn_perm(0u, c1, 0x0C010C00u), __builtin_amdgcn_perm(0u, c1, 0x0C030C02u)});
+                } else {
+                    // codes 8 j .. 8 j + 7: bits 8 BITS j .. + 8 BITS of the lane's little-endian stream
+                    const int b = 8 * BITS * j, i0 = b >> 5, sh = b & 31;
+                    const uint64_t w = ((uint64_t)(i0 + 1 < S::NDW ? cd[i0 + 1] : 0u) << 32 | cd[i0]) >> sh;
+                    constexpr uint32_t m = (1u << BITS) - 1;
+                    uint32_t h[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        h[e] = ((uint32_t)(w >> (2 * e * BITS)) & m) | (((uint32_t)(w >> ((2 * e + 1) * BITS)) & m) << 16);
+                    wv[j] = __builtin_bit_cast(half8_t, gx_u4{h[0], h[1], h[2], h[3]});
                 }
                 xl[j] = (half8_t)0;
                 if (lo && tok) xl[j] = __builtin_bit_cast(half8_t, gload_u4(a.xl + xo + k0 + u * S::SPAN + 8 * j));
@@ -907,12 +930,14 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
 // qmmy_kernel's shapes: 4-bit at gs 32 / 64 / 128, 8-bit at gs 32 / 64; K a multiple of a batch; the
 // group sums' LDS within 64 KiB
 static bool qmmy_supported(int K, int bits, int gs) {
-    if (!((bits == 4 && (gs == 32 || gs == 64 || gs == 128)) || (bits == 8 && (gs == 32 || gs == 64)))) return false;
+    const bool b32 = bits == 2 || bits == 3 || bits == 4 || bits == 6;   // 32 codes per lane
+    if (!((b32 && (gs == 32 || gs == 64 || gs == 128)) || (bits == 8 && (gs == 32 || gs == 64)))) return false;
     const int ng = gs == 128 ? 4 : 8;
     return K % (ng * gs) == 0 && (size_t)(K / gs) * 32 <= 65536;
 }
 
 bool qmmx_supported(int K, int bits, int gs) {
+    if (qmmy_supported(K, bits, gs)) return true;
     return (bits == 4 || bits == 8) && (gs == 32 || gs == 64 || gs == 128) && K % gs == 0 && K % 32 == 0;
 }
 
@@ -951,7 +976,9 @@ hipError_t launch_qmmx(const QmmSmallArgs& a, hipStream_t s) {
             else hipLaunchKernelGGL((qmmy_kernel<B, GS, 1, 4, false>), grid, dim3(256), lds, s, d); \
         } \
         return hipGetLastError(); }
-        QMMY_GO(4, 32) QMMY_GO(4, 64) QMMY_GO(4, 128) QMMY_GO(8, 32) QMMY_GO(8, 64)
+        QMMY_GO(2, 32) QMMY_GO(2, 64) QMMY_GO(2, 128) QMMY_GO(3, 32) QMMY_GO(3, 64) QMMY_GO(3, 128)
+        QMMY_GO(4, 32) QMMY_GO(4, 64) QMMY_GO(4, 128) QMMY_GO(6, 32) QMMY_GO(6, 64) QMMY_GO(6, 128)
+        QMMY_GO(8, 32) QMMY_GO(8, 64)
 #undef QMMY_GO
     }
 #define QMMX_GO(B, GS) if (a.bits == B && a.gs == GS) { \

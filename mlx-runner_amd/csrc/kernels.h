@@ -38,8 +38,9 @@ struct QmmSmallArgs {
     int K = 0, bits = 4, gs = 64, st = 0, O = 0, T = 1;
     const float* x = nullptr; int x_stride = 0;
     float* y = nullptr; int y_stride = 0;
-    // optional pre-pass scratch (as QGemmArgs'): with it, widths 4 and 8 (qmmx_supported) run on
-    // the matrix cores (launch_qmmx); without it, or for other widths, on the fp32 vector path
+    // optional pre-pass scratch (as QGemmArgs'): with it, the shapes qmmx_supported accepts (widths
+    // 2 / 3 / 4 / 6 / 8) run on the matrix cores (launch_qmmx); without it, or for other shapes, on
+    // the fp32 vector path
     uint16_t* xbf = nullptr; uint16_t* xlo = nullptr; float* xgs = nullptr; float* xsc = nullptr; int* xnz = nullptr;
 };
 hipError_t launch_qmm_small(const QmmSmallArgs& a, hipStream_t s);

@@ -104,10 +104,12 @@ def test_qmm_small_batch(gpu, bits):
 
 
 @pytest.mark.parametrize("bits,gs,st", [(4, 32, "bf16"), (4, 64, "f16"), (4, 128, "bf16"), (8, 32, "f16"), (8, 64, "bf16"),
-                                         (8, 128, "bf16")])
+                                         (8, 128, "bf16"), (2, 64, "bf16"), (3, 32, "bf16"), (3, 128, "f16"), (6, 64, "f16"),
+                                         (6, 128, "bf16")])
 def test_qmm_small_batch_wide_loads(gpu, bits, gs, st):
-    """The small-batch kernel with 16-byte code loads (several groups per load at 4-bit gs 32 / 64:
-    one MFMA set per group, the other groups' lanes zeroed): K of several batches per wave (the
+    """The small-batch kernel with wide code loads (32 codes per lane at 2 / 3 / 4 / 6 bits, 16 at 8;
+    several groups per load at gs 32 / 64: one MFMA set per group, the other groups' lanes zeroed;
+    3- and 6-bit codes straddling dwords): K of several batches per wave (the
     eight-wave launch at 4096 / gs 32), two fused parts with ragged row counts, f16 and bf16
     scales, T = 1..8 with fp32 inputs (x lo parts in use) and bf16-valued inputs (no lo parts);
     1e-3 against the fp64 product. 8-bit gs 128 runs the per-group kernel."""
