@@ -768,7 +768,9 @@ __global__ __launch_bounds__(256) void qmmx_kernel(QmmXDev a) {
 // group and is folded with that group's scale and bias in fp32 (y += s 2^24 acc + b sum x).
 // A batch is QY_NG groups of a row: its spans' codes, the 16-byte runs of scales and biases and
 // every span's x are loaded before any is used (one memory round trip per batch); the token
-// group sums sit in LDS. 16 rows per workgroup, the four waves on a quarter of the batches each,
+// group sums sit in LDS. At 32 codes per lane the x of a batch reaches LDS by buffer -> LDS copies
+// (1 KB of 4 tokens' chunks per copy, no lane loading what another lane loads) and the A operands
+// are read from there. 16 rows per workgroup, the four waves on a quarter of the batches each,
 // partial sums added in wave order.
 template <int BITS, int GS> struct QyShape {
     static constexpr int C = BITS == 8 ? 16 : 32;        // codes per lane per span
@@ -785,11 +787,18 @@ template <int BITS, int GS, int ST, int NW, bool PF>
 __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
     using S = QyShape<BITS, GS>;
     static_assert(S::SPAN >= GS && S::SPB >= 1, "span shape");
-    extern __shared__ __attribute__((aligned(16))) float qy_gsum[];   // [G][8]: token group sums, zero past T
+    // dynamic LDS: [G][8] token group sums (zero past T), then (32 codes per lane) each wave's x
+    // buffers: per span, TT = T rounded up to 4 token rows of 256 bytes, 16-byte chunk c of token t
+    // at slot c ^ t (a B-operand read of 16 tokens' same chunk hits distinct banks)
+    extern __shared__ __attribute__((aligned(16))) float qy_gsum[];
     __shared__ f32x4_t red[NW][64];
+    constexpr bool XL = S::C == 32;                            // x through LDS
+    constexpr int NBUF = PF ? 2 : 1;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, q = lane >> 4, T = a.T;
     const int K = a.K, G = K / GS, NB = G / S::NG;
+    const int TT = (T + 3) & ~3, XWB = S::SPB * TT * 256;
+    uint8_t* xlds = reinterpret_cast<uint8_t*>(qy_gsum) + (size_t)(K / GS) * 32;
     for (int i = tid; i < G * 8; i += 64 * NW) {
         const int g = i >> 3, t = i & 7;
         qy_gsum[i] = t < T ? a.gsum[(int64_t)g * T + t] : 0.0f;
@@ -843,18 +852,54 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
             sw[0] = s2.x; sw[1] = s2.y; bw[0] = b2.x; bw[1] = b2.y;
         }
     };
-    if constexpr (PF) load_w(b0);
-    for (int bt = b0; bt < b1; bt++) {
+    // x of batch bt into LDS buffer buf by buffer -> LDS copies: per span and 4 tokens one 1 KB copy,
+    // lane i: token 4 tq + i / 16, chunk (i & 15) ^ token (rows past T repeat row T - 1, unread)
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.xh), 0, T * K * 2, 0x00020000);
+    auto dma_x = [&](int bt, int buf) {
+        bt = max(0, min(bt, NB - 1));
         const int k0 = bt * S::NG * GS;
-        if constexpr (!PF) load_w(bt);
-        half8_t xv[S::SPB][S::STEPS];
+        uint8_t* rb = xlds + (size_t)(wave * NBUF + buf) * XWB;
 #pragma unroll
         for (int u = 0; u < S::SPB; u++)
-#pragma unroll
-            for (int j = 0; j < S::STEPS; j++) {
-                const half8_t v = __builtin_bit_cast(half8_t, gload_u4(a.xh + xo + k0 + u * S::SPAN + 8 * j));
-                xv[u][j] = tok ? v : (half8_t)0;
+            for (int tq = 0; tq < TT / 4; tq++) {
+                const int t = 4 * tq + (lane >> 4), c = (lane & 15) ^ t;
+                const uint32_t off = (uint32_t)(min(t, T - 1) * K + k0 + u * S::SPAN + 8 * c) * 2u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(rb + (u * TT + 4 * tq) * 256), 16, off, 0, 0, 0);
             }
+    };
+    const int mr = min(l16, TT - 1);
+    if constexpr (PF) {
+        load_w(b0);
+        if constexpr (XL) dma_x(b0, 0);
+    }
+    for (int bt = b0; bt < b1; bt++) {
+        const int k0 = bt * S::NG * GS;
+        if constexpr (!PF) {
+            load_w(bt);
+            if constexpr (XL) dma_x(bt, 0);
+        }
+        half8_t xv[S::SPB][S::STEPS];
+        if constexpr (XL) {
+            // this batch's copies (and codes) have landed
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            asm volatile("" ::: "memory");
+            const uint8_t* rb = xlds + (size_t)(wave * NBUF + (PF ? (bt - b0) & 1 : 0)) * XWB;
+#pragma unroll
+            for (int u = 0; u < S::SPB; u++)
+#pragma unroll
+                for (int j = 0; j < S::STEPS; j++) {
+                    const half8_t v = *reinterpret_cast<const half8_t*>(rb + (u * TT + mr) * 256 + ((4 * q + j) ^ mr) * 16);
+                    xv[u][j] = tok ? v : (half8_t)0;
+                }
+        } else {
+#pragma unroll
+            for (int u = 0; u < S::SPB; u++)
+#pragma unroll
+                for (int j = 0; j < S::STEPS; j++) {
+                    const half8_t v = __builtin_bit_cast(half8_t, gload_u4(a.xh + xo + k0 + u * S::SPAN + 8 * j));
+                    xv[u][j] = tok ? v : (half8_t)0;
+                }
+        }
         // this batch's codes and scales into their own registers; with PF (waves of three or more
         // batches) the next batch's stream in behind
         uint32_t cur[S::SPB][S::NDW];
@@ -865,10 +910,13 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
             for (int i = 0; i < S::NDW; i++) cur[u][i] = cw[u][i];
 #pragma unroll
         for (int i = 0; i < S::NG / 2; i++) { scur[i] = sw[i]; bcur[i] = bw[i]; }
-        if constexpr (PF) load_w(bt + 1);
+        if constexpr (PF) {
+            load_w(bt + 1);
+            if constexpr (XL) dma_x(bt + 1, (bt + 1 - b0) & 1);
+        }
 #pragma unroll
         for (int u = 0; u < S::SPB; u++) {
-            const uint32_t* cd = cur[u];
+#define cd cur[u]
             half8_t wv[S::STEPS], xl[S::STEPS];
 #pragma unroll
             for (int j = 0; j < S::STEPS; j++) {
@@ -894,6 +942,7 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
                 xl[j] = (half8_t)0;
                 if (lo && tok) xl[j] = __builtin_bit_cast(half8_t, gload_u4(a.xl + xo + k0 + u * S::SPAN + 8 * j));
             }
+#undef cd
 #pragma unroll
             for (int gi = 0; gi < S::NGS; gi++) {
                 const bool mine = S::NGS == 1 || gq == gi;
@@ -927,8 +976,8 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
     }
 }
 
-// qmmy_kernel's shapes: 4-bit at gs 32 / 64 / 128, 8-bit at gs 32 / 64; K a multiple of a batch; the
-// group sums' LDS within 64 KiB
+// qmmy_kernel's shapes: widths 2 / 3 / 4 / 6 at gs 32 / 64 / 128, 8-bit at gs 32 / 64; K a multiple of
+// a batch; the group sums' LDS within 64 KiB
 static bool qmmy_supported(int K, int bits, int gs) {
     const bool b32 = bits == 2 || bits == 3 || bits == 4 || bits == 6;   // 32 codes per lane
     if (!((b32 && (gs == 32 || gs == 64 || gs == 128)) || (bits == 8 && (gs == 32 || gs == 64)))) return false;
@@ -957,13 +1006,33 @@ hipError_t launch_qmmx(const QmmSmallArgs& a, hipStream_t s) {
     d.xh = a.xbf; d.xl = a.xlo; d.gsum = a.xgs; d.inv = a.xsc; d.nz = a.xnz; d.y = a.y;
     const dim3 grid((unsigned)((a.O + 15) / 16));
     if (qmmy_supported(a.K, a.bits, a.gs)) {
-        const size_t lds = (size_t)(a.K / a.gs) * 32;
         // eight waves (an eighth of the batches each) where a quarter of the batches would be a
-        // long chain per wave
         // long chain per wave; the next batch's loads in flight behind each batch where a wave has
-        // three or more
-        const int nb = a.K / a.gs / (a.gs == 128 ? 4 : 8);
-        const bool w8 = nb >= 16, pf = nb / (w8 ? 8 : 4) >= 3;
+        // three or more; LDS: group sums, then (32 codes per lane) every wave's x buffers
+        const int ng = a.gs == 128 ? 4 : 8, nb = a.K / a.gs / ng;
+        bool w8 = nb >= 16, pf = nb / (w8 ? 8 : 4) >= 3;
+        const int C = a.bits == 8 ? 16 : 32, spb = ng * a.gs / (4 * C), tt = (a.T + 3) & ~3;
+        auto lds_of = [&](bool w, bool p) {
+            return (size_t)(a.K / a.gs) * 32 + (C == 32 ? (size_t)(w ? 8 : 4) * (p ? 2 : 1) * spb * tt * 256 : 0);
+        };
+        // (160 KiB of LDS less the 8 KiB of the waves' partial sums)
+        constexpr size_t QY_LDS_MAX = 152 * 1024;
+        if (lds_of(w8, pf) > QY_LDS_MAX) w8 = pf = false;
+        const size_t lds = lds_of(w8, pf);
+        if (lds > QY_LDS_MAX) return hipErrorInvalidValue;
+        static bool attr = false;
+        if (!attr) {
+#define QMMY_ATTR1(B, GS, ST) \
+            for (const void* f : {(const void*)qmmy_kernel<B, GS, ST, 8, true>, (const void*)qmmy_kernel<B, GS, ST, 8, false>, \
+                                  (const void*)qmmy_kernel<B, GS, ST, 4, false>}) \
+                if (hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)QY_LDS_MAX)) return e;
+#define QMMY_ATTR(B) QMMY_ATTR1(B, 32, 0) QMMY_ATTR1(B, 64, 0) QMMY_ATTR1(B, 128, 0) QMMY_ATTR1(B, 32, 1) QMMY_ATTR1(B, 64, 1) QMMY_ATTR1(B, 128, 1)
+            QMMY_ATTR(2) QMMY_ATTR(3) QMMY_ATTR(4) QMMY_ATTR(6)
+            QMMY_ATTR1(8, 32, 0) QMMY_ATTR1(8, 64, 0) QMMY_ATTR1(8, 32, 1) QMMY_ATTR1(8, 64, 1)
+#undef QMMY_ATTR
+#undef QMMY_ATTR1
+            attr = true;
+        }
 #define QMMY_GO(B, GS) if (a.bits == B && a.gs == GS) { \
         if (w8 && pf) { \
             if (a.st == 0) hipLaunchKernelGGL((qmmy_kernel<B, GS, 0, 8, true>), grid, dim3(512), lds, s, d); \
