@@ -238,7 +238,7 @@ def sweep_main(a):
         "metric": "quantized matvec / GEMM sweep (8B-shape projections, configs[3])",
         "value": round(sum(c["GBs"] for c in dec) / len(dec), 1), "unit": "GB/s (mean over the T = 1 cells)",
         "n_gpus": 1, "steps": len(cells), "warmup": 1, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u3/u4/u6/u8 weights (bf16 scale/bias); fp32 activations and arithmetic at T = 1 and 4; T = 512: exact codes and x as f16 hi + lo on the f16 matrix cores (the lo products skipped where x is bf16-valued, as here), group scale / bias in fp32, fp32 accumulate",
+        "vs_baseline": None, "dtype": "u3/u4/u6/u8 weights (bf16 scale/bias); fp32 activations; T = 1: fp32 arithmetic; T = 4 and exact codes and x as f16 hi + lo on the f16 matrix cores (the lo products skipped where x is bf16-valued, as here), group scale / bias in fp32, fp32 accumulate",
         "data": "synthetic: random code words and bf16 scales / biases, N(0,1) activations rounded to bf16",
         "config": {"workload": "configs[3]: K,N in (4096,14336),(14336,4096),(4096,151936) x 3b g32, 4b g64, 6b g128, 8b g64 x T in 1,4,512"},
         "roofline": {"bound": "hbm", "kernel": f"qmv_kernel, best cell K={best_dec['K']} N={best_dec['N']} {best_dec['bits']}b",
