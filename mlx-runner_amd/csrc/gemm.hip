@@ -812,8 +812,8 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
     const uint8_t* wp = a.w[part] + (int64_t)row * (K / 8 * BITS) + 4 * S::NDW * q;
     const uint16_t* sp = a.s[part] + (int64_t)row * G;
     const uint16_t* bp = a.b[part] + (int64_t)row * G;
-    const bool tok = l16 < T;                                   // A row l16: a token
-    const int64_t xo = (int64_t)(tok ? l16 : 0) * K + S::C * q;
+    const int TT0 = (T + 3) & ~3;
+    const int64_t xo = (int64_t)min(S::NGS == 4 ? (int)(l16 % TT0) : l16, T - 1) * K + S::C * q;   // the token of A row l16
     int nzv[8];
 #pragma unroll
     for (int t = 0; t < 8; t++) nzv[t] = a.nz[min(t, T - 1)];
@@ -867,7 +867,14 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(rb + (u * TT + 4 * tq) * 256), 16, off, 0, 0, 0);
             }
     };
-    const int mr = min(l16, TT - 1);
+    // A rows: NGP = 16 / TT group slots of TT token rows; row l16 is token ta of slot pa. D rows
+    // 4 q .. 4 q + 3: tokens td0 .. td0 + 3 of slot pd. One MFMA set covers NGP groups of a span.
+    // (PACK: spans of four groups; otherwise one slot: row l16 is token l16, D rows tokens 4 q ..)
+    constexpr bool PACK = S::NGS == 4;
+    const int NGP = PACK ? 16 / TT : 1, pa = PACK ? l16 / TT : 0, ta = PACK ? l16 % TT : l16;
+    const int pd = PACK ? (4 * q) / TT : 0, td0 = PACK ? (4 * q) % TT : 4 * q;
+    const bool tva = ta < T;
+    const int mr = min(ta, TT - 1);
     if constexpr (PF) {
         load_w(b0);
         if constexpr (XL) dma_x(b0, 0);
@@ -889,7 +896,7 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
 #pragma unroll
                 for (int j = 0; j < S::STEPS; j++) {
                     const half8_t v = *reinterpret_cast<const half8_t*>(rb + (u * TT + mr) * 256 + ((4 * q + j) ^ mr) * 16);
-                    xv[u][j] = tok ? v : (half8_t)0;
+                    xv[u][j] = tva ? v : (half8_t)0;
                 }
         } else {
 #pragma unroll
@@ -897,7 +904,7 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
 #pragma unroll
                 for (int j = 0; j < S::STEPS; j++) {
                     const half8_t v = __builtin_bit_cast(half8_t, gload_u4(a.xh + xo + k0 + u * S::SPAN + 8 * j));
-                    xv[u][j] = tok ? v : (half8_t)0;
+                    xv[u][j] = tva ? v : (half8_t)0;
                 }
         }
         // this batch's codes and scales into their own registers; with PF (waves of three or more
@@ -940,23 +947,36 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
                     wv[j] = __builtin_bit_cast(half8_t, gx_u4{h[0], h[1], h[2], h[3]});
                 }
                 xl[j] = (half8_t)0;
-                if (lo && tok) xl[j] = __builtin_bit_cast(half8_t, gload_u4(a.xl + xo + k0 + u * S::SPAN + 8 * j));
+                if (lo && tva) xl[j] = __builtin_bit_cast(half8_t, gload_u4(a.xl + xo + k0 + u * S::SPAN + 8 * j));
             }
 #undef cd
 #pragma unroll
-            for (int gi = 0; gi < S::NGS; gi++) {
-                const bool mine = S::NGS == 1 || gq == gi;
+            for (int set = 0; set < S::NGS; set++) {
+                if (PACK && set * NGP >= S::NGS) break;
+                // A row l16 carries group set * NGP + pa: the x of the lanes holding that group's codes
+                const bool mine = S::NGS == 1 || set * NGP + pa == gq;
                 f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int j = 0; j < S::STEPS; j++) {
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(mine ? xv[u][j] : (half8_t)0, wv[j], acc, 0, 0, 0);
                     if (lo) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(mine ? xl[j] : (half8_t)0, wv[j], acc, 0, 0, 0);
                 }
-                const int gb = u * S::NGS + gi;                    // group within the batch
-                const uint32_t sr = (scur[gb >> 1] >> (16 * (gb & 1))) & 0xFFFFu, br = (bcur[gb >> 1] >> (16 * (gb & 1))) & 0xFFFFu;
-                const float sv = (ST == 0 ? __uint_as_float(sr << 16) : f16_to_f32((uint16_t)sr)) * 16777216.0f;
-                const float bv = ST == 0 ? __uint_as_float(br << 16) : f16_to_f32((uint16_t)br);
-                const f32x4_t xs = *reinterpret_cast<const f32x4_t*>(qy_gsum + (bt * S::NG + gb) * 8 + 4 * q);
+                // this lane's D rows: group set * NGP + pd of the span, tokens td0 ..
+                const int gs_ = set * NGP + pd;
+                const bool live = !PACK || gs_ < S::NGS;
+                const int gb = u * S::NGS + min(gs_, S::NGS - 1);   // group within the batch
+                uint32_t sd = scur[0], bd = bcur[0];
+                if constexpr (PACK) {
+#pragma unroll
+                    for (int i = 1; i < S::NG / 2; i++)
+                        if ((gb >> 1) == i) { sd = scur[i]; bd = bcur[i]; }
+                } else {
+                    sd = scur[gb >> 1]; bd = bcur[gb >> 1];
+                }
+                const uint32_t sr = (sd >> (16 * (gb & 1))) & 0xFFFFu, br = (bd >> (16 * (gb & 1))) & 0xFFFFu;
+                const float sv = live ? (ST == 0 ? __uint_as_float(sr << 16) : f16_to_f32((uint16_t)sr)) * 16777216.0f : 0.0f;
+                const float bv = live ? (ST == 0 ? __uint_as_float(br << 16) : f16_to_f32((uint16_t)br)) : 0.0f;
+                const f32x4_t xs = *reinterpret_cast<const f32x4_t*>(qy_gsum + (bt * S::NG + gb) * 8 + td0);
 #pragma unroll
                 for (int i = 0; i < 4; i++) tot[i] = fmaf(sv, acc[i], fmaf(bv, xs[i], tot[i]));
             }
@@ -964,14 +984,16 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
     }
     red[wave][lane] = tot;
     __syncthreads();
-    if (wave != 0 || n >= a.O) return;
-    f32x4_t sum = red[0][lane];
+    // the lanes of slot 0 add every wave's and every slot's partial sums of their tokens, in order
+    if (wave != 0 || pd != 0 || n >= a.O) return;
+    f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int w = 1; w < NW; w++) sum += red[w][lane];
+    for (int w = 0; w < NW; w++)
+        for (int p = 0; p < NGP; p++) sum += red[w][lane + 16 * p * (TT / 4)];
     const float bias = a.bias[part] ? ld_scale<ST>(a.bias[part] + row) : 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int t = 4 * q + i;
+        const int t = td0 + i;
         if (t < T) a.y[(int64_t)t * a.ys + n] = sum[i] * a.inv[t] + bias;
     }
 }
