@@ -87,8 +87,10 @@ __device__ __forceinline__ void load_chunk(const uint8_t* p, uint32_t* w) {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
-// XNORM: x is normalised into LDS by the workgroup (K floats). KS: the waves split K over the same rows.
-template <int BITS, int ST, bool XNORM, bool KS>
+// XNORM: x is normalised into LDS by the workgroup (K floats). XCOPY: x is copied into LDS as it is
+// (the four waves then read it from there: each wave's x would otherwise come through L2 once per
+// four rows, more bytes than its weights). KS: the waves split K over the same rows.
+template <int BITS, int ST, bool XNORM, bool KS, bool XCOPY = false>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
     extern __shared__ __attribute__((aligned(16))) float xs_lds[];
     __shared__ float red[QMV_WAVES];
@@ -112,6 +114,12 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
             float4 o; o.x = v.x * inv * w.x; o.y = v.y * inv * w.y; o.z = v.z * inv * w.z; o.w = v.w * inv * w.w;
             *reinterpret_cast<float4*>(xs_lds + i) = o;
         }
+        __syncthreads();
+        xsrc = xs_lds;
+    }
+    if constexpr (XCOPY && !XNORM) {
+        for (int i = threadIdx.x * 4; i < K; i += 256 * 4)
+            *reinterpret_cast<float4*>(xs_lds + i) = *reinterpret_cast<const float4*>(a.x + i);
         __syncthreads();
         xsrc = xs_lds;
     }
@@ -215,8 +223,20 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
 
 template <int BITS, int ST, bool XNORM>
 static hipError_t qmv_launch(const QmvDev& d, bool ks, int grid, size_t lds, hipStream_t s) {
-    if (ks) hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM, true>), dim3(grid), dim3(256), lds, s, d);
-    else hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM, false>), dim3(grid), dim3(256), lds, s, d);
+    // x staged in LDS where it fits the default 64 KiB (XNORM stages it anyway), not when the waves
+    // split K (each reads a quarter of it), and at 8 bits only over many rounds of workgroups
+    // (measured on the sweep cells: 4096 -> 14336 rows 13.0 -> 10.9 us at 4 bits but 20.2 -> 22.1 at 8
+    // bits; the 151936-row head 120 -> 87 us at 4 bits, 211 -> 171 at 8; the split-K 14336-input cells
+    // 13-19 -> 15-21 us)
+    const bool xc = !XNORM && !ks && (size_t)d.K * sizeof(float) <= 65536 && (BITS < 8 || grid >= 2048);
+    if (xc) lds = (size_t)d.K * sizeof(float);
+    if (ks) {
+        if (xc) hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM, true, true>), dim3(grid), dim3(256), lds, s, d);
+        else hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM, true>), dim3(grid), dim3(256), lds, s, d);
+    } else {
+        if (xc) hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM, false, true>), dim3(grid), dim3(256), lds, s, d);
+        else hipLaunchKernelGGL((qmv_kernel<BITS, ST, XNORM, false>), dim3(grid), dim3(256), lds, s, d);
+    }
     return hipGetLastError();
 }
 
