@@ -21,6 +21,7 @@ namespace mlxr {
 
 constexpr int QMV_WAVES = 4;
 constexpr int QMV_ROWS = 4;   // rows per wave
+constexpr int QMV_KS_ROWS = 8;   // rows of a split-K workgroup (its waves share them, so x is read once per 8 rows)
 
 struct QmvDev {
     const uint8_t* w[3]; const uint16_t* s[3]; const uint16_t* b[3]; const uint16_t* bias[3];
@@ -92,6 +93,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f 
 // four rows, more bytes than its weights). KS: the waves split K over the same rows.
 template <int BITS, int ST, bool XNORM, bool KS, bool XCOPY = false>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
+    constexpr int R = KS ? QMV_KS_ROWS : QMV_ROWS;   // rows per wave (split K: per workgroup)
     extern __shared__ __attribute__((aligned(16))) float xs_lds[];
     __shared__ float red[QMV_WAVES];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -124,20 +126,20 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
         xsrc = xs_lds;
     }
     const bool gated = a.epi == EPI_GATED;
-    const int rows_per_wave = QMV_ROWS;
+    const int rows_per_wave = R;
     const int slot0 = (KS ? blockIdx.x : blockIdx.x * QMV_WAVES + wave) * (gated ? rows_per_wave / 2 : rows_per_wave);
     if (!KS && slot0 >= a.O) return;
     const int64_t rowBytes = (int64_t)K * BITS / 8;
     const int gpr = K / a.gs;
-    const uint8_t* wp[QMV_ROWS]; const uint16_t* sp[QMV_ROWS]; const uint16_t* bp[QMV_ROWS];
-    bool valid[QMV_ROWS];
-    int outIdx[QMV_ROWS];
+    const uint8_t* wp[R]; const uint16_t* sp[R]; const uint16_t* bp[R];
+    bool valid[R];
+    int outIdx[R];
 #pragma unroll
-    for (int r = 0; r < QMV_ROWS; r++) {
+    for (int r = 0; r < R; r++) {
         int part, row;
         if (gated) {
-            const int o = slot0 + (r % (QMV_ROWS / 2));
-            part = r < QMV_ROWS / 2 ? 0 : 1; row = o; valid[r] = o < a.O; outIdx[r] = o;
+            const int o = slot0 + (r % (R / 2));
+            part = r < R / 2 ? 0 : 1; row = o; valid[r] = o < a.O; outIdx[r] = o;
         } else {
             const int gr = slot0 + r;
             valid[r] = gr < a.O; outIdx[r] = gr;
@@ -153,16 +155,16 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
         outIdx[r] = valid[r] ? outIdx[r] : -1;
         (void)part;
     }
-    float acc[QMV_ROWS];
+    float acc[R];
 #pragma unroll
-    for (int r = 0; r < QMV_ROWS; r++) acc[r] = 0.0f;
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
     const int nchunks = K >> 5;
     const int cq0 = KS ? nchunks * wave / QMV_WAVES : 0, cq1 = KS ? nchunks * (wave + 1) / QMV_WAVES : nchunks;
     for (int c = cq0 + lane; c < cq1; c += 64) {
         const int k0 = c << 5;
-        uint32_t w[QMV_ROWS][BITS];
+        uint32_t w[R][BITS];
 #pragma unroll
-        for (int r = 0; r < QMV_ROWS; r++) load_chunk<BITS>(wp[r] + (int64_t)c * (4 * BITS), w[r]);
+        for (int r = 0; r < R; r++) load_chunk<BITS>(wp[r] + (int64_t)c * (4 * BITS), w[r]);
         float x[32];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -174,39 +176,39 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvDev a) {
         for (int j = 0; j < 32; j++) xsum += x[j];
         const int g = k0 / a.gs;
 #pragma unroll
-        for (int r = 0; r < QMV_ROWS; r++) {
+        for (int r = 0; r < R; r++) {
             const float s = ld_scale<ST>(sp[r] + g), b = ld_scale<ST>(bp[r] + g);
             const float d = chunk_dot<BITS>(w[r], x);
             acc[r] += s * d + b * xsum;
         }
     }
 #pragma unroll
-    for (int r = 0; r < QMV_ROWS; r++) acc[r] = wave_sum(acc[r]);
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
     if constexpr (KS) {
-        __shared__ float wred[QMV_WAVES][QMV_ROWS];
+        __shared__ float wred[QMV_WAVES][R];
         if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < QMV_ROWS; r++) wred[wave][r] = acc[r];
+            for (int r = 0; r < R; r++) wred[wave][r] = acc[r];
         }
         __syncthreads();
         if (wave != 0 || slot0 >= a.O) return;
 #pragma unroll
-        for (int r = 0; r < QMV_ROWS; r++) acc[r] = ((wred[0][r] + wred[1][r]) + wred[2][r]) + wred[3][r];
+        for (int r = 0; r < R; r++) acc[r] = ((wred[0][r] + wred[1][r]) + wred[2][r]) + wred[3][r];
     }
     if (lane != 0) return;
     if (gated) {
 #pragma unroll
-        for (int r = 0; r < QMV_ROWS / 2; r++) {
+        for (int r = 0; r < R / 2; r++) {
             const int o = outIdx[r];
             if (o < 0) continue;
-            float g = acc[r], u = acc[r + QMV_ROWS / 2];
+            float g = acc[r], u = acc[r + R / 2];
             if (a.hasBias) { g += ld_scale<ST>(a.bias[0] + o); u += ld_scale<ST>(a.bias[1] + o); }
             a.y[o] = silu_mul(g, u);
         }
         return;
     }
 #pragma unroll
-    for (int r = 0; r < QMV_ROWS; r++) {
+    for (int r = 0; r < R; r++) {
         const int gr = outIdx[r];
         if (gr < 0) continue;
         float v = acc[r];
@@ -258,7 +260,8 @@ hipError_t launch_qmv(const QmvArgs& a, hipStream_t s) {
     // measured on the 14336-input sweep cells: 3 / 4 / 6 bits 19.3 / 18.9 / 21.1 -> 12.9 / 13.5 / 15.6 us;
     // 8-bit rows (twice the bytes per chunk, each wave's loads already busy) 18.6 -> 21.9, so not those
     const bool ks = (a.K >> 5) >= 64 * QMV_WAVES && a.bits < 8;
-    const int per_wg = (ks ? 1 : QMV_WAVES) * (a.epi == EPI_GATED ? QMV_ROWS / 2 : QMV_ROWS);
+    const int rows = ks ? QMV_KS_ROWS : QMV_ROWS;
+    const int per_wg = (ks ? 1 : QMV_WAVES) * (a.epi == EPI_GATED ? rows / 2 : rows);
     const int grid = (a.O + per_wg - 1) / per_wg;
     const bool xn = a.norm_w != nullptr;
     const size_t lds = xn ? (size_t)a.K * sizeof(float) : 0;
