@@ -73,6 +73,8 @@ def small_main(a):
     d = model_dir(a.config, a.seed)
     n_prompt, n_steps = 32, 64
     model = mlxr.Transformer(d, context_length=n_prompt + n_steps + a.step_iters + 16)
+    if a.decode_mode != 1:
+        model.set_decode_mode(a.decode_mode)
     greedy = mlxr.SamplingParameters.greedy()
     prompt = np.random.default_rng(a.seed).integers(0, model.vocab_size, n_prompt).astype(np.int32)
 
