@@ -308,7 +308,7 @@ def test_persistent_abort_fails_both_steps_in_flight(gpu, models):
         assert m.generate(toks, 8, GREEDY) == want
 
 
-@pytest.mark.parametrize("name", ["qwen3", "llama"])
+@pytest.mark.parametrize("name", ["qwen3", "llama", "qwen3_3bit", "qwen3_g128_8bit"])
 def test_verify_batch_matches_incremental_decode(gpu, models, name):
     """verifyBatchMatchesIncrementalDecode (ModelTests.swift:201-230): each row of a T = 2..8 batch
     (all_logits) gives the next-token logits of decoding the tokens one at a time: same argmax, max
