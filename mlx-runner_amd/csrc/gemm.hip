@@ -768,9 +768,9 @@ __global__ __launch_bounds__(256) void qmmx_kernel(QmmXDev a) {
 // group and is folded with that group's scale and bias in fp32 (y += s 2^24 acc + b sum x).
 // A batch is QY_NG groups of a row: its spans' codes, the 16-byte runs of scales and biases and
 // every span's x are loaded before any is used (one memory round trip per batch); the token
-// group sums sit in LDS. At 32 codes per lane the x of a batch reaches LDS by buffer -> LDS copies
-// (1 KB of 4 tokens' chunks per copy, no lane loading what another lane loads) and the A operands
-// are read from there. 16 rows per workgroup, the four waves on a quarter of the batches each,
+// group sums sit in LDS. The x of a batch reaches LDS by buffer -> LDS copies (1 KB of 4 tokens'
+// chunks per copy at 32 codes per lane, of 8 tokens' at 16; no lane loading what another lane
+// loads) and the A operands are read from there. 16 rows per workgroup, the four waves on a quarter of the batches each,
 // partial sums added in wave order.
 template <int BITS, int GS> struct QyShape {
     static constexpr int C = BITS == 8 ? 16 : 32;        // codes per lane per span
@@ -792,12 +792,14 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
     // at slot c ^ t (a B-operand read of 16 tokens' same chunk hits distinct banks)
     extern __shared__ __attribute__((aligned(16))) float qy_gsum[];
     __shared__ f32x4_t red[NW][64];
-    constexpr bool XL = S::C == 32;                            // x through LDS
+    constexpr bool XL = true;                                  // x through LDS
     constexpr int NBUF = PF ? 2 : 1;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, q = lane >> 4, T = a.T;
     const int K = a.K, G = K / GS, NB = G / S::NG;
-    const int TT = (T + 3) & ~3, XWB = S::SPB * TT * 256;
+    // (a span's x per token: CPS chunks of 16 bytes, RB bytes; one copy carries TPI tokens)
+    constexpr int CPS = S::SPAN / 8, TPI = 64 / CPS, RB = S::SPAN * 2;
+    const int TT = (T + 3) & ~3, TTX = (T + TPI - 1) / TPI * TPI, XWB = S::SPB * TTX * RB;
     uint8_t* xlds = reinterpret_cast<uint8_t*>(qy_gsum) + (size_t)(K / GS) * 32;
     for (int i = tid; i < G * 8; i += 64 * NW) {
         const int g = i >> 3, t = i & 7;
@@ -861,10 +863,10 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
         uint8_t* rb = xlds + (size_t)(wave * NBUF + buf) * XWB;
 #pragma unroll
         for (int u = 0; u < S::SPB; u++)
-            for (int tq = 0; tq < TT / 4; tq++) {
-                const int t = 4 * tq + (lane >> 4), c = (lane & 15) ^ t;
+            for (int tq = 0; tq < TTX / TPI; tq++) {
+                const int t = TPI * tq + lane / CPS, c = (lane % CPS) ^ (t & (CPS - 1));
                 const uint32_t off = (uint32_t)(min(t, T - 1) * K + k0 + u * S::SPAN + 8 * c) * 2u;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(rb + (u * TT + 4 * tq) * 256), 16, off, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(rb + (u * TTX + TPI * tq) * RB), 16, off, 0, 0, 0);
             }
     };
     // A rows: NGP = 16 / TT group slots of TT token rows; row l16 is token ta of slot pa. D rows
@@ -874,7 +876,7 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
     const int NGP = PACK ? 16 / TT : 1, pa = PACK ? l16 / TT : 0, ta = PACK ? l16 % TT : l16;
     const int pd = PACK ? (4 * q) / TT : 0, td0 = PACK ? (4 * q) % TT : 4 * q;
     const bool tva = ta < T;
-    const int mr = min(ta, TT - 1);
+    const int mr = min(ta, TTX - 1);
     if constexpr (PF) {
         load_w(b0);
         if constexpr (XL) dma_x(b0, 0);
@@ -895,7 +897,7 @@ __global__ __launch_bounds__(64 * NW) void qmmy_kernel(QmmXDev a) {
             for (int u = 0; u < S::SPB; u++)
 #pragma unroll
                 for (int j = 0; j < S::STEPS; j++) {
-                    const half8_t v = *reinterpret_cast<const half8_t*>(rb + (u * TT + mr) * 256 + ((4 * q + j) ^ mr) * 16);
+                    const half8_t v = *reinterpret_cast<const half8_t*>(rb + (u * TTX + mr) * RB + (((S::C / 8) * q + j) ^ (mr & (CPS - 1))) * 16);
                     xv[u][j] = tva ? v : (half8_t)0;
                 }
         } else {
@@ -1033,9 +1035,9 @@ hipError_t launch_qmmx(const QmmSmallArgs& a, hipStream_t s) {
         // three or more; LDS: group sums, then (32 codes per lane) every wave's x buffers
         const int ng = a.gs == 128 ? 4 : 8, nb = a.K / a.gs / ng;
         bool w8 = nb >= 16, pf = nb / (w8 ? 8 : 4) >= 3;
-        const int C = a.bits == 8 ? 16 : 32, spb = ng * a.gs / (4 * C), tt = (a.T + 3) & ~3;
+        const int C = a.bits == 8 ? 16 : 32, spb = ng * a.gs / (4 * C), tpi = 64 / (C / 2), tt = (a.T + tpi - 1) / tpi * tpi;
         auto lds_of = [&](bool w, bool p) {
-            return (size_t)(a.K / a.gs) * 32 + (C == 32 ? (size_t)(w ? 8 : 4) * (p ? 2 : 1) * spb * tt * 256 : 0);
+            return (size_t)(a.K / a.gs) * 32 + (size_t)(w ? 8 : 4) * (p ? 2 : 1) * spb * tt * (8 * C);
         };
         // (160 KiB of LDS less the 8 KiB of the waves' partial sums)
         constexpr size_t QY_LDS_MAX = 152 * 1024;
